@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the lps token sampler on one MI355X.
+
+A step is one ``lps_sample`` launch over one batch of synthetic logits, the
+BASELINE.json configuration the metric is quoted on (c2: B=64, V=151936 bf16,
+heterogeneous per-row parameters, presence/frequency penalties over 512-id
+histories).  Inputs are resident in HBM before timing; launches rotate over
+>= 2 x 256 MB of distinct logits buffers so the MALL cannot serve the reads,
+and are replayed from a HIP graph so host overhead does not gap the GPU.
+
+Prints ONE JSON line (rank 0, N=1) with the roofline of the sampling kernel
+(algorithmic bytes per launch / average launch time, against 8 TB/s) and the
+CPU baseline (the oracle's op-for-op torch-CPU restatement of the reference
+sampler, row by row, timed on this host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "llm-pipeline_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0
+MALL_BYTES = 256 << 20
+METRIC = "sampled rows/sec at B=64,V=151936 bf16; achieved HBM GB/s vs peak"
+
+
+def alg_bytes(w, n_out_extra=0) -> int:
+    """Algorithmic bytes of one call: logits once, histories, per-row params
+    (6 x 4 B), uniforms, token outputs, plus any logprob outputs."""
+    B, V = w.B, w.V
+    b = B * V * w.logits.element_size()
+    if w.histories is not None:
+        b += int(w.hist_len.sum()) * 4
+    b += B * 24 + B * 4 + B * 8 + n_out_extra
+    return b
+
+
+def build_args(w, dev, logits_dev, out, lib_mod):
+    from lps import _lib
+    import torch
+    a = _lib.SampleArgs()
+    a.logits = logits_dev.data_ptr()
+    a.dtype = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[logits_dev.dtype]
+    a.num_rows = w.B
+    a.vocab = w.V
+    a.rows_inner = 1
+    a.stride_outer = logits_dev.stride(0)
+    for name, t in out["params"].items():
+        setattr(a, name, t.data_ptr())
+    if out.get("hist") is not None:
+        a.history = out["hist"].data_ptr()
+        a.history_stride = out["hist"].stride(0)
+        a.history_len = out["hl"].data_ptr()
+    a.uniforms = out["u"].data_ptr()
+    a.tokens = out["tokens"].data_ptr()
+    a.row_status = out["status"].data_ptr()
+    if w.logprobs:
+        a.chosen_logprob = out["lp"].data_ptr()
+    if w.n_top:
+        a.top_logprobs = out["tl"].data_ptr()
+        a.top_ids = out["ti"].data_ptr()
+        a.n_top = w.n_top
+    return a
+
+
+def cpu_baseline(w, max_rows=None, repeats=3):
+    """Reference-as-written sampler (oracle restatement), one call per row with
+    that row's parameters and history (continuous_batching.py:394-401)."""
+    import torch
+    from oracle import reference_semantics as O
+    from tests import parity as PY
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = max(1, min(share, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    rows = list(range(w.B if max_rows is None else min(w.B, max_rows)))
+    x32 = w.logits.float()
+    g = torch.Generator().manual_seed(0)
+
+    def one_pass():
+        for i in rows:
+            O.reference_sample_token(x32[i:i + 1], PY.row_params(w, i), w.row_history(i), generator=g)
+
+    one_pass()
+    ts = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        one_pass()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": round(len(rows) / t, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{len(rows)} rows of the {w.name} batch x {repeats} repeats (median), fp32-upcast logits, "
+                      f"torch-CPU restatement of sampling.py:51-85 with torch.multinomial"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c3", "c3f", "c5"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sampler shards rows across "
+              f"GPUs with no exchange, which this single-GPU build does not launch.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from lps import _lib
+    from tests import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(),
+            "c3": lambda: W.c3(), "c3f": lambda: W.c3(flat=True), "c5": lambda: W.c5()}[args.config]
+    w = make()
+    lib = _lib.load()
+
+    # device inputs; rotate distinct logits buffers over >= 2 x MALL
+    x = w.logits.to(dev)
+    nbuf = max(2, math.ceil(2 * MALL_BYTES / (x.numel() * x.element_size())))
+    bufs = [x] + [x.clone() for _ in range(nbuf - 1)]
+    B = w.B
+    io = {
+        "params": {
+            "temperature": w.temperature.to(dev), "top_k": w.top_k.to(dev), "top_p": w.top_p.to(dev),
+            "min_p": w.min_p.to(dev), "typical_p": w.typical_p.to(dev), "repetition_penalty": w.rep.to(dev),
+            "presence_penalty": w.pres.to(dev), "frequency_penalty": w.freq.to(dev),
+        },
+        "hist": w.histories.to(dev) if w.histories is not None else None,
+        "hl": w.hist_len.to(dev) if w.hist_len is not None else None,
+        "u": w.uniforms.to(dev),
+        "tokens": torch.empty(B, dtype=torch.int64, device=dev),
+        "status": torch.empty(B, dtype=torch.int32, device=dev),
+        "lp": torch.empty(B, dtype=torch.float32, device=dev),
+        "tl": torch.empty((B, max(w.n_top, 1)), dtype=torch.float32, device=dev),
+        "ti": torch.empty((B, max(w.n_top, 1)), dtype=torch.int64, device=dev),
+    }
+    arglist = [build_args(w, dev, b, io, lib) for b in bufs]
+    extra = (B * 4 + B * w.n_top * 12) if w.logprobs else 0
+    abytes = alg_bytes(w, extra)
+
+    def launch(i):
+        rc = lib.lps_sample(ctypes.byref(arglist[i % nbuf]), torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lps_sample failed: {rc}")
+
+    # correctness self-check of the timed configuration (first rows vs oracle)
+    launch(0)
+    torch.cuda.synchronize()
+    assert int(io["status"].ne(0).sum()) == 0, "row status errors"
+
+    K, Wm = args.steps, args.warmup
+    use_graph = not args.no_graph
+    if use_graph:
+        per_graph = nbuf * max(1, 64 // nbuf)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):
+                launch(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(per_graph):
+                launch(i)
+        reps_w = max(1, math.ceil(Wm / per_graph))
+        reps = max(1, math.ceil(K / per_graph))
+        for _ in range(reps_w):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        steps = reps * per_graph
+    else:
+        for i in range(Wm):
+            launch(i)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(K):
+            launch(i)
+        e1.record()
+        torch.cuda.synchronize()
+        steps = K
+    ms = e0.elapsed_time(e1)
+    ms_step = ms / steps
+    rows_s = B / (ms_step / 1e3)
+    gbs = abytes / (ms_step / 1e3) / 1e9
+    assert int(io["status"].ne(0).sum()) == 0
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, max_rows=64 if B > 64 else None)
+
+    cfg = {"workload": {"c1": "c1: B=1, V=151936 fp32, rep 1.1 over 64 ids, T 0.7, top_k 50, top_p 0.9",
+                        "c1g": "c1 greedy: B=1, V=151936 fp32, rep 1.1, T=0",
+                        "c2": "c2: B=64, V=151936 bf16 N(0,3^2)+3 spikes, T~U[0.3,1.2], top_k in {0,20,50,100}, "
+                              "top_p~U[0.8,1], presence 0.5, frequency 0.3 over 512 Zipf(1.1) ids/row",
+                        "c3": "c3: B=256, V=151936 fp32 Student-t(3)*2, top_p 0.95, T 1",
+                        "c3f": "c3 flat: B=256, V=151936 fp32 N(0,0.1^2), top_p 0.95, T 1",
+                        "c5": "c5: B=512, V=151936 fp16, half greedy, half T 0.9/k 40/p 0.92, rep 1.05 over "
+                              "1024 ids/row, chosen + top-20 logprobs"}[args.config],
+           "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
+           "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes}
+    line = {
+        "metric": METRIC if args.config == "c2" else f"sampled rows/sec ({args.config})",
+        "value": round(rows_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": Wm,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": cfg,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

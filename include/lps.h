@@ -1,0 +1,202 @@
+/*
+ * lps.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Plain C: pointers, sizes and enums only, no torch or HIP types.  The stream
+ * argument is a hipStream_t passed as void* (NULL = the null stream).  Every
+ * pointer in an args struct is a device pointer unless stated otherwise.  All
+ * entry points are stream-ordered, never synchronise, keep no global mutable
+ * state and are safe to call from several host threads at once.
+ *
+ * The entry points replace the logits->token path of DavidAkinpelu/llm-pipeline:
+ *
+ *   lps_sample         Sampler.sample_token
+ *                        src/llm_pipeline/inference/sampling.py:51-85
+ *                      with its filters (:108-238), per-row parameters as the
+ *                      continuous batcher applies them row by row
+ *                        src/llm_pipeline/inference/continuous_batching.py:394-401
+ *                      and the entropy used by sample_mirostat_v2 (:240-279).
+ *   lps_spec_verify    the accept / reject / resample block of speculative_decode
+ *                        src/llm_pipeline/inference/speculative.py:119-174
+ *                      (and the MTP variant :264-276), batched over requests.
+ *   lps_verify_drafts  verify_drafts_batched
+ *                        src/llm_pipeline/inference/speculative_kernel.py:24-58
+ *                      and its torch fallback :84-87.
+ */
+#ifndef LPS_H
+#define LPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LPS_ABI_VERSION 1
+
+/* Return codes.  The reference raises TypeError / ValueError / RuntimeError
+ * (sampling.py:106, speculative.py:90-91, torch.multinomial); the Python
+ * host maps these codes back onto the same exception types. */
+enum {
+  LPS_OK = 0,
+  LPS_EINVAL = 1,              /* bad shape, stride, pointer or parameter     */
+  LPS_EUNSUPPORTED_DTYPE = 2,  /* logits dtype not one of lps_dtype            */
+  LPS_ELAUNCH = 3,             /* the HIP launch failed                         */
+  LPS_EWORKSPACE = 4           /* workspace missing or smaller than required   */
+};
+
+/* Logits element types. */
+enum { LPS_DTYPE_F32 = 0, LPS_DTYPE_BF16 = 1, LPS_DTYPE_F16 = 2 };
+
+/* Per-row status bits written to row_status[] by the kernels.  A set bit on a
+ * sampling row corresponds to the RuntimeError torch.multinomial raises for an
+ * invalid distribution (NaN / +inf / all -inf after temperature). */
+enum {
+  LPS_ROW_OK = 0,
+  LPS_ROW_NONFINITE = 1,       /* NaN or +inf in the scaled logits of a sampling row */
+  LPS_ROW_EMPTY = 2,           /* every logit is -inf on a sampling row               */
+  LPS_ROW_HISTORY_OVERFLOW = 4 /* more distinct history ids than the kernel holds     */
+};
+
+/* Largest top-N logprob count and largest distinct-history size per row. */
+#define LPS_MAX_TOP_LOGPROBS 64
+#define LPS_MAX_HISTORY_DISTINCT 1536
+
+/* Residual used by lps_spec_verify on the first rejected position. */
+enum {
+  LPS_RESIDUAL_TARGET = 0,     /* reference: resample the target distribution (speculative.py:150-157) */
+  LPS_RESIDUAL_LEVIATHAN = 1   /* textbook: norm(max(p - q, 0))                                         */
+};
+
+/*
+ * Logits addressing: row r of R rows starts at element
+ *     (r / rows_inner) * stride_outer + (r % rows_inner) * stride_inner
+ * of `logits`; elements of a row are contiguous.  A plain [B, V] tensor has
+ * rows_inner = 1, stride_outer = row stride.  The engine's strided view
+ * logits[:, -1, :] (qwen3_engine.py:528) is the same with stride_outer = T*V.
+ */
+typedef struct lps_sample_args {
+  /* input logits (read only, never modified) */
+  const void* logits;
+  int32_t dtype;                  /* lps_dtype */
+  int32_t num_rows;               /* R */
+  int32_t vocab;                  /* V */
+  int32_t rows_inner;             /* >= 1 */
+  int64_t stride_outer;           /* elements */
+  int64_t stride_inner;           /* elements */
+
+  /* per-row parameters, float32/int32 [R]; NULL = the neutral value
+   * (temperature 1, top_k 0, top_p 1, min_p 0, typical_p 1,
+   *  repetition 1, presence 0, frequency 0).  temperature <= 0 = greedy. */
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* min_p;
+  const float* typical_p;
+  const float* repetition_penalty;
+  const float* presence_penalty;
+  const float* frequency_penalty;
+
+  /* per-row token histories: int32 [R, history_stride], row r holds
+   * history_len[r] ids; ids outside [0, V) are ignored (sampling.py:126).
+   * history == NULL: no penalties. */
+  const int32_t* history;
+  int64_t history_stride;
+  const int32_t* history_len;
+
+  /* uniforms in [0, 1), float32 [R]: the inverse-CDF draw of sampling rows.
+   * Required when any row samples (temperature > 0). */
+  const float* uniforms;
+
+  /* optional query tokens: query_prob[r] = probability of the query token
+   * under row r's kept distribution.  Row r's query is
+   * query_tokens[(r / rows_inner) * query_inner + (r % rows_inner)] when
+   * r % rows_inner < query_inner, else none (query_prob[r] = 0). */
+  const int64_t* query_tokens;
+  int32_t query_inner;
+  float* query_prob;              /* float32 [R] or NULL */
+
+  /* outputs */
+  int64_t* tokens;                /* int64 [R], required (-1 on a failed row) */
+  float* chosen_logprob;          /* float32 [R] or NULL */
+  float* top_logprobs;            /* float32 [R, n_top] or NULL */
+  int64_t* top_ids;               /* int64 [R, n_top] or NULL */
+  int32_t n_top;                  /* 0 .. LPS_MAX_TOP_LOGPROBS */
+  float* entropy;                 /* float32 [R] or NULL: H of softmax(scaled logits), nats */
+  int32_t* row_status;            /* int32 [R] or NULL: LPS_ROW_* bits */
+  int32_t skip_draw;              /* 1: compute query_prob / logprobs only, tokens[r] = -1 for sampling rows */
+
+  /* optional kept-set descriptor of each row after every filter: the kept set
+   * is {z > kept_cut} plus the first kept_ties ids (vocabulary order) with
+   * z == kept_cut, where z is the penalised, temperature-scaled logit. */
+  float* kept_cut;                /* float32 [R] or NULL */
+  int32_t* kept_ties;             /* int32 [R] or NULL (-1 = every id at the cut) */
+  int32_t* kept_count;            /* int32 [R] or NULL */
+
+  /* caller-owned scratch, lps_workspace_bytes() bytes (may be NULL when 0) */
+  void* workspace;
+  size_t workspace_bytes;
+} lps_sample_args;
+
+typedef struct lps_spec_args {
+  /* target logits [B, k+1, V], draft logits [B, k, V]; rows contiguous,
+   * strides in elements */
+  const void* target_logits;
+  int64_t target_stride_b, target_stride_k;
+  const void* draft_logits;
+  int64_t draft_stride_b, draft_stride_k;
+  int32_t dtype;                  /* lps_dtype, shared by target and draft */
+  int32_t batch;                  /* B */
+  int32_t k;                      /* draft length, >= 1 */
+  int32_t vocab;                  /* V */
+  float temperature;              /* shared; <= 0 = greedy */
+  float top_p;                    /* shared; >= 1 = off */
+  int32_t residual;               /* LPS_RESIDUAL_* */
+  const int64_t* draft_tokens;    /* int64 [B, k] */
+  const float* u_accept;          /* float32 [B, k] */
+  const float* u_resample;        /* float32 [B, k+1] */
+  /* outputs */
+  int32_t* n_accepted;            /* int32 [B] */
+  int64_t* tokens;                /* int64 [B, k+1]: accepted drafts, then the
+                                     replacement / bonus token, then -1 */
+  int8_t* accept;                 /* int8 [B, k] or NULL: per-position accept bit */
+  float* p_target;                /* float32 [B, k] or NULL */
+  float* q_draft;                 /* float32 [B, k] or NULL */
+  int32_t* row_status;            /* int32 [B*(2k+1)] or NULL */
+  void* workspace;
+  size_t workspace_bytes;
+} lps_spec_args;
+
+/* ABI version (LPS_ABI_VERSION). */
+int lps_version(void);
+
+/* Human-readable name of a return code. */
+const char* lps_status_string(int code);
+
+/* Scratch bytes lps_sample needs for num_rows rows of vocab V. */
+size_t lps_workspace_bytes(int num_rows, int vocab, int flags);
+
+/* Scratch bytes lps_spec_verify needs. */
+size_t lps_spec_workspace_bytes(int batch, int k, int vocab);
+
+/* Sampler.sample_token (sampling.py:51-85), batched with per-row parameters. */
+int lps_sample(const lps_sample_args* args, void* stream);
+
+/* speculative.py:119-174, batched: accept / reject, then the replacement or
+ * bonus token. */
+int lps_spec_verify(const lps_spec_args* args, void* stream);
+
+/* verify_drafts_batched (speculative_kernel.py:24-58):
+ *   accept[i] = rand_uniform[i] < min(target_probs[i, draft_tokens[i]] / max(draft_probs[i], 1e-9), 1)
+ * target_probs is [K, V] of `dtype` with element strides (stride_k, stride_v);
+ * draft_probs and rand_uniform are float32 [K]; draft_tokens int64 [K];
+ * accept int8 [K]. */
+int lps_verify_drafts(const void* target_probs, int32_t dtype, int64_t K, int64_t V, int64_t stride_k,
+                      int64_t stride_v, const float* draft_probs, const int64_t* draft_tokens,
+                      const float* rand_uniform, int8_t* accept, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LPS_H */

@@ -1,0 +1,255 @@
+// C ABI of the lps token sampler (declarations and reference citations are in
+// include/lps.h).  Launches only; no allocation, no synchronisation, no global
+// mutable state.
+#include <hip/hip_runtime.h>
+
+#include "lps_generic.h"
+#include "lps_spec.h"
+
+using namespace lps;
+
+namespace {
+
+constexpr int kMaxVocab = (1 << 19) - 1;  // fixed-point masses: V * 2^44 < 2^63
+
+template <int DT, int VEC>
+hipError_t launch_gen(const KParams& P, hipStream_t s) {
+  hipLaunchKernelGGL((gen_row_kernel<DT, VEC>), dim3(P.R), dim3(GEN_NT), 0, s, P);
+  return hipGetLastError();
+}
+
+hipError_t dispatch_gen(int dtype, bool vec, const KParams& P, hipStream_t s) {
+  switch (dtype) {
+    case LPS_DTYPE_F32: return vec ? launch_gen<LPS_DTYPE_F32, 4>(P, s) : launch_gen<LPS_DTYPE_F32, 1>(P, s);
+    case LPS_DTYPE_BF16: return vec ? launch_gen<LPS_DTYPE_BF16, 8>(P, s) : launch_gen<LPS_DTYPE_BF16, 1>(P, s);
+    default: return vec ? launch_gen<LPS_DTYPE_F16, 8>(P, s) : launch_gen<LPS_DTYPE_F16, 1>(P, s);
+  }
+}
+
+// 16-byte vector loads are legal when every row start is 16-byte aligned and V
+// is a whole number of vectors.
+bool vec_ok(const void* base, int dtype, int V, int rows_inner, int64_t so, int64_t si) {
+  const int vec = dtype == LPS_DTYPE_F32 ? 4 : 8;
+  if (reinterpret_cast<uintptr_t>(base) % 16) return false;
+  if (V % vec) return false;
+  if (so % vec) return false;
+  if (rows_inner > 1 && si % vec) return false;
+  return true;
+}
+
+bool dtype_ok(int d) { return d == LPS_DTYPE_F32 || d == LPS_DTYPE_BF16 || d == LPS_DTYPE_F16; }
+
+KParams neutral_params() {
+  KParams P{};
+  P.rows_inner = 1;
+  P.temperature_def = 1.0f;
+  P.top_k_def = 0;
+  P.top_p_def = 1.0f;
+  P.min_p_def = 0.0f;
+  P.typical_p_def = 1.0f;
+  P.rep_def = 1.0f;
+  P.pres_def = 0.0f;
+  P.freq_def = 0.0f;
+  return P;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct SpecWs {
+  int64_t* draws_t;   // [B*(k+1)]
+  int64_t* draws_d;   // [B*k]
+  float* p_t;         // [B*(k+1)]
+  float* q_d;         // [B*k]
+  int32_t* first_rej; // [B]
+  RowPlan* plans;     // [B*(k+1) + B*k]
+  size_t bytes;
+};
+
+SpecWs spec_layout(void* base, int B, int k) {
+  SpecWs w{};
+  const size_t Rt = (size_t)B * (k + 1), Rd = (size_t)B * k;
+  size_t off = 0;
+  char* p = reinterpret_cast<char*>(base);
+  w.draws_t = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rt * 8);
+  w.draws_d = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rd * 8);
+  w.p_t = reinterpret_cast<float*>(p + off); off = align256(off + Rt * 4);
+  w.q_d = reinterpret_cast<float*>(p + off); off = align256(off + Rd * 4);
+  w.first_rej = reinterpret_cast<int32_t*>(p + off); off = align256(off + (size_t)B * 4);
+  w.plans = reinterpret_cast<RowPlan*>(p + off); off = align256(off + (Rt + Rd) * sizeof(RowPlan));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lps_version(void) { return LPS_ABI_VERSION; }
+
+const char* lps_status_string(int code) {
+  switch (code) {
+    case LPS_OK: return "ok";
+    case LPS_EINVAL: return "invalid argument";
+    case LPS_EUNSUPPORTED_DTYPE: return "unsupported logits dtype";
+    case LPS_ELAUNCH: return "kernel launch failed";
+    case LPS_EWORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+size_t lps_workspace_bytes(int num_rows, int vocab, int flags) {
+  (void)num_rows; (void)vocab; (void)flags;
+  return 0;
+}
+
+size_t lps_spec_workspace_bytes(int batch, int k, int vocab) {
+  (void)vocab;
+  if (batch <= 0 || k <= 0) return 0;
+  return spec_layout(nullptr, batch, k).bytes;
+}
+
+int lps_sample(const lps_sample_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  if (!dtype_ok(a->dtype)) return LPS_EUNSUPPORTED_DTYPE;
+  if (a->num_rows < 0 || a->vocab < 1 || a->vocab > kMaxVocab || a->rows_inner < 1) return LPS_EINVAL;
+  if (a->num_rows == 0) return LPS_OK;
+  if (!a->logits || !a->tokens) return LPS_EINVAL;
+  if (a->stride_outer < 0 || a->stride_inner < 0) return LPS_EINVAL;
+  if (a->n_top < 0 || a->n_top > LPS_MAX_TOP_LOGPROBS || (a->n_top > 0 && !a->top_logprobs)) return LPS_EINVAL;
+  if (!a->uniforms && !a->skip_draw) return LPS_EINVAL;
+  if (a->history && (!a->history_len || a->history_stride < 0)) return LPS_EINVAL;
+  if (a->query_tokens && (a->query_inner < 0 || a->query_inner > a->rows_inner)) return LPS_EINVAL;
+  KParams P = neutral_params();
+  P.logits = a->logits;
+  P.V = a->vocab;
+  P.R = a->num_rows;
+  P.rows_inner = a->rows_inner;
+  P.stride_outer = a->stride_outer;
+  P.stride_inner = a->stride_inner;
+  P.temperature = a->temperature;
+  P.top_k = a->top_k;
+  P.top_p = a->top_p;
+  P.min_p = a->min_p;
+  P.typical_p = a->typical_p;
+  P.rep = a->repetition_penalty;
+  P.pres = a->presence_penalty;
+  P.freq = a->frequency_penalty;
+  P.history = a->history;
+  P.history_stride = a->history_stride;
+  P.history_len = a->history_len;
+  P.uniforms = a->uniforms;
+  P.query_tokens = a->query_tokens;
+  P.query_inner = a->query_tokens ? a->query_inner : 0;
+  P.query_prob = a->query_prob;
+  P.tokens = a->tokens;
+  P.chosen_logprob = a->chosen_logprob;
+  P.top_logprobs = a->top_logprobs;
+  P.top_ids = a->top_ids;
+  P.n_top = a->n_top;
+  P.entropy = a->entropy;
+  P.row_status = a->row_status;
+  P.skip_draw = a->skip_draw;
+  P.kept_cut = a->kept_cut;
+  P.kept_ties = a->kept_ties;
+  P.kept_count = a->kept_count;
+  P.plans = nullptr;
+  const bool vec = vec_ok(a->logits, a->dtype, a->vocab, a->rows_inner, a->stride_outer, a->stride_inner);
+  hipError_t e = dispatch_gen(a->dtype, vec, P, reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
+
+int lps_spec_verify(const lps_spec_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  if (!dtype_ok(a->dtype)) return LPS_EUNSUPPORTED_DTYPE;
+  if (a->batch < 0 || a->k < 1 || a->vocab < 1 || a->vocab > kMaxVocab) return LPS_EINVAL;
+  if (a->batch == 0) return LPS_OK;
+  if (!a->target_logits || !a->draft_logits || !a->draft_tokens || !a->u_accept || !a->u_resample ||
+      !a->n_accepted || !a->tokens)
+    return LPS_EINVAL;
+  if (a->residual != LPS_RESIDUAL_TARGET && a->residual != LPS_RESIDUAL_LEVIATHAN) return LPS_EINVAL;
+  const int B = a->batch, k = a->k, V = a->vocab;
+  const SpecWs need = spec_layout(nullptr, B, k);
+  if (!a->workspace || a->workspace_bytes < need.bytes) return LPS_EWORKSPACE;
+  const SpecWs w = spec_layout(a->workspace, B, k);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool lev = a->residual == LPS_RESIDUAL_LEVIATHAN && a->temperature > 0.0f;
+
+  // target rows: probability of each draft token, and a draw per position
+  KParams P = neutral_params();
+  P.logits = a->target_logits;
+  P.V = V;
+  P.R = B * (k + 1);
+  P.rows_inner = k + 1;
+  P.stride_outer = a->target_stride_b;
+  P.stride_inner = a->target_stride_k;
+  P.temperature_def = a->temperature;
+  P.top_p_def = a->top_p;
+  P.uniforms = a->u_resample;
+  P.query_tokens = a->draft_tokens;
+  P.query_inner = k;
+  P.query_prob = w.p_t;
+  P.tokens = w.draws_t;
+  P.row_status = a->row_status;
+  P.plans = w.plans;
+  bool vec = vec_ok(a->target_logits, a->dtype, V, k + 1, a->target_stride_b, a->target_stride_k);
+  if (dispatch_gen(a->dtype, vec, P, s) != hipSuccess) return LPS_ELAUNCH;
+
+  // draft rows: probability of each draft token only
+  KParams D = P;
+  D.logits = a->draft_logits;
+  D.R = B * k;
+  D.rows_inner = k;
+  D.stride_outer = a->draft_stride_b;
+  D.stride_inner = a->draft_stride_k;
+  D.uniforms = nullptr;
+  D.query_inner = k;
+  D.query_prob = w.q_d;
+  D.tokens = w.draws_d;
+  D.row_status = a->row_status ? a->row_status + (size_t)B * (k + 1) : nullptr;
+  D.skip_draw = 1;
+  D.plans = w.plans + (size_t)B * (k + 1);
+  vec = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
+  if (dispatch_gen(a->dtype, vec, D, s) != hipSuccess) return LPS_ELAUNCH;
+
+  hipLaunchKernelGGL(spec_epilogue_kernel, dim3((B + 255) / 256), dim3(256), 0, s, B, k, a->temperature, w.p_t,
+                     w.q_d, w.draws_t, a->draft_tokens, a->u_accept, a->n_accepted, a->tokens, a->accept,
+                     a->p_target, a->q_draft, lev ? 1 : 0, w.first_rej);
+  if (hipGetLastError() != hipSuccess) return LPS_ELAUNCH;
+  if (lev) {
+    const bool vt = vec_ok(a->target_logits, a->dtype, V, k + 1, a->target_stride_b, a->target_stride_k) &&
+                    vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
+    if (launch_residual(a->dtype, vt, a->target_logits, a->target_stride_b, a->target_stride_k, a->draft_logits,
+                        a->draft_stride_b, a->draft_stride_k, B, k, V, w.plans, w.first_rej, a->u_resample,
+                        a->tokens, s) != hipSuccess)
+      return LPS_ELAUNCH;
+  }
+  return LPS_OK;
+}
+
+int lps_verify_drafts(const void* target_probs, int32_t dtype, int64_t K, int64_t V, int64_t stride_k,
+                      int64_t stride_v, const float* draft_probs, const int64_t* draft_tokens,
+                      const float* rand_uniform, int8_t* accept, void* stream) {
+  if (!dtype_ok(dtype)) return LPS_EUNSUPPORTED_DTYPE;
+  if (K < 0 || V < 1) return LPS_EINVAL;
+  if (K == 0) return LPS_OK;
+  if (!target_probs || !draft_probs || !draft_tokens || !rand_uniform || !accept) return LPS_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((K + 255) / 256));
+  switch (dtype) {
+    case LPS_DTYPE_F32:
+      hipLaunchKernelGGL((verify_drafts_kernel<LPS_DTYPE_F32>), grid, dim3(256), 0, s, target_probs, K, V, stride_k,
+                         stride_v, draft_probs, draft_tokens, rand_uniform, accept);
+      break;
+    case LPS_DTYPE_BF16:
+      hipLaunchKernelGGL((verify_drafts_kernel<LPS_DTYPE_BF16>), grid, dim3(256), 0, s, target_probs, K, V, stride_k,
+                         stride_v, draft_probs, draft_tokens, rand_uniform, accept);
+      break;
+    default:
+      hipLaunchKernelGGL((verify_drafts_kernel<LPS_DTYPE_F16>), grid, dim3(256), 0, s, target_probs, K, V, stride_k,
+                         stride_v, draft_probs, draft_tokens, rand_uniform, accept);
+      break;
+  }
+  return hipGetLastError() == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,711 @@
+// General row sampler: one 1024-thread workgroup per row.
+//
+// Exact for every parameter combination the ABI accepts.  The row is streamed
+// from memory once per pass (the first pass from HBM, later ones mostly from
+// L2 / MALL); selections are sort-free MSB-first radix selects over
+// order-preserving keys of the temperature-scaled logits with LDS histograms
+// (11 + 11 + 10 bits), masses are fixed-point so every decision is
+// deterministic and independent of accumulation order.
+//
+// Semantics follow Sampler.sample_token (src/llm_pipeline/inference/
+// sampling.py:51-85): penalties (:108-137 plus presence/frequency), greedy
+// argmax for T <= 0 (:72-75), x / T, top-k with all ties at the k-th value kept
+// (:139-156), top-p "keep sorted position j iff j == 0 or cum[j-1] <= p" with
+// ties ordered lower index first (:158-185), min-p (:187-205), typical-p
+// (:207-238, including its NaN fallback to the argmax when the row holds
+// -inf), then an inverse-CDF draw in vocabulary order from the caller's
+// uniform.
+#pragma once
+
+#include "lps_common.h"
+
+namespace lps {
+
+constexpr int GEN_NT = 1024;
+constexpr int GEN_NW = GEN_NT / 64;
+constexpr int HASH_CAP = 2048;     // history hash slots (power of two)
+constexpr int BLOOM_WORDS = 2048;  // 65536-bit bloom filter over token ids
+constexpr int NBINS = 2048;        // radix digit bins (11 bits)
+constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // f2key(-inf)
+
+struct RowPlan {
+  float zmax;        // max scaled logit
+  float T;           // effective temperature (1 for greedy)
+  uint32_t key_lo;   // kept: key > key_lo, or key == key_lo and tie rank < n_tie
+  uint32_t n_tie;    // kNoTie = all ties at key_lo kept
+  uint64_t Zf;       // fixed-point mass of the kept set
+  int32_t greedy;
+  int32_t argmax;
+};
+
+struct KParams {
+  const void* logits;
+  int V, R, rows_inner;
+  int64_t stride_outer, stride_inner;
+  const float* temperature; float temperature_def;
+  const int32_t* top_k; int top_k_def;
+  const float* top_p; float top_p_def;
+  const float* min_p; float min_p_def;
+  const float* typical_p; float typical_p_def;
+  const float* rep; float rep_def;
+  const float* pres; float pres_def;
+  const float* freq; float freq_def;
+  const int32_t* history; int64_t history_stride; const int32_t* history_len;
+  const float* uniforms;
+  const int64_t* query_tokens; int query_inner; float* query_prob;
+  int64_t* tokens;
+  float* chosen_logprob;
+  float* top_logprobs; int64_t* top_ids; int n_top;
+  float* entropy;
+  int32_t* row_status;
+  int skip_draw;
+  float* kept_cut;
+  int32_t* kept_ties;
+  int32_t* kept_count;
+  RowPlan* plans;
+};
+
+struct GenShared {
+  uint32_t bloom[BLOOM_WORDS];
+  int32_t hkey[HASH_CAP];
+  int32_t hcnt[HASH_CAP];
+  union {
+    struct {
+      uint32_t cnt[NBINS];
+      uint64_t mass[NBINS];
+    } h;
+    struct {
+      uint32_t key[LPS_MAX_TOP_LOGPROBS];
+      int32_t idx[LPS_MAX_TOP_LOGPROBS];
+      int32_t n;
+    } lst;
+  } u;
+  uint64_t red64[GEN_NW];
+  double redd[GEN_NW];
+  uint32_t red32[GEN_NW];
+  int32_t misc[8];
+  uint64_t misc64[4];
+};
+
+__device__ __forceinline__ uint32_t hash_id(int id) { return ((uint32_t)id * 2654435761u) >> (32 - 11); }
+
+struct PenCtx {
+  bool active;
+  float rep, pres, freq;
+  const uint32_t* bloom;
+  const int32_t* hkey;
+  const int32_t* hcnt;
+
+  __device__ __forceinline__ int lookup(int id) const {
+    uint32_t s = hash_id(id);
+    for (int p = 0; p < HASH_CAP; p++) {
+      int k = hkey[s];
+      if (k == id) return hcnt[s];
+      if (k < 0) return 0;
+      s = (s + 1) & (HASH_CAP - 1);
+    }
+    return 0;
+  }
+  template <int VEC>
+  __device__ __forceinline__ void apply(int64_t i0, float (&x)[VEC]) const {
+    if (!active) return;
+    uint32_t w = bloom[(i0 >> 5) & (BLOOM_WORDS - 1)] >> (i0 & 31);
+    if (VEC < 32) w &= (1u << VEC) - 1u;
+    if (!w) return;
+#pragma unroll
+    for (int j = 0; j < VEC; j++) {
+      if ((w >> j) & 1u) {
+        int c = lookup((int)(i0 + j));
+        if (c) x[j] = penalize(x[j], c, rep, pres, freq);
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Block helpers (GEN_NT threads).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t gblock_max_u64(uint64_t v, GenShared& S) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t r = S.red64[0];
+#pragma unroll
+  for (int i = 1; i < GEN_NW; i++) r = S.red64[i] > r ? S.red64[i] : r;
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ uint64_t gblock_sum_u64(uint64_t v, GenShared& S) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < GEN_NW; i++) r += S.red64[i];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ uint32_t gblock_min_u32(uint32_t v, GenShared& S) {
+  v = wave_min(v);
+  if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = S.red32[0];
+#pragma unroll
+  for (int i = 1; i < GEN_NW; i++) r = S.red32[i] < r ? S.red32[i] : r;
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ uint32_t gblock_sum_u32(uint32_t v, GenShared& S) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < GEN_NW; i++) r += S.red32[i];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ double gblock_sum_f64(double v, GenShared& S) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) S.redd[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0;
+#pragma unroll
+  for (int i = 0; i < GEN_NW; i++) r += S.redd[i];
+  __syncthreads();
+  return r;
+}
+// Exclusive scan over the block in thread order; *total = block sum.
+template <typename T>
+__device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch) {
+  T inc = wave_incl_scan(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 63) scratch[w] = inc;
+  __syncthreads();
+  T off = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < GEN_NW; i++) {
+    T s = scratch[i];
+    off += (i < w) ? s : (T)0;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+// ---------------------------------------------------------------------------
+// Row passes.
+// ---------------------------------------------------------------------------
+template <int DT, int VEC, typename F>
+__device__ __forceinline__ void row_pass(const void* row, int V, const PenCtx& pc, F&& f) {
+  for (int64_t i0 = (int64_t)threadIdx.x * VEC; i0 < V; i0 += (int64_t)GEN_NT * VEC) {
+    float x[VEC];
+    loadv<DT, VEC>(row, i0, x);
+    pc.apply<VEC>(i0, x);
+#pragma unroll
+    for (int j = 0; j < VEC; j++) f((int)(i0 + j), x[j]);
+  }
+}
+
+// Digit layout of the 32-bit key: 11 + 11 + 10 bits.
+__device__ __forceinline__ int lvl_shift(int l) { return l == 0 ? 21 : (l == 1 ? 10 : 0); }
+__device__ __forceinline__ int lvl_bins(int l) { return l == 2 ? 1024 : 2048; }
+__device__ __forceinline__ uint32_t lvl_himask(int l) { return l == 0 ? 0u : (l == 1 ? 0xFFE00000u : 0xFFFFFC00u); }
+
+// Scan the current histogram from the top bin down.  For counts: the bin b
+// where (count above b) < target <= (count above b) + cnt[b].  For masses:
+// the bin where base + (mass above b) <= limit < base + (mass above b) + mass[b].
+// Writes the bin to S.misc[0] and the "above" amounts to S.misc64[0..1].
+__device__ void find_bin(GenShared& S, int nb, bool by_mass, uint64_t target_or_limit, uint64_t base) {
+  if (threadIdx.x == 0) { S.misc[0] = -1; S.misc64[0] = 0; S.misc64[1] = 0; }
+  // thread t owns descending positions r = 2t, 2t+1 (bin = nb-1-r)
+  uint64_t m0 = 0, m1 = 0;
+  uint32_t c0 = 0, c1 = 0;
+  const int r0 = 2 * threadIdx.x, r1 = r0 + 1;
+  if (r0 < nb) { c0 = S.u.h.cnt[nb - 1 - r0]; m0 = S.u.h.mass[nb - 1 - r0]; }
+  if (r1 < nb) { c1 = S.u.h.cnt[nb - 1 - r1]; m1 = S.u.h.mass[nb - 1 - r1]; }
+  uint64_t v = by_mass ? (m0 + m1) : (uint64_t)(c0 + c1);
+  uint64_t tot;
+  uint64_t ex = gblock_excl_scan<uint64_t>(v, &tot, S.red64);
+  uint64_t a0 = by_mass ? m0 : c0, a1 = by_mass ? m1 : c1;
+  if (by_mass) {
+    uint64_t lim = target_or_limit;
+    if (r0 < nb && base + ex <= lim && lim < base + ex + a0) { S.misc[0] = nb - 1 - r0; S.misc64[0] = ex; }
+    else if (r1 < nb && base + ex + a0 <= lim && lim < base + ex + a0 + a1) { S.misc[0] = nb - 1 - r1; S.misc64[0] = ex + a0; }
+  } else {
+    uint64_t tg = target_or_limit;
+    if (r0 < nb && ex < tg && tg <= ex + a0) { S.misc[0] = nb - 1 - r0; S.misc64[0] = ex; }
+    else if (r1 < nb && ex + a0 < tg && tg <= ex + a0 + a1) { S.misc[0] = nb - 1 - r1; S.misc64[0] = ex + a0; }
+  }
+  __syncthreads();
+}
+
+template <int DT, int VEC>
+__device__ void clear_hist(GenShared& S) {
+  for (int i = threadIdx.x; i < NBINS; i += GEN_NT) { S.u.h.cnt[i] = 0; S.u.h.mass[i] = 0; }
+  __syncthreads();
+}
+
+// kk-th largest key (1-based, counting multiplicity) of keyf over the row.
+// Returns the key; *n_above = number of elements with a strictly larger key.
+template <int DT, int VEC, typename KF>
+__device__ uint32_t select_kth(const void* row, int V, const PenCtx& pc, GenShared& S, uint32_t kk, KF keyf,
+                               uint32_t* n_above) {
+  uint32_t prefix = 0;
+  uint32_t above = 0;
+  for (int l = 0; l < 3; l++) {
+    const int sh = lvl_shift(l), nb = lvl_bins(l);
+    const uint32_t hm = lvl_himask(l);
+    clear_hist<DT, VEC>(S);
+    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+      uint32_t k = keyf(x);
+      if ((k & hm) == prefix) atomicAdd(&S.u.h.cnt[(k >> sh) & (nb - 1)], 1u);
+    });
+    __syncthreads();
+    find_bin(S, nb, false, kk, 0);
+    int b = S.misc[0];
+    uint32_t ex = (uint32_t)S.misc64[0];
+    __syncthreads();
+    if (b < 0) b = 0;  // unreachable when kk <= V
+    prefix |= (uint32_t)b << sh;
+    kk -= ex;
+    above += ex;
+  }
+  *n_above = above;
+  return prefix;
+}
+
+struct MassCut {
+  uint32_t key;    // v*
+  uint64_t above;  // mass strictly above v*
+  uint32_t c_eq;   // elements at v*
+  uint64_t m_eq;   // their total mass
+};
+
+// Largest key v with mass(active, key >= v) > limit (limit < total active mass).
+template <int DT, int VEC, typename KF, typename AF>
+__device__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShared& S, uint64_t limit, KF keyf,
+                               AF massf) {
+  uint32_t prefix = 0;
+  uint64_t A = 0;
+  MassCut mc{};
+  for (int l = 0; l < 3; l++) {
+    const int sh = lvl_shift(l), nb = lvl_bins(l);
+    const uint32_t hm = lvl_himask(l);
+    clear_hist<DT, VEC>(S);
+    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+      uint32_t k;
+      uint64_t m;
+      if (massf(x, &k, &m) && (k & hm) == prefix) {
+        const int b = (k >> sh) & (nb - 1);
+        atomicAdd(&S.u.h.cnt[b], 1u);
+        if (m) atomicAdd((unsigned long long*)&S.u.h.mass[b], (unsigned long long)m);
+      }
+    });
+    __syncthreads();
+    find_bin(S, nb, true, limit, A);
+    int b = S.misc[0];
+    uint64_t ex = S.misc64[0];
+    if (b < 0) b = 0;  // unreachable while limit < total active mass
+    const uint32_t c_b = S.u.h.cnt[b];
+    const uint64_t m_b = S.u.h.mass[b];
+    __syncthreads();
+    prefix |= (uint32_t)b << sh;
+    A += ex;
+    mc.c_eq = c_b;
+    mc.m_eq = m_b;
+  }
+  mc.key = prefix;
+  mc.above = A;
+  return mc;
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.
+// ---------------------------------------------------------------------------
+template <int DT, int VEC>
+__global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
+  __shared__ GenShared S;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
+  const void* row = reinterpret_cast<const char*>(P.logits) +
+                    ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
+  const int V = P.V;
+
+  const float T = P.temperature ? P.temperature[r] : P.temperature_def;
+  const int topk = P.top_k ? P.top_k[r] : P.top_k_def;
+  float topp = P.top_p ? P.top_p[r] : P.top_p_def;
+  const float minp = P.min_p ? P.min_p[r] : P.min_p_def;
+  const float typp = P.typical_p ? P.typical_p[r] : P.typical_p_def;
+  const float rep = P.rep ? P.rep[r] : P.rep_def;
+  const float pres = P.pres ? P.pres[r] : P.pres_def;
+  const float freq = P.freq ? P.freq[r] : P.freq_def;
+  if (topp != topp) topp = 1.0f;  // NaN top_p removes nothing in the reference
+  const bool greedy = !(T > 0.0f);
+  const bool want_lp = P.chosen_logprob || (P.n_top > 0 && P.top_logprobs);
+  const bool want_H = P.entropy != nullptr;
+  int status = 0;
+
+  // ---- history table (counts of distinct in-range ids) ----
+  int hlen = (P.history && P.history_len) ? P.history_len[r] : 0;
+  if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;  // never past the row
+  const bool pen = hlen > 0 && (rep != 1.0f || pres != 0.0f || freq != 0.0f);
+  for (int i = tid; i < BLOOM_WORDS; i += GEN_NT) S.bloom[i] = 0u;
+  for (int i = tid; i < HASH_CAP; i += GEN_NT) { S.hkey[i] = -1; S.hcnt[i] = 0; }
+  __syncthreads();
+  if (pen) {
+    const int32_t* h = P.history + (int64_t)r * P.history_stride;
+    for (int j = tid; j < hlen; j += GEN_NT) {
+      const int id = h[j];
+      if (id < 0 || id >= V) continue;
+      uint32_t s = hash_id(id);
+      for (int p = 0; p < HASH_CAP; p++) {
+        int old = atomicCAS(&S.hkey[s], -1, id);
+        if (old == -1 || old == id) { atomicAdd(&S.hcnt[s], 1); break; }
+        s = (s + 1) & (HASH_CAP - 1);
+      }
+      atomicOr(&S.bloom[(id >> 5) & (BLOOM_WORDS - 1)], 1u << (id & 31));
+    }
+  }
+  __syncthreads();
+  {
+    uint32_t used = 0;
+    for (int i = tid; i < HASH_CAP; i += GEN_NT) used += S.hkey[i] >= 0 ? 1u : 0u;
+    used = gblock_sum_u32(used, S);
+    if (used > LPS_MAX_HISTORY_DISTINCT) status |= LPS_ROW_HISTORY_OVERFLOW;
+  }
+  PenCtx pc{pen, rep, pres, freq, S.bloom, S.hkey, S.hcnt};
+
+  // ---- pass 1: max and first argmax of the penalised logits ----
+  uint64_t best = 0;
+  row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+    const uint64_t pk = ((uint64_t)f2key(x) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+    best = pk > best ? pk : best;
+  });
+  best = gblock_max_u64(best, S);
+  const uint32_t mkey = (uint32_t)(best >> 32);
+  const int argmax = (int)(0xFFFFFFFFu - (uint32_t)best);
+  const float Mx = key2f(mkey);
+  const bool has_nan = mkey == 0xFFFFFFFFu;
+
+  const float Te = greedy ? 1.0f : T;
+  const float zmax = greedy ? Mx : __fdiv_rn(Mx, T);
+  auto zval = [&](float x) -> float { return greedy ? x : __fdiv_rn(x, T); };
+  auto zkey = [&](float x) -> uint32_t { return f2key(zval(x)); };
+
+  int64_t token = -1;
+  if (!greedy) {
+    if (has_nan || Mx == INFINITY || zmax == INFINITY) status |= LPS_ROW_NONFINITE;
+    else if (Mx == -INFINITY) status |= LPS_ROW_EMPTY;
+  } else {
+    token = argmax;
+  }
+  if (status & LPS_ROW_HISTORY_OVERFLOW) token = -1;
+
+  // ---- full-row statistics: Z over all tokens, sum of e * (z - zmax) ----
+  const bool stats_ok = !has_nan && Mx != INFINITY && Mx != -INFINITY && zmax != INFINITY;
+  uint64_t Zfull = 0;
+  double Sed = 0.0;
+  const bool need_full = stats_ok && !(status & LPS_ROW_HISTORY_OVERFLOW) &&
+                         (want_lp || want_H || (!greedy && status == 0 && topk <= 0 && topp < 1.0f) ||
+                          (!greedy && typp < 1.0f));
+  if (need_full) {
+    uint64_t zs = 0;
+    double sd = 0.0;
+    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+      const float z = zval(x);
+      const float e = mass_f(z, zmax);
+      zs += mass_fixed(e);
+      if (e > 0.0f) sd += (double)e * (double)__fsub_rn(z, zmax);
+    });
+    Zfull = gblock_sum_u64(zs, S);
+    Sed = gblock_sum_f64(sd, S);
+  }
+  const double Zf_d = (double)Zfull / (double)kMassScale;
+  const double lnZ = need_full ? log(Zf_d) : 0.0;
+  if (want_H && tid == 0) P.entropy[r] = need_full ? (float)(lnZ - Sed / (double)Zfull * (double)kMassScale) : NAN;
+
+  // ---- sampling-row selection ----
+  uint32_t key_lo = 0, n_tie = kNoTie;
+  uint64_t Zk = 0;
+  float qprob = 0.0f;
+  const int64_t qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
+                           ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
+                           : -1;
+  if (greedy) {
+    key_lo = mkey;
+    n_tie = 1;
+    qprob = (qtok >= 0 && qtok == argmax) ? 1.0f : 0.0f;
+  } else if (status == 0) {
+    // top-k threshold (all ties at the k-th value kept)
+    uint32_t thk = 0;
+    if (topk > 0) {
+      const uint32_t kk = (uint32_t)(topk < V ? topk : V);
+      uint32_t na;
+      thk = select_kth<DT, VEC>(row, V, pc, S, kk, zkey, &na);
+    }
+    key_lo = thk;
+    // top-p cut on the mass of the top-k kept set
+    if (topp < 1.0f) {
+      if (topk <= 0) {
+        Zk = Zfull;
+      } else {
+        uint64_t zs = 0;
+        row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+          const float z = zval(x);
+          if (f2key(z) >= thk) zs += mass_fixed(mass_f(z, zmax));
+        });
+        Zk = gblock_sum_u64(zs, S);
+      }
+      const double pl = topp > 0.0f ? (double)topp * (double)Zk : 0.0;
+      uint64_t limit = (uint64_t)pl;
+      if (limit >= Zk) limit = Zk - 1;
+      MassCut mc = select_mass<DT, VEC>(row, V, pc, S, limit, zkey, [&](float x, uint32_t* k, uint64_t* m) {
+        const float z = zval(x);
+        *k = f2key(z);
+        if (*k < thk) return false;
+        *m = mass_fixed(mass_f(z, zmax));
+        return true;
+      });
+      key_lo = mc.key;
+      const uint64_t e1 = mc.c_eq ? mc.m_eq / mc.c_eq : 0;
+      uint64_t nt = e1 ? (limit - mc.above) / e1 + 1 : (uint64_t)mc.c_eq;
+      n_tie = nt >= mc.c_eq ? kNoTie : (uint32_t)nt;
+    }
+    // min-p: keep e >= min_p (the max has e == 1)
+    if (minp > 0.0f) {
+      uint32_t mk = 0xFFFFFFFFu;
+      row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+        const float z = zval(x);
+        const uint32_t k = f2key(z);
+        if (k >= key_lo && mass_f(z, zmax) >= minp) mk = k < mk ? k : mk;
+      });
+      mk = gblock_min_u32(mk, S);
+      if (mk == 0xFFFFFFFFu) status |= LPS_ROW_EMPTY;
+      else if (mk > key_lo) { key_lo = mk; n_tie = kNoTie; }
+    }
+    // typical-p
+    if (status == 0 && typp < 1.0f) {
+      uint32_t ngt = 0, neq = 0, ninf = 0;
+      const uint32_t kinf = f2key(-INFINITY);
+      row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+        const uint32_t k = zkey(x);
+        ngt += k > key_lo ? 1u : 0u;
+        neq += k == key_lo ? 1u : 0u;
+        ninf += k == kinf ? 1u : 0u;
+      });
+      ngt = gblock_sum_u32(ngt, S);
+      neq = gblock_sum_u32(neq, S);
+      ninf = gblock_sum_u32(ninf, S);
+      const uint32_t nk = ngt + (n_tie == kNoTie ? neq : (n_tie < neq ? n_tie : neq));
+      const uint32_t zmkey = f2key(zmax);
+      if (nk < (uint32_t)V || ninf > 0) {
+        key_lo = zmkey;
+        n_tie = 1;
+      } else {
+        // information = ln Z - d <= exp(H) * typical_p  <=>  d >= ln Z - tau
+        const double H = lnZ - Sed / (double)Zfull * (double)kMassScale;
+        const float tau = __fmul_rn((float)exp(H), typp);
+        const double dmin = lnZ - (double)tau;
+        uint32_t mk = 0xFFFFFFFFu;
+        row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+          const float z = zval(x);
+          if ((double)__fsub_rn(z, zmax) >= dmin) { const uint32_t k = f2key(z); mk = k < mk ? k : mk; }
+        });
+        mk = gblock_min_u32(mk, S);
+        if (mk == 0xFFFFFFFFu) { key_lo = zmkey; n_tie = 1; }
+        else { key_lo = mk; n_tie = kNoTie; }
+      }
+    }
+  }
+
+  // ---- kept mass (vocabulary order, tie ranks) and the query probability ----
+  uint64_t Zf = 0;
+  uint32_t kept_n = greedy ? 1u : 0u;
+  if (!greedy && status == 0) {
+    uint64_t acc = 0;
+    uint32_t tie_run = 0, nkept = 0;
+    uint64_t qm = 0;
+    int qk = 0;
+    for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+      const int64_t i0 = tile + (int64_t)tid * VEC;
+      float x[VEC];
+      uint32_t k[VEC];
+      uint32_t nt_loc = 0;
+      if (i0 < V) {
+        loadv<DT, VEC>(row, i0, x);
+        pc.apply<VEC>(i0, x);
+#pragma unroll
+        for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == key_lo ? 1u : 0u; }
+      }
+      uint32_t tot = 0, ex = 0;
+      if (n_tie != kNoTie) ex = gblock_excl_scan<uint32_t>(nt_loc, &tot, S.red32);
+      if (i0 < V) {
+        uint32_t rk = tie_run + ex;
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+          bool kept = k[j] > key_lo || (k[j] == key_lo && (n_tie == kNoTie || rk < n_tie));
+          if (k[j] == key_lo) rk++;
+          if (kept) {
+            const uint64_t m = mass_fixed(mass_f(zval(x[j]), zmax));
+            acc += m;
+            nkept += k[j] != kNegInfKey ? 1u : 0u;
+            if (i0 + j == qtok) { qm = m; qk = 1; }
+          }
+        }
+      }
+      tie_run += tot;
+    }
+    Zf = gblock_sum_u64(acc, S);
+    kept_n = gblock_sum_u32(nkept, S);
+    const uint64_t qmr = gblock_sum_u64(qm, S);
+    const uint32_t qkr = gblock_sum_u32((uint32_t)qk, S);
+    qprob = qkr ? (float)((double)qmr / (double)Zf) : 0.0f;
+  }
+
+  // ---- inverse-CDF draw in vocabulary order ----
+  if (!greedy && status == 0 && !P.skip_draw) {
+    float u = P.uniforms ? P.uniforms[r] : 0.5f;
+    if (!(u >= 0.0f)) u = 0.0f;
+    if (u >= 1.0f) u = 0.99999994f;
+    uint64_t target = (uint64_t)((double)u * (double)Zf);
+    if (target >= Zf) target = Zf - 1;
+    uint64_t run = 0;
+    uint32_t tie_run = 0;
+    if (tid == 0) S.misc[1] = -1;
+    __syncthreads();
+    for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+      const int64_t i0 = tile + (int64_t)tid * VEC;
+      float x[VEC];
+      uint32_t k[VEC];
+      uint64_t m[VEC];
+      uint32_t nt_loc = 0;
+      uint64_t msum = 0;
+      if (i0 < V) {
+        loadv<DT, VEC>(row, i0, x);
+        pc.apply<VEC>(i0, x);
+#pragma unroll
+        for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == key_lo ? 1u : 0u; }
+      }
+      uint32_t ttot = 0, tex = 0;
+      if (n_tie != kNoTie) tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
+      if (i0 < V) {
+        uint32_t rk = tie_run + tex;
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+          bool kept = k[j] > key_lo || (k[j] == key_lo && (n_tie == kNoTie || rk < n_tie));
+          if (k[j] == key_lo) rk++;
+          m[j] = kept ? mass_fixed(mass_f(zval(x[j]), zmax)) : 0;
+          msum += m[j];
+        }
+      }
+      uint64_t btot;
+      const uint64_t bex = gblock_excl_scan<uint64_t>(msum, &btot, S.red64);
+      if (i0 < V && run + bex <= target && target < run + bex + msum) {
+        uint64_t a = run + bex;
+#pragma unroll
+        for (int j = 0; j < VEC; j++) {
+          if (m[j] && a <= target && target < a + m[j]) S.misc[1] = (int)(i0 + j);
+          a += m[j];
+        }
+      }
+      __syncthreads();
+      const int found = S.misc[1];
+      __syncthreads();
+      if (found >= 0) { token = found; break; }
+      run += btot;
+      tie_run += ttot;
+    }
+  } else if (!greedy) {
+    token = -1;
+  }
+
+  // ---- logprobs: chosen id and top-N of log_softmax(penalised z) ----
+  if (want_lp) {
+    if (P.chosen_logprob && tid == 0) {
+      float lp = NAN;
+      if (token >= 0 && need_full) {
+        float xt = load1<DT>(row, token);
+        float xa[1] = {xt};
+        if (pen) { int c = pc.lookup((int)token); if (c) xa[0] = penalize(xt, c, rep, pres, freq); }
+        lp = (float)((double)__fsub_rn(zval(xa[0]), zmax) - lnZ);
+      }
+      P.chosen_logprob[r] = lp;
+    }
+    if (P.n_top > 0 && P.top_logprobs) {
+      const int N = P.n_top < V ? P.n_top : V;
+      uint32_t nabove;
+      const uint32_t thn = select_kth<DT, VEC>(row, V, pc, S, (uint32_t)N, zkey, &nabove);
+      const uint32_t ties_take = (uint32_t)N - nabove;
+      if (tid == 0) S.u.lst.n = 0;
+      __syncthreads();
+      uint32_t tie_run = 0;
+      for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+        const int64_t i0 = tile + (int64_t)tid * VEC;
+        float x[VEC];
+        uint32_t k[VEC];
+        uint32_t nt_loc = 0;
+        if (i0 < V) {
+          loadv<DT, VEC>(row, i0, x);
+          pc.apply<VEC>(i0, x);
+#pragma unroll
+          for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == thn ? 1u : 0u; }
+        }
+        uint32_t ttot, tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
+        if (i0 < V) {
+          uint32_t rk = tie_run + tex;
+#pragma unroll
+          for (int j = 0; j < VEC; j++) {
+            bool take = k[j] > thn || (k[j] == thn && rk < ties_take);
+            if (k[j] == thn) rk++;
+            if (take) {
+              int slot = atomicAdd(&S.u.lst.n, 1);
+              if (slot < LPS_MAX_TOP_LOGPROBS) { S.u.lst.key[slot] = k[j]; S.u.lst.idx[slot] = (int)(i0 + j); }
+            }
+          }
+        }
+        tie_run += ttot;
+      }
+      __syncthreads();
+      const int n = S.u.lst.n < N ? S.u.lst.n : N;
+      if (tid < n) {
+        const uint32_t ki = S.u.lst.key[tid];
+        const int ii = S.u.lst.idx[tid];
+        int rank = 0;
+        for (int j = 0; j < n; j++) {
+          const uint32_t kj = S.u.lst.key[j];
+          const int ij = S.u.lst.idx[j];
+          rank += (kj > ki || (kj == ki && ij < ii)) ? 1 : 0;
+        }
+        const float z = key2f(ki);
+        P.top_logprobs[(int64_t)r * P.n_top + rank] = need_full ? (float)((double)__fsub_rn(z, zmax) - lnZ) : NAN;
+        if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + rank] = ii;
+      }
+      for (int j = n + tid; j < P.n_top; j += GEN_NT) {
+        P.top_logprobs[(int64_t)r * P.n_top + j] = -INFINITY;
+        if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + j] = -1;
+      }
+      __syncthreads();
+    }
+  }
+
+  if (tid == 0) {
+    const bool failed = (status & LPS_ROW_HISTORY_OVERFLOW) || (!greedy && status != 0);
+    P.tokens[r] = failed ? -1 : token;
+    if (P.row_status) P.row_status[r] = status;
+    if (P.query_prob) P.query_prob[r] = qprob;
+    if (P.kept_cut) P.kept_cut[r] = key_lo <= kNegInfKey ? -INFINITY : key2f(key_lo);  // key 0: nothing cut
+    if (P.kept_ties) P.kept_ties[r] = n_tie == kNoTie ? -1 : (int32_t)n_tie;
+    if (P.kept_count) P.kept_count[r] = (int32_t)kept_n;
+    if (P.plans) {
+      RowPlan pl;
+      pl.zmax = zmax; pl.T = Te; pl.key_lo = key_lo; pl.n_tie = n_tie; pl.Zf = Zf;
+      pl.greedy = greedy ? 1 : 0; pl.argmax = argmax;
+      P.plans[r] = pl;
+    }
+  }
+}
+
+}  // namespace lps

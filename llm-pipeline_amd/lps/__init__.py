@@ -1,0 +1,22 @@
+"""lps: MI355X-native token sampler, a drop-in for the logits -> token path of
+the llm-pipeline inference engine (``llm_pipeline.inference`` exports
+``Sampler``, ``SamplingConfig`` and ``verify_drafts_batched``,
+``src/llm_pipeline/inference/__init__.py:4,17,37-38``)."""
+
+from .batch import SampleOutput, SamplingParams, pad_histories, raise_on_status, sample_rows
+from .sampling import Sampler, SamplingConfig
+from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
+
+__all__ = [
+    "Sampler",
+    "SamplingConfig",
+    "SamplingParams",
+    "SampleOutput",
+    "sample_rows",
+    "pad_histories",
+    "raise_on_status",
+    "verify_drafts_batched",
+    "spec_verify",
+    "SpecVerifyOutput",
+    "SpecDecStats",
+]

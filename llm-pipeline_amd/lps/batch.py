@@ -1,0 +1,197 @@
+"""Batched, per-row sampling on the GPU: one ``lps_sample`` launch for a whole
+decode batch with heterogeneous parameters.
+
+The reference applies per-request parameters by calling the scalar sampler
+once per row (``src/llm_pipeline/inference/continuous_batching.py:394-401``);
+``sample_rows`` gives the same per-row result in one launch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, fields
+from typing import Iterable, Optional, Sequence
+
+import torch
+
+from . import _device as D
+from . import _lib
+
+
+@dataclass
+class SamplingParams:
+    """Per-row sampling parameters as device tensors of length ``B``.
+
+    Field meanings follow ``SamplingConfig`` (reference ``sampling.py:10-37``):
+    ``temperature <= 0`` is greedy, ``top_k <= 0`` and ``top_p >= 1`` are off,
+    ``min_p <= 0`` and ``typical_p >= 1`` are off, ``repetition_penalty == 1``
+    and zero presence / frequency penalties are off."""
+
+    temperature: torch.Tensor
+    top_k: torch.Tensor
+    top_p: torch.Tensor
+    min_p: torch.Tensor
+    typical_p: torch.Tensor
+    repetition_penalty: torch.Tensor
+    presence_penalty: torch.Tensor
+    frequency_penalty: torch.Tensor
+
+    @classmethod
+    def build(cls, B: int, device, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, typical_p=1.0,
+              repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0) -> "SamplingParams":
+        """Scalars broadcast to every row; tensors are taken per row."""
+        return cls(D.as_f32(temperature, B, device), D.as_i32(top_k, B, device), D.as_f32(top_p, B, device),
+                   D.as_f32(min_p, B, device), D.as_f32(typical_p, B, device),
+                   D.as_f32(repetition_penalty, B, device), D.as_f32(presence_penalty, B, device),
+                   D.as_f32(frequency_penalty, B, device))
+
+    @classmethod
+    def from_configs(cls, configs: Sequence, device) -> "SamplingParams":
+        """Tensorise a list of ``SamplingConfig`` objects (one per row)."""
+        cols = {f.name: [] for f in fields(cls)}
+        for c in configs:
+            for name in cols:
+                cols[name].append(getattr(c, name, 0.0 if "penalty" in name and name != "repetition_penalty" else 1.0))
+        return cls(
+            torch.tensor(cols["temperature"], dtype=torch.float32, device=device),
+            torch.tensor([int(v) for v in cols["top_k"]], dtype=torch.int32, device=device),
+            torch.tensor(cols["top_p"], dtype=torch.float32, device=device),
+            torch.tensor(cols["min_p"], dtype=torch.float32, device=device),
+            torch.tensor(cols["typical_p"], dtype=torch.float32, device=device),
+            torch.tensor(cols["repetition_penalty"], dtype=torch.float32, device=device),
+            torch.tensor(cols["presence_penalty"], dtype=torch.float32, device=device),
+            torch.tensor(cols["frequency_penalty"], dtype=torch.float32, device=device),
+        )
+
+
+@dataclass
+class SampleOutput:
+    tokens: torch.Tensor                       # int64 [B]
+    status: torch.Tensor                       # int32 [B], LPS_ROW_* bits
+    chosen_logprob: Optional[torch.Tensor] = None   # float32 [B]
+    top_logprobs: Optional[torch.Tensor] = None     # float32 [B, n]
+    top_ids: Optional[torch.Tensor] = None          # int64 [B, n]
+    query_prob: Optional[torch.Tensor] = None       # float32 [B]
+    entropy: Optional[torch.Tensor] = None          # float32 [B]
+    kept_cut: Optional[torch.Tensor] = None         # float32 [B]: scaled logit at the cut
+    kept_ties: Optional[torch.Tensor] = None        # int32 [B]: kept ids at the cut (-1 = all)
+    kept_count: Optional[torch.Tensor] = None       # int32 [B]
+
+
+def pad_histories(histories: Iterable[Sequence[int]], device) -> tuple:
+    """Per-row token lists -> padded ``int32 [B, H]`` and lengths ``int32 [B]``."""
+    hs = [list(h) for h in histories]
+    H = max([len(h) for h in hs] + [1])
+    buf = torch.zeros((len(hs), H), dtype=torch.int32)
+    lens = torch.zeros((len(hs),), dtype=torch.int32)
+    for i, h in enumerate(hs):
+        if h:
+            buf[i, : len(h)] = torch.tensor(h, dtype=torch.int32)
+        lens[i] = len(h)
+    return buf.to(device), lens.to(device)
+
+
+def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional[torch.Tensor] = None, *,
+                histories: Optional[torch.Tensor] = None, history_lengths: Optional[torch.Tensor] = None,
+                logprobs: bool = False, top_logprobs: int = 0, entropy: bool = False,
+                query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
+                generator: Optional[torch.Generator] = None) -> SampleOutput:
+    """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
+    vocabulary dimension must be contiguous).  Asynchronous: nothing is
+    synchronised and ``status`` is returned as a device tensor."""
+    D.require_device(logits, "logits")
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [B, V]; got {tuple(logits.shape)}")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    B, V = logits.shape
+    dev = logits.device
+    dt = D.dtype_code(logits)
+    if not 0 <= top_logprobs <= _lib.LPS_MAX_TOP_LOGPROBS:
+        raise ValueError(f"top_logprobs must be in [0, {_lib.LPS_MAX_TOP_LOGPROBS}]")
+    if uniforms is None and not skip_draw:
+        uniforms = torch.rand((B,), device=dev, dtype=torch.float32, generator=generator)
+    if uniforms is not None:
+        uniforms = uniforms.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if uniforms.numel() != B:
+            raise ValueError("uniforms must hold one value per row")
+    tokens = torch.empty((B,), dtype=torch.int64, device=dev)
+    status = torch.empty((B,), dtype=torch.int32, device=dev)
+    out = SampleOutput(tokens, status)
+    if logprobs:
+        out.chosen_logprob = torch.empty((B,), dtype=torch.float32, device=dev)
+    if top_logprobs:
+        out.top_logprobs = torch.empty((B, top_logprobs), dtype=torch.float32, device=dev)
+        out.top_ids = torch.empty((B, top_logprobs), dtype=torch.int64, device=dev)
+    if entropy:
+        out.entropy = torch.empty((B,), dtype=torch.float32, device=dev)
+    if kept_set:
+        out.kept_cut = torch.empty((B,), dtype=torch.float32, device=dev)
+        out.kept_ties = torch.empty((B,), dtype=torch.int32, device=dev)
+        out.kept_count = torch.empty((B,), dtype=torch.int32, device=dev)
+    if query_tokens is not None:
+        query_tokens = query_tokens.to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+        out.query_prob = torch.empty((B,), dtype=torch.float32, device=dev)
+    if histories is not None:
+        histories = histories.to(device=dev, dtype=torch.int32)
+        if histories.dim() != 2 or histories.shape[0] != B:
+            raise ValueError("histories must be int32 [B, H]")
+        histories = histories.contiguous()
+        if history_lengths is None:
+            history_lengths = torch.full((B,), histories.shape[1], dtype=torch.int32, device=dev)
+        history_lengths = history_lengths.to(device=dev, dtype=torch.int32).contiguous()
+    p = params
+    a = _lib.SampleArgs()
+    a.logits = D.ptr(logits)
+    a.dtype = dt
+    a.num_rows = B
+    a.vocab = V
+    a.rows_inner = 1
+    a.stride_outer = logits.stride(0)
+    a.stride_inner = 0
+    a.temperature = D.ptr(p.temperature)
+    a.top_k = D.ptr(p.top_k)
+    a.top_p = D.ptr(p.top_p)
+    a.min_p = D.ptr(p.min_p)
+    a.typical_p = D.ptr(p.typical_p)
+    a.repetition_penalty = D.ptr(p.repetition_penalty)
+    a.presence_penalty = D.ptr(p.presence_penalty)
+    a.frequency_penalty = D.ptr(p.frequency_penalty)
+    a.history = D.ptr(histories)
+    a.history_stride = histories.stride(0) if histories is not None else 0
+    a.history_len = D.ptr(history_lengths) if histories is not None else 0
+    a.uniforms = D.ptr(uniforms)
+    a.query_tokens = D.ptr(query_tokens)
+    a.query_inner = 1 if query_tokens is not None else 0
+    a.query_prob = D.ptr(out.query_prob)
+    a.tokens = D.ptr(tokens)
+    a.chosen_logprob = D.ptr(out.chosen_logprob)
+    a.top_logprobs = D.ptr(out.top_logprobs)
+    a.top_ids = D.ptr(out.top_ids)
+    a.n_top = top_logprobs
+    a.entropy = D.ptr(out.entropy)
+    a.row_status = D.ptr(status)
+    a.skip_draw = 1 if skip_draw else 0
+    a.kept_cut = D.ptr(out.kept_cut)
+    a.kept_ties = D.ptr(out.kept_ties)
+    a.kept_count = D.ptr(out.kept_count)
+    ws_bytes = _lib.load().lps_workspace_bytes(B, V, 0)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
+    a.workspace = D.ptr(ws)
+    a.workspace_bytes = ws_bytes
+    with torch.cuda.device(dev):
+        rc = _lib.load().lps_sample(ctypes.byref(a), D.stream_of(dev))
+    _lib.check(rc, "lps_sample")
+    return out
+
+
+def raise_on_status(status: torch.Tensor) -> None:
+    """Raise what the reference raises for rows the kernel could not sample
+    (``torch.multinomial`` rejects NaN / inf / empty distributions)."""
+    bad = int(status.ne(0).any().item())
+    if not bad:
+        return
+    s = int(status.max().item())
+    if s & _lib.LPS_ROW_HISTORY_OVERFLOW:
+        raise ValueError(f"token history holds more than {_lib.LPS_MAX_HISTORY_DISTINCT} distinct ids")
+    raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")

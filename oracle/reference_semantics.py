@@ -1,0 +1,497 @@
+"""CPU oracle for the token-sampling hot path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (``llm-pipeline_amd/``) may
+import, call or execute this module.  Only ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker
+(or as the timed CPU baseline), never as the thing measured on the GPU.
+
+It restates, op for op in torch-CPU fp32, the reference sampler of
+DavidAkinpelu/llm-pipeline:
+
+* ``src/llm_pipeline/inference/sampling.py:51-238``   (Sampler.sample_token and
+  its filters), ``:240-279`` (Mirostat v2);
+* ``src/llm_pipeline/inference/speculative.py:50-62, 119-174, 264-276``
+  (sampling primitives and the accept / reject / resample step);
+* ``src/llm_pipeline/inference/speculative_kernel.py:24-58, 84-87``
+  (``verify_drafts_batched`` and its torch reference);
+* ``src/llm_pipeline/inference/continuous_batching.py:394-401`` (heterogeneous
+  per-row parameters = one scalar-parameter call per row).
+
+Parity rules adopted (the reference leaves these open):
+
+1. bf16 / fp16 logits are upcast to fp32 before any op ("fp32 accumulate").
+2. ``x / T`` and ``x / penalty`` are correctly rounded fp32 divisions.
+3. Sort ties are resolved lower-index-first (``torch.sort(stable=True)``); the
+   reference's default sort is unstable, so only tie *counts* are reference-fixed.
+4. Top-p decisions are compared bit-exactly outside an epsilon band around
+   ``cum == top_p`` (see ``top_p_band``).
+
+Build extensions (absent from the reference, defined here by closed form):
+presence / frequency penalties (OpenAI definition), per-row histories,
+caller-supplied uniforms with an inverse-CDF draw in vocabulary order, the
+probability of a query token under the kept distribution, full-vocab logprobs
+and top-N logprobs.
+
+Pinning: every function here is checked in ``tests/test_oracle.py`` against a
+brute-force loop, a closed form, a library routine or the reference's own
+known-answer tests (``testing/unit/test_kernels_low_level.py:439-466``,
+``testing/unit/test_speculative_decoding.py:59-150``).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+LOG2E = 1.4426950408889634
+# Fixed-point scale used by the GPU path for softmax masses (mass in (0, 1]).
+MASS_FRAC_BITS = 44
+
+
+@dataclass
+class RowParams:
+    """Scalar sampling parameters of one row (reference ``SamplingConfig``,
+    ``sampling.py:10-37``, plus the build's presence/frequency penalties)."""
+
+    temperature: float = 1.0
+    top_k: int = 50
+    top_p: float = 0.9
+    min_p: float = 0.0
+    typical_p: float = 1.0
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+
+
+def upcast(logits: torch.Tensor) -> torch.Tensor:
+    """Parity rule 1: fp32 copy on the CPU (never mutates the caller's tensor)."""
+    return logits.detach().to("cpu", torch.float32).clone()
+
+
+def f32(v: float) -> np.float32:
+    return np.float32(v)
+
+
+# --------------------------------------------------------------------------- #
+# Penalties
+# --------------------------------------------------------------------------- #
+
+
+def apply_repetition_penalty(x: torch.Tensor, history: Sequence[int], penalty: float) -> torch.Tensor:
+    """CTRL penalty, ``sampling.py:108-137``: ids filtered to ``[0, V)`` (:126),
+    de-duplicated with ``torch.unique`` (:130) so each distinct id is penalised
+    once, ``where(x > 0, x / pen, x * pen)`` (:133), scattered into a clone.
+    ``x`` is ``[B, V]``; the one history applies to every row, as in the
+    reference."""
+    if not history or penalty == 1.0:
+        return x
+    V = x.size(-1)
+    t = torch.tensor(list(history), dtype=torch.int64)
+    t = t[(t >= 0) & (t < V)]
+    if t.numel() == 0:
+        return x
+    u = torch.unique(t)
+    sel = x.index_select(dim=-1, index=u)
+    adj = torch.where(sel > 0, sel / penalty, sel * penalty)
+    x = x.clone()
+    x[:, u] = adj
+    return x
+
+
+def apply_presence_frequency(x: torch.Tensor, history: Sequence[int], presence: float,
+                             frequency: float) -> torch.Tensor:
+    """Build extension (absent from the reference): OpenAI presence / frequency
+    penalties, ``x[d] -= cnt_d * frequency`` then ``x[d] -= presence`` for every
+    distinct in-range id ``d`` of the history, each step rounded to fp32.
+    Applied after the repetition penalty and before temperature."""
+    if not history or (presence == 0.0 and frequency == 0.0):
+        return x
+    V = x.size(-1)
+    t = torch.tensor(list(history), dtype=torch.int64)
+    t = t[(t >= 0) & (t < V)]
+    if t.numel() == 0:
+        return x
+    u, cnt = torch.unique(t, return_counts=True)
+    x = x.clone()
+    sel = x.index_select(dim=-1, index=u)
+    if frequency != 0.0:
+        sel = sel - cnt.to(torch.float32) * torch.tensor(frequency, dtype=torch.float32)
+    if presence != 0.0:
+        sel = sel - torch.tensor(presence, dtype=torch.float32)
+    x[:, u] = sel
+    return x
+
+
+# --------------------------------------------------------------------------- #
+# Filters (sampling.py)
+# --------------------------------------------------------------------------- #
+
+
+def apply_top_k(z: torch.Tensor, top_k: int) -> torch.Tensor:
+    """``sampling.py:139-156``: ``k <= 0`` no-op; ``k = min(k, V)``; keep
+    ``z >= kth`` (all ties at the k-th value are kept)."""
+    if top_k <= 0:
+        return z
+    k = min(top_k, z.size(-1))
+    kth = torch.topk(z, k, dim=-1).values[:, -1].unsqueeze(-1)
+    return torch.where(z < kth, torch.full_like(z, float("-inf")), z)
+
+
+def apply_top_p(z: torch.Tensor, top_p: float) -> torch.Tensor:
+    """``sampling.py:158-185`` with a stable sort (parity rule 3): sort
+    descending, fp32 softmax, cumsum, remove ``cum > top_p`` shifted right by
+    one, position 0 always kept, scatter back, ``masked_fill(-inf)``."""
+    if top_p >= 1.0:
+        return z
+    sz, si = torch.sort(z, descending=True, dim=-1, stable=True)
+    probs = F.softmax(sz, dim=-1)
+    cum = torch.cumsum(probs, dim=-1)
+    rm = cum > top_p
+    rm[:, 1:] = rm[:, :-1].clone()
+    rm[:, 0] = False
+    remove = torch.zeros_like(z, dtype=torch.bool)
+    remove.scatter_(1, si, rm)
+    return z.masked_fill(remove, float("-inf"))
+
+
+def apply_min_p(z: torch.Tensor, min_p: float) -> torch.Tensor:
+    """``sampling.py:187-205``: remove ``softmax(z) < min_p * max(softmax(z))``."""
+    if min_p <= 0.0:
+        return z
+    probs = F.softmax(z, dim=-1)
+    mx, _ = torch.max(probs, dim=-1, keepdim=True)
+    return z.masked_fill(probs < min_p * mx, float("-inf"))
+
+
+def apply_typical_p(z: torch.Tensor, typical_p: float) -> torch.Tensor:
+    """``sampling.py:207-238``, restated op for op.  Note the reference's
+    behaviour when the row already holds ``-inf`` (from top-k / top-p or the
+    input): ``probs * log_probs`` is ``0 * -inf = NaN``, the entropy is NaN, no
+    token passes ``information <= NaN`` and the per-row fallback keeps only the
+    argmax (``:231-234``)."""
+    if typical_p >= 1.0:
+        return z
+    probs = F.softmax(z, dim=-1)
+    logp = F.log_softmax(z, dim=-1)
+    ent = -torch.sum(probs * logp, dim=-1, keepdim=True)
+    thr = torch.exp(ent) * typical_p
+    mask = (-logp) <= thr
+    for i in range(mask.size(0)):
+        if not mask[i].any():
+            mask[i, torch.argmax(z[i])] = True
+    return torch.where(mask, z, torch.full_like(z, float("-inf")))
+
+
+# --------------------------------------------------------------------------- #
+# One row through the whole path
+# --------------------------------------------------------------------------- #
+
+
+@dataclass
+class RowResult:
+    greedy: bool
+    token: int                    # greedy argmax, or the inverse-CDF draw
+    x: torch.Tensor               # penalised fp32 logits [V]
+    z: torch.Tensor               # temperature-scaled pre-filter logits [V] (x for greedy)
+    filtered: Optional[torch.Tensor]   # after all filters, -inf = removed [V]; None for greedy
+    kept: Optional[np.ndarray]    # bool [V]
+    probs64: Optional[np.ndarray]  # final distribution in fp64 [V]
+    error: Optional[str] = None
+
+
+def penalise_row(x_row: torch.Tensor, p: RowParams, history: Sequence[int]) -> torch.Tensor:
+    """Penalties on one row ``[V]``; the reference applies the repetition
+    penalty only when the history is non-empty and ``penalty != 1``
+    (``sampling.py:69-70``)."""
+    x = x_row.reshape(1, -1)
+    if history and p.repetition_penalty != 1.0:
+        x = apply_repetition_penalty(x, history, p.repetition_penalty)
+    x = apply_presence_frequency(x, history, p.presence_penalty, p.frequency_penalty)
+    return x.reshape(-1)
+
+
+def filter_row(z_row: torch.Tensor, p: RowParams) -> torch.Tensor:
+    """Filters in the reference order (``sampling.py:77-82``)."""
+    z = z_row.reshape(1, -1)
+    z = apply_top_k(z, p.top_k)
+    z = apply_top_p(z, p.top_p)
+    z = apply_min_p(z, p.min_p)
+    if p.typical_p < 1.0:
+        z = apply_typical_p(z, p.typical_p)
+    return z.reshape(-1)
+
+
+def draw_inverse_cdf(filtered: torch.Tensor, u: float) -> int:
+    """Build definition of the draw from caller uniform ``u in [0, 1)``: the
+    kept distribution ``p_i ~ exp(z_i - max z)`` in fp64, and the first index
+    in vocabulary order whose inclusive cumulative mass exceeds ``u * Z``.  The
+    reference's ``torch.multinomial`` draws from the same distribution
+    (``sampling.py:84-85``)."""
+    zf = filtered.double().numpy()
+    m = np.max(zf)
+    e = np.where(np.isfinite(zf), np.exp(zf - m), 0.0)
+    cum = np.cumsum(e)
+    tgt = u * cum[-1]
+    j = int(np.searchsorted(cum, tgt, side="right"))
+    if j >= len(e):                      # u * Z rounded up to Z: last kept id
+        j = int(np.nonzero(e > 0)[0][-1])
+    return j
+
+
+def sample_row(x_row: torch.Tensor, p: RowParams, history: Sequence[int] = (), u: float = 0.5) -> RowResult:
+    """Whole path for one row (``sampling.py:51-85`` with the build's draw)."""
+    x = penalise_row(upcast(x_row).reshape(-1), p, list(history))
+    if p.temperature <= 0:
+        tok = int(torch.argmax(x).item())
+        return RowResult(True, tok, x, x, None, None, None)
+    z = x / p.temperature
+    if torch.isnan(z).any() or torch.isposinf(z).any() or torch.isneginf(z).all():
+        return RowResult(False, -1, x, z, None, None, None, error="nonfinite")
+    filt = filter_row(z, p)
+    kept = torch.isfinite(filt).numpy()
+    zf = filt.double().numpy()
+    m = np.max(zf)
+    e = np.where(kept, np.exp(zf - m), 0.0)
+    probs = e / e.sum()
+    tok = draw_inverse_cdf(filt, u)
+    return RowResult(False, tok, x, z, filt, kept, probs)
+
+
+def sample_rows(logits: torch.Tensor, params: Sequence[RowParams], histories: Sequence[Sequence[int]],
+                uniforms: Sequence[float]) -> List[RowResult]:
+    """Heterogeneous per-row parameters: one scalar call per row, as the
+    reference's continuous batcher does (``continuous_batching.py:394-401``)."""
+    return [sample_row(logits[i], params[i], histories[i], float(uniforms[i])) for i in range(logits.shape[0])]
+
+
+# --------------------------------------------------------------------------- #
+# Reference-as-written sampler (CPU baseline timing and multinomial checks)
+# --------------------------------------------------------------------------- #
+
+
+def reference_sample_token(logits: torch.Tensor, p: RowParams, generated_tokens: Optional[List[int]] = None,
+                           generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """``Sampler.sample_token`` (``sampling.py:51-85``) on fp32 CPU logits
+    ``[B, V]`` with one shared history, ending in ``torch.multinomial``."""
+    x = upcast(logits)
+    if generated_tokens and p.repetition_penalty != 1.0:
+        x = apply_repetition_penalty(x, generated_tokens, p.repetition_penalty)
+    x = apply_presence_frequency(x, generated_tokens or [], p.presence_penalty, p.frequency_penalty)
+    if p.temperature > 0:
+        x = x / p.temperature
+    else:
+        return torch.argmax(x, dim=-1)
+    x = apply_top_k(x, p.top_k)
+    x = apply_top_p(x, p.top_p)
+    x = apply_min_p(x, p.min_p)
+    if p.typical_p < 1.0:
+        x = apply_typical_p(x, p.typical_p)
+    probs = F.softmax(x, dim=-1)
+    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(1)
+
+
+# --------------------------------------------------------------------------- #
+# Logprobs (build extension)
+# --------------------------------------------------------------------------- #
+
+
+def logprobs_row(z_pre: torch.Tensor, token: int, n_top: int):
+    """Full-vocab ``log_softmax`` of the penalised, temperature-scaled,
+    pre-filter logits (temperature 1 for greedy rows) at the chosen id, plus
+    the top-``n_top`` ``(logprob, id)`` pairs, ties lower-index-first.  The
+    nearest reference code is ``advanced_sampling.py:81-82`` (log_softmax then
+    topk)."""
+    lp = F.log_softmax(z_pre.reshape(1, -1), dim=-1).reshape(-1)
+    chosen = float(lp[token].item())
+    # log_softmax is monotone in z: rank by z itself (ties lower index first)
+    order = np.lexsort((np.arange(lp.numel()), -z_pre.reshape(-1).double().numpy()))[:n_top]
+    return chosen, lp[order].numpy().astype(np.float32), order.astype(np.int64)
+
+
+def entropy_row(z: torch.Tensor) -> float:
+    """Shannon entropy of ``softmax(z)`` in nats (``sampling.py:261-264``)."""
+    probs = F.softmax(z.reshape(1, -1), dim=-1)
+    lp = F.log_softmax(z.reshape(1, -1), dim=-1)
+    return float(-torch.sum(probs * lp).item())
+
+
+# --------------------------------------------------------------------------- #
+# Top-p epsilon band (parity rule 4)
+# --------------------------------------------------------------------------- #
+
+
+def top_p_truth(z_after_topk: torch.Tensor, top_p: float):
+    """fp64 truth for the top-p keep rule on one row: stable descending order,
+    exclusive prefix mass ``cum_{j-1}`` (normalised), and the kept count under
+    "keep j iff j == 0 or cum_{j-1} <= top_p"."""
+    zz = z_after_topk.double().numpy()
+    order = np.lexsort((np.arange(zz.size), -zz))
+    s = zz[order]
+    fin = np.isfinite(s)
+    e = np.where(fin, np.exp(s - s[0]), 0.0)
+    cum = np.cumsum(e) / e.sum()
+    excl = np.concatenate([[0.0], cum[:-1]])
+    keep = excl <= top_p
+    keep[0] = True
+    n = int(np.argmin(keep)) if not keep.all() else keep.size
+    return order, excl, n
+
+
+def top_p_reference_cum(z_after_topk: torch.Tensor):
+    """The reference's own exclusive prefix masses in stable descending order:
+    fp32 softmax then fp32 ``cumsum`` (``sampling.py:171-174``), as fp64."""
+    zz = z_after_topk.reshape(1, -1)
+    sz, si = torch.sort(zz, descending=True, dim=-1, stable=True)
+    cum = torch.cumsum(F.softmax(sz, dim=-1), dim=-1).reshape(-1).double().numpy()
+    return np.concatenate([[0.0], cum[:-1]])
+
+
+def top_p_reference_rounding(z_after_topk: torch.Tensor, top_p: float, n_a: int, n_b: int,
+                             eps: float = 2e-6) -> bool:
+    """True when kept counts ``n_a`` and ``n_b`` differ only at sorted
+    positions where the reference's fp32 prefix mass is further from the fp64
+    truth than the truth is from ``top_p`` (the reference's own rounding moved
+    its boundary), up to ``eps``."""
+    if n_a == n_b:
+        return True
+    _, excl, _ = top_p_truth(z_after_topk, top_p)
+    ref = top_p_reference_cum(z_after_topk)
+    lo, hi = sorted((n_a, n_b))
+    dist = np.abs(excl[lo:hi] - top_p)
+    err = np.abs(ref[lo:hi] - excl[lo:hi])
+    return bool(np.all(dist <= err + eps))
+
+
+def top_p_band(z_after_topk: torch.Tensor, top_p: float, n_a: int, n_b: int, eps: float = 2e-6) -> bool:
+    """True when two kept counts differ only at positions whose exclusive
+    prefix mass lies within ``eps`` of ``top_p`` (boundary-ambiguous)."""
+    if n_a == n_b:
+        return True
+    _, excl, _ = top_p_truth(z_after_topk, top_p)
+    lo, hi = sorted((n_a, n_b))
+    return bool(np.all(np.abs(excl[lo:hi] - top_p) <= eps))
+
+
+# --------------------------------------------------------------------------- #
+# Speculative decoding (speculative.py, speculative_kernel.py)
+# --------------------------------------------------------------------------- #
+
+
+def softmax_with_temp(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """``speculative.py:50-57``: one-hot argmax for ``T <= 0`` else
+    ``softmax(logits / T)``."""
+    if temperature <= 0:
+        idx = logits.argmax(dim=-1, keepdim=True)
+        out = torch.zeros_like(logits)
+        out.scatter_(-1, idx, 1.0)
+        return out
+    return F.softmax(logits / temperature, dim=-1)
+
+
+def verify_drafts_ref(target_probs: torch.Tensor, draft_probs: torch.Tensor, draft_tokens: torch.Tensor,
+                      rand_uniform: torch.Tensor) -> torch.Tensor:
+    """``speculative_kernel.py:84-87``: ``accept = u < min(p / max(q, 1e-9), 1)``
+    as int8."""
+    p = target_probs.gather(-1, draft_tokens.unsqueeze(-1)).squeeze(-1)
+    ratio = (p / draft_probs.clamp_min(1e-9)).clamp(max=1.0)
+    return (rand_uniform < ratio).to(torch.int8)
+
+
+def spec_probs_row(logits_row: torch.Tensor, temperature: float, top_p: float) -> torch.Tensor:
+    """Distribution of one speculative row: ``T <= 0`` gives the reference's
+    one-hot (``speculative.py:50-56``); otherwise temperature, then the build's
+    top-p filter (the reference speculative path has none), then softmax."""
+    x = upcast(logits_row).reshape(1, -1)
+    if temperature <= 0:
+        return softmax_with_temp(x, 0.0).reshape(-1)
+    z = apply_top_p(x / temperature, top_p)
+    return F.softmax(z, dim=-1).reshape(-1)
+
+
+def spec_verify_ref(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_tokens: torch.Tensor,
+                    u_accept: torch.Tensor, u_resample: torch.Tensor, temperature: float, top_p: float = 1.0,
+                    residual: str = "target"):
+    """Batched restatement of the accept / reject / resample block
+    (``speculative.py:119-174``) for ``B`` requests of draft length ``k``.
+
+    target_logits ``[B, k+1, V]``, draft_logits ``[B, k, V]``, draft_tokens
+    ``[B, k]``, u_accept ``[B, k]``, u_resample ``[B, k+1]``.  Position ``i``
+    is accepted iff ``u < min(p/max(q, 1e-9), 1)`` (``:134-135``); greedy
+    accepts iff the target one-hot is 1 at the draft token (``:130-132``).  On
+    the first reject ``j`` the replacement is drawn from the target
+    distribution (``residual="target"``, the reference's ``:150-157``) or from
+    ``norm(max(p - q, 0))`` (``"leviathan"``); greedy takes the target argmax
+    (``:147-148``).  If all ``k`` are accepted a bonus token is drawn from
+    target row ``k`` (``:166-170``).  Returns ``(n_accepted[B], tokens[B, k+1],
+    accept_bits[B, k], p[B, k], q[B, k])``; ``tokens`` is ``-1`` past the
+    emitted ones."""
+    B, k1, V = target_logits.shape
+    k = k1 - 1
+    n_acc = torch.zeros(B, dtype=torch.int64)
+    out = torch.full((B, k1), -1, dtype=torch.int64)
+    bits = torch.zeros((B, k), dtype=torch.int8)
+    P = torch.zeros((B, k), dtype=torch.float32)
+    Q = torch.zeros((B, k), dtype=torch.float32)
+    for b in range(B):
+        rejected = -1
+        for i in range(k):
+            tp = spec_probs_row(target_logits[b, i], temperature, top_p)
+            dp = spec_probs_row(draft_logits[b, i], temperature, top_p)
+            tok = int(draft_tokens[b, i])
+            p = tp[tok]
+            q = dp[tok]
+            P[b, i] = p
+            Q[b, i] = q
+            if temperature == 0.0:
+                acc = bool(p.item() == 1.0)
+            else:
+                ratio = (p / q.clamp_min(1e-9)).clamp(max=1.0)
+                acc = bool(float(u_accept[b, i]) < float(ratio))
+            bits[b, i] = int(acc)
+            if rejected < 0:
+                if acc:
+                    out[b, i] = tok
+                    n_acc[b] += 1
+                else:
+                    rejected = i
+        j = rejected if rejected >= 0 else k
+        tz = upcast(target_logits[b, j]).reshape(-1)
+        if temperature == 0.0:
+            out[b, j] = int(torch.argmax(tz).item())
+        else:
+            z = apply_top_p((tz / temperature).reshape(1, -1), top_p).reshape(-1)
+            if rejected >= 0 and residual == "leviathan":
+                tp = spec_probs_row(target_logits[b, j], temperature, top_p).double()
+                dp = spec_probs_row(draft_logits[b, j], temperature, top_p).double()
+                r = torch.clamp(tp - dp, min=0.0)
+                if float(r.sum()) <= 0.0:
+                    r = tp
+                cum = torch.cumsum(r, 0)
+                tgt = float(u_resample[b, j]) * float(cum[-1])
+                out[b, j] = int(min(int(torch.searchsorted(cum, torch.tensor([tgt], dtype=torch.float64), right=True)), V - 1))
+            else:
+                out[b, j] = draw_inverse_cdf(z, float(u_resample[b, j]))
+    return n_acc, out, bits, P, Q
+
+
+def mirostat_v2_ref(logits: torch.Tensor, temperature: float, tau: float, eta: float,
+                    previous_entropy: Optional[float], u: float):
+    """``sampling.py:240-279`` with the build's inverse-CDF draw: entropy of
+    ``softmax(logits / T)``, ``prev -= eta * (H - tau)``, top-k with
+    ``k = max(1, int(exp(prev)))`` when ``prev > 0``, then a draw."""
+    x = upcast(logits).reshape(1, -1)
+    if temperature > 0:
+        x = x / temperature
+    H = entropy_row(x)
+    prev = H if previous_entropy is None else previous_entropy
+    prev -= eta * (H - tau)
+    k = 0
+    if prev > 0:
+        k = max(1, int(math.exp(prev)))
+        x = apply_top_k(x, k)
+    return draw_inverse_cdf(x.reshape(-1), u), prev, k

@@ -1,0 +1,298 @@
+"""GPU parity of the HIP sampler against the CPU oracle, through the C ABI
+(``lps.sample_rows`` -> ``lps_sample``), on the seeded BASELINE.json
+configurations and the reference's edge cases."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_semantics as O
+from tests import parity as PY
+from tests import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(msg):
+    print(msg, flush=True)
+
+
+def test_c1_single_row_sampling_and_greedy(dev):
+    for greedy in (False, True):
+        w = W.c1(greedy=greedy)
+        out = PY.run_workload(w, dev)
+        rep = PY.check_rows(w, out)
+        _print(f"c1 greedy={greedy}: {rep}")
+
+
+def test_c2_mixed_params_bf16_full_size(dev):
+    w = W.c2()
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out)
+    _print(f"c2: {rep}")
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_c3_nucleus_fp32(dev, flat):
+    w = W.c3(B=16, flat=flat)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out)
+    _print(f"c3 flat={flat}: {rep} kept_counts={out.kept_count.cpu().tolist()[:6]}")
+
+
+def test_c5_logprobs_fp16_subset(dev):
+    w = W.c5(B=32)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out, lp=True)
+    _print(f"c5 subset: {rep}")
+
+
+def test_c5_full_size_properties(dev):
+    """B=512 fp16 with logprobs at full size: size-independent properties."""
+    w = W.c5()
+    out = PY.run_workload(w, dev)
+    tok = out.tokens.cpu()
+    assert (out.status.cpu() == 0).all()
+    assert ((tok >= 0) & (tok < w.V)).all()
+    lp = out.chosen_logprob.cpu()
+    tl = out.top_logprobs.cpu()
+    ti = out.top_ids.cpu()
+    assert (lp <= 1e-6).all() and (tl <= 1e-6).all()
+    assert (tl[:, :-1] >= tl[:, 1:]).all()                 # sorted descending
+    greedy = w.temperature <= 0
+    assert torch.equal(ti[greedy, 0], tok[greedy])          # greedy token = top-1 id
+    assert torch.allclose(lp[greedy], tl[greedy, 0])
+    assert (lp[~greedy] <= tl[~greedy, 0] + 1e-6).all()
+    # sampled rows draw inside their top-40 (top_k = 40, ties aside)
+    cnt = out.kept_count.cpu()
+    assert (cnt[~greedy] >= 1).all() and (cnt[~greedy] <= 60).all()
+    # a few full-size rows against the oracle
+    PY.check_rows(w, out, rows=[0, 1, 257, 511], lp=True)
+
+
+def test_determinism_repeat(dev):
+    w = W.c2(B=16)
+    a = PY.run_workload(w, dev)
+    b = PY.run_workload(w, dev)
+    assert torch.equal(a.tokens, b.tokens)
+    assert torch.equal(a.kept_cut, b.kept_cut) and torch.equal(a.kept_ties, b.kept_ties)
+
+
+def _small(V, B, dtype, seed, **over):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    x = torch.randn((B, V), generator=g) * 2
+    if seed % 3 == 0:
+        x = torch.round(x * 2)             # ties
+    x = x.to(dtype)
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    T = torch.from_numpy(rng.choice([0.0, 0.5, 1.0, 1.7, -1.0], size=B).astype(np.float32))
+    k = torch.from_numpy(rng.choice([0, 1, 3, V, V + 5], size=B).astype(np.int32))
+    p = torch.from_numpy(rng.choice([1.0, 0.9, 0.5, 0.0, -0.5], size=B).astype(np.float32))
+    H = 12
+    hist = torch.from_numpy(rng.integers(-3, V + 3, size=(B, H)).astype(np.int32))
+    hl = torch.from_numpy(rng.integers(0, H + 1, size=B).astype(np.int32))
+    w = W.Workload("small", x, T, k, p, f(0.0), f(1.0), f(1.3), f(0.2), f(0.1), hist, hl, torch.rand((B,), generator=g))
+    for kk, vv in over.items():
+        setattr(w, kk, vv)
+    return w
+
+
+@pytest.mark.parametrize("V", [1, 7, 64, 1000, 4099])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_small_vocab_mixed_params(dev, V, dtype):
+    """Scalar (V % 8 != 0) and vector paths, ties, every filter edge, penalties
+    with out-of-range and empty histories."""
+    w = _small(V, 24, dtype, seed=V + int(dtype == torch.bfloat16) * 7)
+    out = PY.run_workload(w, dev)
+    PY.check_rows(w, out)
+
+
+@pytest.mark.parametrize("what", ["min_p", "typical", "typical_noinf"])
+def test_min_p_typical(dev, what):
+    B, V = 16, 512
+    w = _small(V, B, torch.float32, seed=11)
+    w.temperature = torch.full((B,), 0.8)
+    if what == "min_p":
+        w.min_p = torch.linspace(0.01, 0.9, B)
+    elif what == "typical":
+        w.typical_p = torch.full((B,), 0.7)           # with top-k / top-p active -> argmax fallback
+    else:
+        w.typical_p = torch.linspace(0.2, 0.99, B)
+        w.top_k = torch.zeros(B, dtype=torch.int32)
+        w.top_p = torch.ones(B)
+    out = PY.run_workload(w, dev)
+    PY.check_rows(w, out)
+
+
+def test_strided_rows_engine_view(dev):
+    """logits[:, -1, :] of a [B, T, V] tensor (qwen3_engine.py:528)."""
+    g = torch.Generator().manual_seed(12)
+    B, T, V = 8, 3, 5000
+    big = (torch.randn((B, T, V), generator=g) * 2).to(dev)
+    view = big[:, -1, :]
+    from lps import SamplingParams, sample_rows
+    u = torch.rand(B, generator=g)
+    p = SamplingParams.build(B, dev, temperature=0.9, top_k=30, top_p=0.9)
+    out = sample_rows(view, p, u.to(dev), kept_set=True)
+    ref = sample_rows(view.contiguous(), p, u.to(dev), kept_set=True)
+    assert torch.equal(out.tokens, ref.tokens)
+    w = W.Workload("strided", view.cpu().contiguous(), torch.full((B,), 0.9), torch.full((B,), 30, dtype=torch.int32),
+                   torch.full((B,), 0.9), torch.zeros(B), torch.ones(B), torch.ones(B), torch.zeros(B), torch.zeros(B),
+                   None, None, u)
+    PY.check_rows(w, out)
+
+
+def test_nonfinite_rows_report_status(dev):
+    from lps import SamplingParams, sample_rows, Sampler
+    V = 300
+    x = torch.randn(4, V)
+    x[0, 5] = float("nan")
+    x[1, :] = float("-inf")
+    x[2, 7] = float("inf")
+    x[3, 9] = float("nan")
+    p = SamplingParams.build(4, dev, temperature=torch.tensor([1.0, 1.0, 1.0, 0.0]))
+    out = sample_rows(x.to(dev), p, torch.rand(4).to(dev))
+    st = out.status.cpu().tolist()
+    assert st[0] == 1 and st[1] == 2 and st[2] == 1 and st[3] == 0
+    assert out.tokens.cpu().tolist()[:3] == [-1, -1, -1]
+    assert out.tokens.cpu().tolist()[3] == 9              # torch.argmax returns the NaN index
+    with pytest.raises(RuntimeError):
+        Sampler().sample_token(x[:1].to(dev), {"temperature": 1.0})
+
+
+def test_chi_square_one_million_draws(dev):
+    """North-star distribution test: 1e6 draws of one row vs the fp64 kept law."""
+    from scipy.stats import chisquare
+    from lps import SamplingParams, sample_rows
+    g = torch.Generator().manual_seed(13)
+    V, N = 96, 1_000_000
+    row = torch.randn((1, V), generator=g) * 1.5
+    params = O.RowParams(temperature=0.7, top_k=40, top_p=0.9)
+    r = O.sample_row(row[0], params, [], 0.5)
+    x = row.to(dev).expand(N, V)                          # stride 0 over rows
+    p = SamplingParams.build(N, dev, temperature=0.7, top_k=40, top_p=0.9)
+    u = torch.rand(N, device=dev)
+    out = sample_rows(x, p, u)
+    counts = torch.bincount(out.tokens, minlength=V).cpu().numpy()
+    kept = r.kept
+    assert counts[~kept].sum() == 0
+    stat, pval = chisquare(counts[kept], r.probs64[kept] * N)
+    _print(f"chi-square 1e6 draws: kept={int(kept.sum())} stat={stat:.1f} p={pval:.3g}")
+    assert pval > 1e-4
+
+
+def test_sampler_drop_in_matches_oracle(dev):
+    """Sampler.sample_token with the reference call shape: one override dict and
+    one shared history for the whole batch (sampling.py:51-85)."""
+    from lps import Sampler, SamplingConfig
+    g = torch.Generator().manual_seed(14)
+    B, V = 6, 3000
+    x = torch.randn((B, V), generator=g) * 2
+    hist = [5, 9, 9, 2999, 3000, -1]
+    u = torch.rand(B, generator=g)
+    s = Sampler(SamplingConfig(temperature=0.8, top_k=20, top_p=0.85, repetition_penalty=1.2))
+    tok = s.sample_token(x.to(dev), None, hist, uniforms=u.to(dev)).cpu()
+    for i in range(B):
+        r = O.sample_row(x[i], O.RowParams(0.8, 20, 0.85, repetition_penalty=1.2), hist, float(u[i]))
+        assert PY.draw_ok(r.z, r.kept, float(u[i]), int(tok[i]))
+    tg = s.sample_token(x.to(dev), {"temperature": 0.0}, hist).cpu()
+    for i in range(B):
+        assert int(tg[i]) == O.sample_row(x[i], O.RowParams(0.0, repetition_penalty=1.2), hist).token
+
+
+def test_mirostat_entropy(dev):
+    from lps import Sampler
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn((1, 2000), generator=g) * 2
+    s = Sampler()
+    tok, prev = s.sample_mirostat_v2(x.to(dev), {"temperature": 0.9}, None, uniforms=torch.tensor([0.3], device=dev))
+    ref_tok, ref_prev, k = O.mirostat_v2_ref(x[0], 0.9, 5.0, 0.1, None, 0.3)
+    assert abs(prev - ref_prev) < 1e-4
+    assert 0 <= int(tok) < 2000
+
+
+# ------------------------------------------------------------ speculative --
+
+
+def test_verify_drafts_batched_exact(dev):
+    from lps import verify_drafts_batched
+    g = torch.Generator().manual_seed(16)
+    K, V = 300, 777
+    tp = torch.softmax(torch.randn(K, V, generator=g), -1)
+    q = torch.rand(K, generator=g) * 0.01
+    q[:5] = 0.0
+    t = torch.randint(0, V, (K,), generator=g)
+    u = torch.rand(K, generator=g) * 0.02
+    ref = O.verify_drafts_ref(tp, q, t, u)
+    big = torch.zeros(K, 2 * V)
+    big[:, ::2] = tp                                   # strided target_probs (stride_v = 2)
+    got = verify_drafts_batched(big[:, ::2].to(dev), q.to(dev), t.to(dev), u.to(dev)).cpu()
+    assert got.dtype == torch.int8 and torch.equal(got, ref)
+    assert 0 < int(ref.sum()) < K
+
+
+def _check_spec(sw, out, residual="target"):
+    n_ref, tok_ref, bits_ref, P_ref, Q_ref = O.spec_verify_ref(sw.target, sw.draft, sw.draft_tokens, sw.u_accept,
+                                                               sw.u_resample, sw.temperature, sw.top_p, residual)
+    P = out.p_target.cpu()
+    Q = out.q_draft.cpu()
+    bits = out.accept.cpu()
+    n = out.n_accepted.cpu()
+    tok = out.tokens.cpu()
+    B, k = sw.draft_tokens.shape
+    amb = 0
+    for b in range(B):
+        for i in range(k):
+            for a, r in ((P[b, i], P_ref[b, i]), (Q[b, i], Q_ref[b, i])):
+                assert abs(float(a) - float(r)) <= 1e-5 * abs(float(r)) + 1e-7, (b, i, float(a), float(r))
+            if int(bits[b, i]) != int(bits_ref[b, i]):
+                ratio = min(float(P_ref[b, i]) / max(float(Q_ref[b, i]), 1e-9), 1.0)
+                assert abs(float(sw.u_accept[b, i]) - ratio) < 1e-5
+                amb += 1
+        j = k if bits[b].all() else int(torch.nonzero(bits[b] == 0)[0])
+        assert int(n[b]) == j
+        assert tok[b, :j].tolist() == sw.draft_tokens[b, :j].tolist()
+        assert (tok[b, j + 1:] == -1).all()
+        if sw.temperature <= 0:
+            assert int(tok[b, j]) == int(torch.argmax(sw.target[b, j]))
+        elif residual == "target" and int(n[b]) == int(n_ref[b]):
+            z = O.apply_top_p((sw.target[b, j] / sw.temperature).reshape(1, -1), sw.top_p).reshape(-1)
+            kept = torch.isfinite(z).numpy()
+            assert PY.draw_ok(sw.target[b, j] / sw.temperature, kept, float(sw.u_resample[b, j]), int(tok[b, j]))
+    return amb
+
+
+def test_c4_spec_verify_full_size(dev):
+    from lps import spec_verify
+    sw = W.c4()
+    out = spec_verify(sw.target.to(dev), sw.draft.to(dev), sw.draft_tokens.to(dev), sw.u_accept.to(dev),
+                      sw.u_resample.to(dev), sw.temperature, sw.top_p)
+    torch.cuda.synchronize()
+    assert (out.status.cpu() == 0).all()
+    amb = _check_spec(sw, out)
+    _print(f"c4 spec: accepted={out.n_accepted.cpu().tolist()} ambiguous={amb}")
+
+
+def test_spec_verify_greedy_and_leviathan(dev):
+    from lps import spec_verify
+    sw = W.c4(B=8, V=4000, temperature=0.0)
+    out = spec_verify(sw.target.to(dev), sw.draft.to(dev), sw.draft_tokens.to(dev), sw.u_accept.to(dev),
+                      sw.u_resample.to(dev), 0.0, 1.0)
+    torch.cuda.synchronize()
+    _check_spec(sw, out)
+    sw = W.c4(B=8, V=4000, temperature=1.0, top_p=0.9)
+    out = spec_verify(sw.target.to(dev), sw.draft.to(dev), sw.draft_tokens.to(dev), sw.u_accept.to(dev),
+                      sw.u_resample.to(dev), 1.0, 0.9, residual="leviathan")
+    torch.cuda.synchronize()
+    _check_spec(sw, out, residual="leviathan")
+    tok = out.tokens.cpu()
+    n = out.n_accepted.cpu()
+    for b in range(8):
+        j = int(n[b])
+        if j < 4:
+            tp = O.spec_probs_row(sw.target[b, j], 1.0, 0.9).double()
+            dp = O.spec_probs_row(sw.draft[b, j], 1.0, 0.9).double()
+            assert float(tp[int(tok[b, j])] - dp[int(tok[b, j])]) > -1e-6   # drawn where p > q
