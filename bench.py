@@ -71,6 +71,10 @@ def build_args(w, dev, logits_dev, out, lib_mod):
         a.top_logprobs = out["tl"].data_ptr()
         a.top_ids = out["ti"].data_ptr()
         a.n_top = w.n_top
+    a.flags = out.get("flags", 0)
+    if out.get("ws") is not None:
+        a.workspace = out["ws"].data_ptr()
+        a.workspace_bytes = out["ws"].numel()
     return a
 
 
@@ -111,6 +115,7 @@ def main():
     ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c3", "c3f", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sampler shards rows across "
@@ -148,6 +153,9 @@ def main():
         "tl": torch.empty((B, max(w.n_top, 1)), dtype=torch.float32, device=dev),
         "ti": torch.empty((B, max(w.n_top, 1)), dtype=torch.int64, device=dev),
     }
+    io["flags"] = 1 if args.generic else 0
+    wsb = lib.lps_workspace_bytes(B, w.V, io["flags"])
+    io["ws"] = torch.zeros((max(wsb, 1),), dtype=torch.uint8, device=dev) if wsb else None
     arglist = [build_args(w, dev, b, io, lib) for b in bufs]
     extra = (B * 4 + B * w.n_top * 12) if w.logprobs else 0
     abytes = alg_bytes(w, extra)
@@ -221,7 +229,8 @@ def main():
                         "c5": "c5: B=512, V=151936 fp16, half greedy, half T 0.9/k 40/p 0.92, rep 1.05 over "
                               "1024 ids/row, chosen + top-20 logprobs"}[args.config],
            "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
-           "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes}
+           "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes,
+           "kernel": "gen_row_kernel" if args.generic else "fast_kernel"}
     line = {
         "metric": METRIC if args.config == "c2" else f"sampled rows/sec ({args.config})",
         "value": round(rows_s, 1),

@@ -62,6 +62,11 @@ enum {
 #define LPS_MAX_TOP_LOGPROBS 64
 #define LPS_MAX_HISTORY_DISTINCT 1536
 
+/* lps_sample_args.flags */
+enum {
+  LPS_FLAG_GENERIC = 1     /* use the general one-workgroup-per-row kernel only */
+};
+
 /* Residual used by lps_spec_verify on the first rejected position. */
 enum {
   LPS_RESIDUAL_TARGET = 0,     /* reference: resample the target distribution (speculative.py:150-157) */
@@ -133,7 +138,17 @@ typedef struct lps_sample_args {
   int32_t* kept_ties;             /* int32 [R] or NULL (-1 = every id at the cut) */
   int32_t* kept_count;            /* int32 [R] or NULL */
 
-  /* caller-owned scratch, lps_workspace_bytes() bytes (may be NULL when 0) */
+  /* optional: which path finished each row (0 = multi-workgroup fast path,
+   * 1 = general one-workgroup-per-row algorithm), int32 [R] or NULL */
+  int32_t* row_path;
+
+  /* LPS_FLAG_* */
+  int32_t flags;
+
+  /* caller-owned scratch of lps_workspace_bytes() bytes, zero-filled before
+   * its first use and then reused as is (every launch leaves it ready for
+   * the next); NULL selects the general one-workgroup-per-row kernel.  Calls
+   * that overlap in time must not share a workspace. */
   void* workspace;
   size_t workspace_bytes;
 } lps_sample_args;

@@ -3,6 +3,7 @@
 // mutable state.
 #include <hip/hip_runtime.h>
 
+#include "lps_fast_kernel.h"
 #include "lps_generic.h"
 #include "lps_spec.h"
 
@@ -38,6 +39,121 @@ bool vec_ok(const void* base, int dtype, int V, int rows_inner, int64_t so, int6
 }
 
 bool dtype_ok(int d) { return d == LPS_DTYPE_F32 || d == LPS_DTYPE_BF16 || d == LPS_DTYPE_F16; }
+
+size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// Fast-path workspace: per-row counters, row status, chunk summaries,
+// histograms and candidates, every row's region a whole number of 128-byte
+// lines.
+struct FastWs {
+  uint32_t* counters;
+  int32_t* status;
+  ChunkSum1* sum1;
+  ChunkSum2* sum2;
+  float* hist;
+  uint2* cands;
+  int64_t s_stride, h_stride, c_stride;
+  size_t bytes;
+};
+
+// Rows per fast launch; larger batches are split.  The counter region has this
+// fixed size at offset 0, so a workspace reused for any (rows, vocab) keeps its
+// counters apart from the data regions (the counters must stay zero between
+// launches; every launch leaves them zero).
+constexpr int FAST_MAX_ROWS = 8192;
+
+FastWs fast_layout(void* base, int R, int V) {
+  FastWs w{};
+  const int G = (V + FCH - 1) / FCH;
+  if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
+  w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
+  w.h_stride = (int64_t)round_up((size_t)G * (HB + HU + 2), 32);     // floats
+  w.c_stride = (int64_t)G * PUBCAP;                                  // uint2, multiple of 16
+  size_t off = 0;
+  char* p = reinterpret_cast<char*>(base);
+  w.counters = reinterpret_cast<uint32_t*>(p + off); off = (size_t)FAST_MAX_ROWS * 128;
+  w.status = reinterpret_cast<int32_t*>(p + off); off = round_up(off + (size_t)R * 4, 256);
+  w.sum1 = reinterpret_cast<ChunkSum1*>(p + off); off = round_up(off + (size_t)R * w.s_stride * sizeof(ChunkSum1), 256);
+  w.sum2 = reinterpret_cast<ChunkSum2*>(p + off); off = round_up(off + (size_t)R * w.s_stride * sizeof(ChunkSum2), 256);
+  w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * w.h_stride * 4, 256);
+  w.cands = reinterpret_cast<uint2*>(p + off); off = round_up(off + (size_t)R * w.c_stride * 8, 256);
+  w.bytes = off;
+  return w;
+}
+
+template <int DT, int VEC>
+hipError_t launch_fast(const FParams& F, int rows_pad, hipStream_t s) {
+  hipLaunchKernelGGL((fast_kernel<DT, VEC>), dim3((unsigned)(rows_pad * F.G)), dim3(FT), 0, s, F);
+  return hipGetLastError();
+}
+
+hipError_t dispatch_fast(int dtype, bool vec, const FParams& F, int rows_pad, hipStream_t s) {
+  switch (dtype) {
+    case LPS_DTYPE_F32: return vec ? launch_fast<LPS_DTYPE_F32, 4>(F, rows_pad, s) : launch_fast<LPS_DTYPE_F32, 1>(F, rows_pad, s);
+    case LPS_DTYPE_BF16: return vec ? launch_fast<LPS_DTYPE_BF16, 8>(F, rows_pad, s) : launch_fast<LPS_DTYPE_BF16, 1>(F, rows_pad, s);
+    default: return vec ? launch_fast<LPS_DTYPE_F16, 8>(F, rows_pad, s) : launch_fast<LPS_DTYPE_F16, 1>(F, rows_pad, s);
+  }
+}
+
+// Per-row pointers of a row block starting at row r0 (a multiple of rows_inner).
+KParams row_block(const KParams& P, int r0, int nr, int es) {
+  KParams B = P;
+  const int64_t g0 = r0 / P.rows_inner;
+  B.logits = reinterpret_cast<const char*>(P.logits) + es * g0 * P.stride_outer;
+  B.R = nr;
+  auto f = [&](const float* p) { return p ? p + r0 : p; };
+  B.temperature = f(P.temperature); B.top_p = f(P.top_p); B.min_p = f(P.min_p); B.typical_p = f(P.typical_p);
+  B.rep = f(P.rep); B.pres = f(P.pres); B.freq = f(P.freq); B.uniforms = f(P.uniforms);
+  B.top_k = P.top_k ? P.top_k + r0 : nullptr;
+  B.history = P.history ? P.history + (int64_t)r0 * P.history_stride : nullptr;
+  B.history_len = P.history_len ? P.history_len + r0 : nullptr;
+  B.query_tokens = P.query_tokens ? P.query_tokens + g0 * P.query_inner : nullptr;
+  B.query_prob = P.query_prob ? P.query_prob + r0 : nullptr;
+  B.tokens = P.tokens + r0;
+  B.chosen_logprob = P.chosen_logprob ? P.chosen_logprob + r0 : nullptr;
+  B.top_logprobs = P.top_logprobs ? P.top_logprobs + (int64_t)r0 * P.n_top : nullptr;
+  B.top_ids = P.top_ids ? P.top_ids + (int64_t)r0 * P.n_top : nullptr;
+  B.entropy = P.entropy ? P.entropy + r0 : nullptr;
+  B.row_status = P.row_status ? P.row_status + r0 : nullptr;
+  B.kept_cut = P.kept_cut ? P.kept_cut + r0 : nullptr;
+  B.kept_ties = P.kept_ties ? P.kept_ties + r0 : nullptr;
+  B.kept_count = P.kept_count ? P.kept_count + r0 : nullptr;
+  B.row_path = P.row_path ? P.row_path + r0 : nullptr;
+  B.plans = P.plans ? P.plans + r0 : nullptr;
+  return B;
+}
+
+// Runs the fast kernel (rows it cannot finish exactly fall back to the general
+// algorithm inside it), or the general kernel when asked or without workspace.
+hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws_bytes, int flags, hipStream_t s) {
+  const FastWs need = fast_layout(nullptr, P.R, P.V);
+  if ((flags & LPS_FLAG_GENERIC) || !ws || ws_bytes < need.bytes) return dispatch_gen(dtype, vec, P, s);
+  if (P.R > FAST_MAX_ROWS) {
+    const int blk = FAST_MAX_ROWS / P.rows_inner * P.rows_inner;
+    const int es = dtype == LPS_DTYPE_F32 ? 4 : 2;
+    for (int r0 = 0; r0 < P.R; r0 += blk) {
+      const int nr = P.R - r0 < blk ? P.R - r0 : blk;
+      hipError_t e = run_sample(row_block(P, r0, nr, es), dtype, vec, ws, ws_bytes, flags, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  const FastWs w = fast_layout(ws, P.R, P.V);
+  FParams F{};
+  F.k = P;
+  F.G = (P.V + FCH - 1) / FCH;
+  F.counters = w.counters;
+  F.status = w.status;
+  F.sum1 = w.sum1;
+  F.sum2 = w.sum2;
+  F.hist = w.hist;
+  F.cands = w.cands;
+  F.s_stride = w.s_stride;
+  F.h_stride = w.h_stride;
+  F.c_stride = w.c_stride;
+  const int rows_pad = (P.R + 7) / 8 * 8;
+  return dispatch_fast(dtype, vec, F, rows_pad, s);
+}
 
 KParams neutral_params() {
   KParams P{};
@@ -98,8 +214,8 @@ const char* lps_status_string(int code) {
 }
 
 size_t lps_workspace_bytes(int num_rows, int vocab, int flags) {
-  (void)num_rows; (void)vocab; (void)flags;
-  return 0;
+  if (num_rows <= 0 || vocab < 1 || vocab > kMaxVocab || (flags & LPS_FLAG_GENERIC)) return 0;
+  return fast_layout(nullptr, num_rows, vocab).bytes;
 }
 
 size_t lps_spec_workspace_bytes(int batch, int k, int vocab) {
@@ -153,8 +269,12 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   P.kept_ties = a->kept_ties;
   P.kept_count = a->kept_count;
   P.plans = nullptr;
+  P.only_status = nullptr;
+  P.row_path = a->row_path;
+  if (a->workspace && a->workspace_bytes < lps_workspace_bytes(a->num_rows, a->vocab, a->flags)) return LPS_EWORKSPACE;
   const bool vec = vec_ok(a->logits, a->dtype, a->vocab, a->rows_inner, a->stride_outer, a->stride_inner);
-  hipError_t e = dispatch_gen(a->dtype, vec, P, reinterpret_cast<hipStream_t>(stream));
+  hipError_t e = run_sample(P, a->dtype, vec, a->workspace, a->workspace_bytes, a->flags,
+                            reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
 }
 

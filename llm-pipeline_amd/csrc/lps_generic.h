@@ -21,8 +21,8 @@
 
 namespace lps {
 
-constexpr int GEN_NT = 1024;
-constexpr int GEN_NW = GEN_NT / 64;
+constexpr int GEN_NT = 1024;            // threads of the general kernel (the code runs with any multiple of 64 up to it)
+constexpr int GEN_NW = GEN_NT / 64;     // scratch sized for the largest block
 constexpr int HASH_CAP = 2048;     // history hash slots (power of two)
 constexpr int BLOOM_WORDS = 2048;  // 65536-bit bloom filter over token ids
 constexpr int NBINS = 2048;        // radix digit bins (11 bits)
@@ -63,6 +63,8 @@ struct KParams {
   int32_t* kept_ties;
   int32_t* kept_count;
   RowPlan* plans;
+  const int32_t* only_status;  // non-null: process only rows whose entry has bit 8 (deferred by the fast kernel)
+  int32_t* row_path;           // optional: 0 fast kernel, 1 general kernel
 };
 
 struct GenShared {
@@ -123,15 +125,14 @@ struct PenCtx {
 };
 
 // ---------------------------------------------------------------------------
-// Block helpers (GEN_NT threads).
+// Block helpers (blockDim.x threads, a multiple of 64, at most GEN_NT).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t gblock_max_u64(uint64_t v, GenShared& S) {
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = S.red64[0];
-#pragma unroll
-  for (int i = 1; i < GEN_NW; i++) r = S.red64[i] > r ? S.red64[i] : r;
+  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = S.red64[i] > r ? S.red64[i] : r;
   __syncthreads();
   return r;
 }
@@ -140,8 +141,7 @@ __device__ __forceinline__ uint64_t gblock_sum_u64(uint64_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = 0;
-#pragma unroll
-  for (int i = 0; i < GEN_NW; i++) r += S.red64[i];
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.red64[i];
   __syncthreads();
   return r;
 }
@@ -150,8 +150,7 @@ __device__ __forceinline__ uint32_t gblock_min_u32(uint32_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
   __syncthreads();
   uint32_t r = S.red32[0];
-#pragma unroll
-  for (int i = 1; i < GEN_NW; i++) r = S.red32[i] < r ? S.red32[i] : r;
+  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = S.red32[i] < r ? S.red32[i] : r;
   __syncthreads();
   return r;
 }
@@ -160,8 +159,7 @@ __device__ __forceinline__ uint32_t gblock_sum_u32(uint32_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
   __syncthreads();
   uint32_t r = 0;
-#pragma unroll
-  for (int i = 0; i < GEN_NW; i++) r += S.red32[i];
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.red32[i];
   __syncthreads();
   return r;
 }
@@ -170,8 +168,7 @@ __device__ __forceinline__ double gblock_sum_f64(double v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.redd[threadIdx.x >> 6] = v;
   __syncthreads();
   double r = 0;
-#pragma unroll
-  for (int i = 0; i < GEN_NW; i++) r += S.redd[i];
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.redd[i];
   __syncthreads();
   return r;
 }
@@ -183,8 +180,7 @@ __device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch) {
   if ((threadIdx.x & 63) == 63) scratch[w] = inc;
   __syncthreads();
   T off = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < GEN_NW; i++) {
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) {
     T s = scratch[i];
     off += (i < w) ? s : (T)0;
     tot += s;
@@ -199,7 +195,7 @@ __device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch) {
 // ---------------------------------------------------------------------------
 template <int DT, int VEC, typename F>
 __device__ __forceinline__ void row_pass(const void* row, int V, const PenCtx& pc, F&& f) {
-  for (int64_t i0 = (int64_t)threadIdx.x * VEC; i0 < V; i0 += (int64_t)GEN_NT * VEC) {
+  for (int64_t i0 = (int64_t)threadIdx.x * VEC; i0 < V; i0 += (int64_t)(int)blockDim.x * VEC) {
     float x[VEC];
     loadv<DT, VEC>(row, i0, x);
     pc.apply<VEC>(i0, x);
@@ -219,31 +215,33 @@ __device__ __forceinline__ uint32_t lvl_himask(int l) { return l == 0 ? 0u : (l 
 // Writes the bin to S.misc[0] and the "above" amounts to S.misc64[0..1].
 __device__ void find_bin(GenShared& S, int nb, bool by_mass, uint64_t target_or_limit, uint64_t base) {
   if (threadIdx.x == 0) { S.misc[0] = -1; S.misc64[0] = 0; S.misc64[1] = 0; }
-  // thread t owns descending positions r = 2t, 2t+1 (bin = nb-1-r)
-  uint64_t m0 = 0, m1 = 0;
-  uint32_t c0 = 0, c1 = 0;
-  const int r0 = 2 * threadIdx.x, r1 = r0 + 1;
-  if (r0 < nb) { c0 = S.u.h.cnt[nb - 1 - r0]; m0 = S.u.h.mass[nb - 1 - r0]; }
-  if (r1 < nb) { c1 = S.u.h.cnt[nb - 1 - r1]; m1 = S.u.h.mass[nb - 1 - r1]; }
-  uint64_t v = by_mass ? (m0 + m1) : (uint64_t)(c0 + c1);
+  // thread t owns descending positions r = t*per .. t*per+per-1 (bin = nb-1-r)
+  const int per = nb / (int)blockDim.x > 0 ? nb / (int)blockDim.x : 1;
+  const int r0 = threadIdx.x * per;
+  uint64_t v = 0;
+  for (int q = 0; q < per; q++) {
+    const int rr = r0 + q;
+    if (rr < nb) v += by_mass ? S.u.h.mass[nb - 1 - rr] : (uint64_t)S.u.h.cnt[nb - 1 - rr];
+  }
   uint64_t tot;
-  uint64_t ex = gblock_excl_scan<uint64_t>(v, &tot, S.red64);
-  uint64_t a0 = by_mass ? m0 : c0, a1 = by_mass ? m1 : c1;
-  if (by_mass) {
-    uint64_t lim = target_or_limit;
-    if (r0 < nb && base + ex <= lim && lim < base + ex + a0) { S.misc[0] = nb - 1 - r0; S.misc64[0] = ex; }
-    else if (r1 < nb && base + ex + a0 <= lim && lim < base + ex + a0 + a1) { S.misc[0] = nb - 1 - r1; S.misc64[0] = ex + a0; }
-  } else {
-    uint64_t tg = target_or_limit;
-    if (r0 < nb && ex < tg && tg <= ex + a0) { S.misc[0] = nb - 1 - r0; S.misc64[0] = ex; }
-    else if (r1 < nb && ex + a0 < tg && tg <= ex + a0 + a1) { S.misc[0] = nb - 1 - r1; S.misc64[0] = ex + a0; }
+  uint64_t a = gblock_excl_scan<uint64_t>(v, &tot, S.red64);
+  for (int q = 0; q < per; q++) {
+    const int rr = r0 + q;
+    if (rr >= nb) break;
+    const uint64_t c = by_mass ? S.u.h.mass[nb - 1 - rr] : (uint64_t)S.u.h.cnt[nb - 1 - rr];
+    if (by_mass) {
+      if (base + a <= target_or_limit && target_or_limit < base + a + c) { S.misc[0] = nb - 1 - rr; S.misc64[0] = a; }
+    } else {
+      if (a < target_or_limit && target_or_limit <= a + c) { S.misc[0] = nb - 1 - rr; S.misc64[0] = a; }
+    }
+    a += c;
   }
   __syncthreads();
 }
 
 template <int DT, int VEC>
 __device__ void clear_hist(GenShared& S) {
-  for (int i = threadIdx.x; i < NBINS; i += GEN_NT) { S.u.h.cnt[i] = 0; S.u.h.mass[i] = 0; }
+  for (int i = threadIdx.x; i < NBINS; i += (int)blockDim.x) { S.u.h.cnt[i] = 0; S.u.h.mass[i] = 0; }
   __syncthreads();
 }
 
@@ -325,9 +323,7 @@ __device__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShar
 // The kernel.
 // ---------------------------------------------------------------------------
 template <int DT, int VEC>
-__global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
-  __shared__ GenShared S;
-  const int r = blockIdx.x;
+__device__ void gen_row(const KParams& P, const int r, GenShared& S) {
   const int tid = threadIdx.x;
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   const void* row = reinterpret_cast<const char*>(P.logits) +
@@ -352,12 +348,12 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
   int hlen = (P.history && P.history_len) ? P.history_len[r] : 0;
   if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;  // never past the row
   const bool pen = hlen > 0 && (rep != 1.0f || pres != 0.0f || freq != 0.0f);
-  for (int i = tid; i < BLOOM_WORDS; i += GEN_NT) S.bloom[i] = 0u;
-  for (int i = tid; i < HASH_CAP; i += GEN_NT) { S.hkey[i] = -1; S.hcnt[i] = 0; }
+  for (int i = tid; i < BLOOM_WORDS; i += (int)blockDim.x) S.bloom[i] = 0u;
+  for (int i = tid; i < HASH_CAP; i += (int)blockDim.x) { S.hkey[i] = -1; S.hcnt[i] = 0; }
   __syncthreads();
   if (pen) {
     const int32_t* h = P.history + (int64_t)r * P.history_stride;
-    for (int j = tid; j < hlen; j += GEN_NT) {
+    for (int j = tid; j < hlen; j += (int)blockDim.x) {
       const int id = h[j];
       if (id < 0 || id >= V) continue;
       uint32_t s = hash_id(id);
@@ -372,7 +368,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
   __syncthreads();
   {
     uint32_t used = 0;
-    for (int i = tid; i < HASH_CAP; i += GEN_NT) used += S.hkey[i] >= 0 ? 1u : 0u;
+    for (int i = tid; i < HASH_CAP; i += (int)blockDim.x) used += S.hkey[i] >= 0 ? 1u : 0u;
     used = gblock_sum_u32(used, S);
     if (used > LPS_MAX_HISTORY_DISTINCT) status |= LPS_ROW_HISTORY_OVERFLOW;
   }
@@ -529,7 +525,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
     uint32_t tie_run = 0, nkept = 0;
     uint64_t qm = 0;
     int qk = 0;
-    for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+    for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       float x[VEC];
       uint32_t k[VEC];
@@ -576,7 +572,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
     uint32_t tie_run = 0;
     if (tid == 0) S.misc[1] = -1;
     __syncthreads();
-    for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+    for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       float x[VEC];
       uint32_t k[VEC];
@@ -642,7 +638,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
       if (tid == 0) S.u.lst.n = 0;
       __syncthreads();
       uint32_t tie_run = 0;
-      for (int64_t tile = 0; tile < V; tile += (int64_t)GEN_NT * VEC) {
+      for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
         const int64_t i0 = tile + (int64_t)tid * VEC;
         float x[VEC];
         uint32_t k[VEC];
@@ -683,7 +679,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
         P.top_logprobs[(int64_t)r * P.n_top + rank] = need_full ? (float)((double)__fsub_rn(z, zmax) - lnZ) : NAN;
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + rank] = ii;
       }
-      for (int j = n + tid; j < P.n_top; j += GEN_NT) {
+      for (int j = n + tid; j < P.n_top; j += (int)blockDim.x) {
         P.top_logprobs[(int64_t)r * P.n_top + j] = -INFINITY;
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + j] = -1;
       }
@@ -699,6 +695,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
     if (P.kept_cut) P.kept_cut[r] = key_lo <= kNegInfKey ? -INFINITY : key2f(key_lo);  // key 0: nothing cut
     if (P.kept_ties) P.kept_ties[r] = n_tie == kNoTie ? -1 : (int32_t)n_tie;
     if (P.kept_count) P.kept_count[r] = (int32_t)kept_n;
+    if (P.row_path) P.row_path[r] = 1;
     if (P.plans) {
       RowPlan pl;
       pl.zmax = zmax; pl.T = Te; pl.key_lo = key_lo; pl.n_tie = n_tie; pl.Zf = Zf;
@@ -706,6 +703,14 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
       P.plans[r] = pl;
     }
   }
+}
+
+template <int DT, int VEC>
+__global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
+  __shared__ GenShared S;
+  const int r = blockIdx.x;
+  if (P.only_status && !(P.only_status[r] & 8)) return;
+  gen_row<DT, VEC>(P, r, S);
 }
 
 }  // namespace lps

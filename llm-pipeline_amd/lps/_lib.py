@@ -30,6 +30,8 @@ LPS_ROW_HISTORY_OVERFLOW = 4
 LPS_MAX_TOP_LOGPROBS = 64
 LPS_MAX_HISTORY_DISTINCT = 1536
 
+LPS_FLAG_GENERIC = 1
+
 LPS_RESIDUAL_TARGET = 0
 LPS_RESIDUAL_LEVIATHAN = 1
 
@@ -53,6 +55,8 @@ class SampleArgs(ctypes.Structure):
         ("tokens", _vp), ("chosen_logprob", _vp), ("top_logprobs", _vp), ("top_ids", _vp), ("n_top", _i32),
         ("entropy", _vp), ("row_status", _vp), ("skip_draw", _i32),
         ("kept_cut", _vp), ("kept_ties", _vp), ("kept_count", _vp),
+        ("row_path", _vp),
+        ("flags", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 

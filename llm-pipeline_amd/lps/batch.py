@@ -9,6 +9,7 @@ once per row (``src/llm_pipeline/inference/continuous_batching.py:394-401``);
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass, fields
 from typing import Iterable, Optional, Sequence
 
@@ -64,6 +65,24 @@ class SamplingParams:
         )
 
 
+_WS_LOCK = threading.Lock()
+_WS = {}
+
+
+def workspace_for(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled scratch for the fast kernel, cached per (device, stream).
+    Every launch leaves it ready for the next, so it is filled only when it is
+    created; launches on one stream never overlap, so they may share it."""
+    dev = torch.device(device)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    with _WS_LOCK:
+        t = _WS.get(key)
+        if t is None or t.numel() < nbytes:
+            t = torch.zeros((max(nbytes, 1 << 20),), dtype=torch.uint8, device=dev)
+            _WS[key] = t
+        return t
+
+
 @dataclass
 class SampleOutput:
     tokens: torch.Tensor                       # int64 [B]
@@ -76,6 +95,7 @@ class SampleOutput:
     kept_cut: Optional[torch.Tensor] = None         # float32 [B]: scaled logit at the cut
     kept_ties: Optional[torch.Tensor] = None        # int32 [B]: kept ids at the cut (-1 = all)
     kept_count: Optional[torch.Tensor] = None       # int32 [B]
+    row_path: Optional[torch.Tensor] = None         # int32 [B]: 0 fast kernel, 1 general kernel
 
 
 def pad_histories(histories: Iterable[Sequence[int]], device) -> tuple:
@@ -95,10 +115,17 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
                 histories: Optional[torch.Tensor] = None, history_lengths: Optional[torch.Tensor] = None,
                 logprobs: bool = False, top_logprobs: int = 0, entropy: bool = False,
                 query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
-                generator: Optional[torch.Generator] = None) -> SampleOutput:
+                path: str = "auto", generator: Optional[torch.Generator] = None) -> SampleOutput:
     """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
-    synchronised and ``status`` is returned as a device tensor."""
+    synchronised and ``status`` is returned as a device tensor.
+
+    ``path``: ``"auto"`` runs the multi-workgroup kernel (a row it cannot
+    finish exactly falls back to the general algorithm inside it; ``row_path``
+    reports which); ``"generic"`` runs only the general
+    one-workgroup-per-row kernel."""
+    if path not in ("auto", "generic"):
+        raise ValueError("path must be 'auto' or 'generic'")
     D.require_device(logits, "logits")
     if logits.dim() != 2:
         raise ValueError(f"logits must be [B, V]; got {tuple(logits.shape)}")
@@ -118,6 +145,7 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     tokens = torch.empty((B,), dtype=torch.int64, device=dev)
     status = torch.empty((B,), dtype=torch.int32, device=dev)
     out = SampleOutput(tokens, status)
+    out.row_path = torch.empty((B,), dtype=torch.int32, device=dev)
     if logprobs:
         out.chosen_logprob = torch.empty((B,), dtype=torch.float32, device=dev)
     if top_logprobs:
@@ -175,10 +203,12 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_cut = D.ptr(out.kept_cut)
     a.kept_ties = D.ptr(out.kept_ties)
     a.kept_count = D.ptr(out.kept_count)
-    ws_bytes = _lib.load().lps_workspace_bytes(B, V, 0)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
+    a.row_path = D.ptr(out.row_path)
+    a.flags = 0 if path == "auto" else _lib.LPS_FLAG_GENERIC
+    ws_bytes = _lib.load().lps_workspace_bytes(B, V, a.flags)
+    ws = workspace_for(dev, ws_bytes) if ws_bytes else None
     a.workspace = D.ptr(ws)
-    a.workspace_bytes = ws_bytes
+    a.workspace_bytes = ws.numel() if ws is not None else 0
     with torch.cuda.device(dev):
         rc = _lib.load().lps_sample(ctypes.byref(a), D.stream_of(dev))
     _lib.check(rc, "lps_sample")

@@ -121,13 +121,13 @@ def check_rows(w, out, rows=None, report: RowReport = None, lp=False) -> RowRepo
     return report
 
 
-def run_workload(w, dev, **kw):
+def run_workload(w, dev, path="auto", **kw):
     from lps import SamplingParams, sample_rows
     p = SamplingParams(w.temperature.to(dev), w.top_k.to(dev), w.top_p.to(dev), w.min_p.to(dev),
                        w.typical_p.to(dev), w.rep.to(dev), w.pres.to(dev), w.freq.to(dev))
     hist = w.histories.to(dev) if w.histories is not None else None
     hl = w.hist_len.to(dev) if w.hist_len is not None else None
     out = sample_rows(w.logits.to(dev), p, w.uniforms.to(dev), histories=hist, history_lengths=hl,
-                      logprobs=w.logprobs, top_logprobs=w.n_top, kept_set=True, **kw)
+                      logprobs=w.logprobs, top_logprobs=w.n_top, kept_set=True, path=path, **kw)
     torch.cuda.synchronize(dev)
     return out

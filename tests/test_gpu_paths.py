@@ -1,0 +1,59 @@
+"""The multi-workgroup fast kernel against the oracle and against the general
+kernel, on the BASELINE.json configurations: both paths must meet the parity
+bar, and the fast path must finish the rows of the benchmark configurations
+itself (rows it defers are finished by the general kernel)."""
+
+import pytest
+import torch
+
+from tests import parity as PY
+from tests import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _paths(w, dev, rows=None, lp=False):
+    fast = PY.run_workload(w, dev, path="auto")
+    gen = PY.run_workload(w, dev, path="generic")
+    rf = PY.check_rows(w, fast, rows=rows, lp=lp)
+    rg = PY.check_rows(w, gen, rows=rows, lp=lp)
+    nfast = int((fast.row_path.cpu() == 0).sum())
+    same = int((fast.tokens == gen.tokens).sum())
+    print(f"{w.name}: fast-path rows {nfast}/{w.B}; tokens equal to the general kernel {same}/{w.B}; "
+          f"fast {rf}; general {rg}", flush=True)
+    return fast, gen, nfast
+
+
+def test_paths_c2(dev):
+    w = W.c2()
+    fast, gen, nfast = _paths(w, dev)
+    assert nfast == w.B
+
+
+def test_paths_c1(dev):
+    for g in (False, True):
+        w = W.c1(greedy=g)
+        fast, gen, nfast = _paths(w, dev)
+        assert nfast == 1
+
+
+@pytest.mark.parametrize("flat", [False, True])
+def test_paths_c3(dev, flat):
+    w = W.c3(B=16, flat=flat)
+    _paths(w, dev)
+
+
+def test_paths_c5(dev):
+    w = W.c5(B=32)
+    fast, gen, nfast = _paths(w, dev, lp=True)
+    assert nfast == w.B
+
+
+def test_fast_small_and_ragged(dev):
+    """Vocabularies below one chunk, exactly one chunk, ragged last chunk, scalar loads."""
+    from tests.test_gpu_parity import _small
+    for V in (5, 777, 8192, 8193, 20011):
+        for dt in (torch.float32, torch.bfloat16):
+            w = _small(V, 16, dt, seed=V)
+            out = PY.run_workload(w, dev)
+            PY.check_rows(w, out)
