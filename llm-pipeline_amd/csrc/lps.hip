@@ -67,7 +67,7 @@ FastWs fast_layout(void* base, int R, int V) {
   const int G = (V + FCH - 1) / FCH;
   if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
   w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
-  w.h_stride = (int64_t)round_up((size_t)G * (HB + HU + 2), 32);     // floats
+  w.h_stride = (int64_t)round_up((size_t)G * HB, 32);                // floats
   w.c_stride = (int64_t)G * PUBCAP;                                  // uint2, multiple of 16
   size_t off = 0;
   char* p = reinterpret_cast<char*>(base);

@@ -1,34 +1,44 @@
 // Fast row sampler: every row is split into G chunks of 8192 logits, one
-// 256-thread workgroup per chunk, the chunk held in registers for the whole
-// kernel (the logits are read from HBM exactly once).
+// 256-thread workgroup per chunk, the chunk held in registers (the logits are
+// read from HBM once; only the chunk that holds the draw of a nucleus / pure
+// row is read a second time, by the row's finaliser, normally from the L2).
 //
 // Placement: workgroup ids are dispatched round-robin over the XCDs, so chunk
 // workgroups of a row are given ids congruent modulo 8.  They then share one
 // L2, and their partial results meet there: a workgroup publishes with plain
 // stores (write-through L1 -> L2), waits for them, and counts its arrival with
-// a global atomic; the last arrival of a row finalises it, reading the
-// partials with L1-bypassing loads.  No agent-scope release fence (an L2
-// write-back) is ever issued.
+// a global atomic; the last arrival of a row finalises it.  No agent-scope
+// release fence (an L2 write-back) is ever issued.  A row whose chunks were
+// not all seen on one XCD is finished by the general algorithm instead.
 //
 // Row modes (decided per row from its parameters):
 //   GREEDY  T <= 0: first argmax (plus logprobs).
-//   TOPK    0 < top_k <= FAST_KMAX: each chunk publishes its exact local
-//           top-k' (k' = max(k, n_top)) candidates; the finaliser selects the
-//           global k-th value, applies top-p / min-p / typical-p on the small
-//           kept set and draws from it.
+//   TOPK    0 < top_k <= FAST_KMAX: each chunk publishes a small superset of
+//           its local top-k' (k' = max(k, n_top)), found with per-wave ballot
+//           selection; the finaliser selects the global k-th value among the
+//           published candidates, applies top-p / min-p / typical-p on the
+//           small kept set and draws from it.
 //   PURE    top_k off and no other filter: no cut; the finaliser picks the
 //           chunk holding the draw from per-chunk masses and rescans it.
 //   NUCLEUS top_k off, top_p < 1: chunks publish a fine mass histogram, pass
-//           one intra-XCD barrier, derive the same global cut region, publish
-//           the candidates inside it plus their exact mass above it; the
-//           finaliser makes the exact cut and rescans the chunk holding the
-//           draw.
+//           one intra-XCD barrier, all derive the same cut region (the bins
+//           whose cumulative mass meets top_p within a tolerance band), and
+//           publish the candidates inside it plus their exact mass above it;
+//           the finaliser makes the exact cut by a mass-weighted radix select
+//           and rescans the chunk holding the draw.
 // A row the fast path cannot finish exactly (e.g. a flat row whose cut region
 // holds more candidates than fit, min-p / typical-p without top-k, top_k above
-// FAST_KMAX) is flagged LPS_ROW_DEFERRED and finished by the general kernel.
+// FAST_KMAX) is flagged LPS_ROW_DEFERRED and runs the general algorithm in the
+// same workgroup.
 #pragma once
 
 #include "lps_generic.h"
+#include "lps_wave.h"
+
+// Phase marks inside the fast kernel; empty unless a timing build defines it.
+#ifndef LPS_STAMP
+#define LPS_STAMP(i) ((void)0)
+#endif
 
 namespace lps {
 
@@ -37,30 +47,29 @@ constexpr int FW = FT / 64;             // waves per workgroup
 constexpr int FE = 32;                  // elements per thread
 constexpr int FCH = FT * FE;            // chunk size (8192)
 constexpr int FAST_KMAX = 256;          // largest top_k / top-N handled by the fast path
-constexpr int LCAP = 1024;              // local candidate list (per workgroup)
 constexpr int PUBCAP = 512;             // published candidates per chunk
+constexpr int FCPT = 16;                // finaliser candidates per thread (registers)
+constexpr int FCAP = FT * FCPT;         // finaliser candidate capacity (4096)
 constexpr int KEPTCAP = 512;            // finaliser kept list
 constexpr int HB = 256;                 // histogram bins per chunk (1/8 log2 unit each)
 constexpr int HS = 8;                   // bins per log2 unit
-constexpr int HU = HB / HS;             // histogram units (1 log2 unit each)
-constexpr int FHASH = 1024;             // per-chunk history hash slots
-constexpr int FHASH_MAX = 768;          // distinct ids a chunk table holds
-constexpr int FBITS = FCH / 32;         // per-chunk history bitmap words
+constexpr int SELD = 11;                // select digit bits
+constexpr int SELB = 1 << SELD;         // select histogram bins
+constexpr int HPF = 4;                  // history ids prefetched per thread
 constexpr int MAXG = 64;                // chunks per row (V <= 524287)
 
 enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEFER = 4 };
 enum { CF_OVERFLOW = 1, CF_HISTORY = 2, CF_SPLIT = 4, CF_REGION = 8 };
-constexpr int32_t LPS_ROW_DEFERRED = 8;  // internal: finished by the general kernel
+constexpr int32_t LPS_ROW_DEFERRED = 8;  // internal: finished by the general algorithm
 
 struct ChunkSum1 {   // published before the barrier / handoff
-  uint32_t mkey;     // max key of the penalised logits of the chunk
-  int32_t amax;      // its first index
-  float zsum;        // sum over the chunk of exp2((x - xmax_chunk) * c)
+  uint32_t mkey;     // max key of the penalised logits of the chunk (NaN -> 0xFFFFFFFF)
+  int32_t amax;      // greedy rows: first index of that key
+  float zsum;        // sum over the chunk of exp2(x c - xmax_chunk c), c = log2(e) / T
   int32_t btop;      // histogram top bin (absolute) of the chunk
-  uint32_t ninf;     // -inf logits in the chunk
+  uint32_t ninf;     // -inf logits in the chunk (when counted)
   uint32_t flags;    // CF_*
-  uint32_t xcc;      // XCD the chunk ran on
-  uint32_t pad;
+  uint32_t pad[2];
 };
 struct ChunkSum2 {   // published at the handoff
   uint32_t ncand;    // candidates published
@@ -77,64 +86,52 @@ struct FParams {
   int32_t* status;     // [R]
   ChunkSum1* sum1;     // row r at sum1 + r * s_stride
   ChunkSum2* sum2;
-  float* hist;         // row r at hist + r * h_stride: G x (HB fine + HU unit) masses
-  uint2* cands;        // row r at cands + r * c_stride: G x PUBCAP (key, idx)
+  float* hist;         // row r at hist + r * h_stride: G x HB masses (chunk reference)
+  uint2* cands;        // row r at cands + r * c_stride: G x PUBCAP (x key, idx)
   int64_t s_stride, h_stride, c_stride;
 };
 
+// LDS.  The chunk phase and the finaliser never overlap in one workgroup.
 struct FShared {
-  int32_t hkey[FHASH];
-  uint32_t hcnt[FHASH / 2];  // two 16-bit counts per word
-  uint32_t bits[FBITS];
-  uint32_t rh[256];          // radix digit histogram
   union {
-    struct {                 // chunk phase
-      uint64_t hm[HB];       // fixed-point histogram masses (chunk reference)
-      uint32_t tmax[FT];
+    struct {                              // chunk phase
+      uint32_t hc[FCH / 2];               // history counts, two 16-bit counts per word
+      unsigned long long hm[HB];          // chunk mass histogram, fixed point
+      double scale[MAXG];                 // nucleus region: chunk -> row reference
+      int32_t btop[MAXG];
+    } c;
+    struct {                              // finaliser
       union {
         struct {
-          uint32_t lkey[LCAP];
-          int32_t lidx[LCAP];
-        } l;
-        struct {             // nucleus region search
-          double scale[MAXG];
-          int32_t btop[MAXG];
-          double zs[MAXG];
-          double um[HU + 2];
-          double bm[HS];
-        } n;
-      } v;
-    } c;
-    struct {                 // finaliser
-      uint32_t kkey[KEPTCAP];  // z keys
-      uint32_t kx[KEPTCAP];    // x keys
-      int32_t kidx[KEPTCAP];
-      uint64_t km[KEPTCAP];
-      int32_t kord[KEPTCAP];
-      int32_t iord[KEPTCAP];
-      uint64_t cum[KEPTCAP];
-      uint32_t cmk[MAXG];      // per-chunk max key
-      int32_t cam[MAXG];       // per-chunk argmax
-      float czs[MAXG];         // per-chunk zsum
-      uint32_t cnc[MAXG];      // per-chunk published candidates
-      uint32_t pre[MAXG];      // candidate prefix
-      uint32_t cfl[MAXG];
-      uint32_t cninf[MAXG];
-      uint32_t ctie[MAXG];     // kept ties in chunks before q
-      double scale[MAXG];      // chunk reference -> row reference
-      double keptm[MAXG];      // kept mass per chunk
-      double abv[MAXG];
-      uint32_t nab[MAXG];
-      unsigned long long keptf[MAXG];  // kept candidate mass per chunk (fixed point)
-      uint32_t keptc[MAXG];            // kept candidate count per chunk
+          uint32_t cnt[SELB];
+          unsigned long long mass[SELB];
+        } sel;                            // select histograms
+        struct {
+          uint32_t kkey[KEPTCAP];         // z keys
+          uint32_t kx[KEPTCAP];           // x keys
+          int32_t kidx[KEPTCAP];
+          unsigned long long km[KEPTCAP];
+          int32_t kord[KEPTCAP];          // sorted position -> slot
+          int32_t iord[KEPTCAP];          // index-order position -> slot
+          unsigned long long cum[KEPTCAP];
+        } k;                              // kept list
+        uint32_t hc[FCH / 2];             // rescan history counts
+      } x;
+      uint32_t pre[MAXG + 1];             // candidate prefix over chunks
+      double scale[MAXG];                 // chunk -> row reference
+      double keptm[MAXG];                 // kept mass per chunk
+      double abvm[MAXG];                  // nucleus: mass above the region per chunk
+      unsigned long long epre[MAXG];      // nucleus: kept candidate mass prefix at chunk starts
+      unsigned long long eend[MAXG];      // ... and after each chunk's last candidate
     } f;
   } u;
-  uint64_t r64[FW];
-  double rd[FW];
-  uint32_t r32[FW];
-  int32_t mi[16];
+  // cross-wave exchange slots (each slot is reused only after an intervening barrier)
+  uint64_t xa[FW], xb[FW];
+  double xd[FW], xe[FW];
+  uint32_t xc[FW], xf[FW], xg[FW], xh[FW];
+  double xv[FW][8];
+  int32_t mi[32];
   uint64_t m64[8];
-  float mf[8];
   double md[8];
 };
 
@@ -161,139 +158,42 @@ __device__ __forceinline__ uint32_t l2_fetch_add(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---------------------------------------------------------------------------
-// 256-thread block helpers.
+// 256-thread block helpers: wave results meet in one exchange slot, one barrier.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t fmax_u64(uint64_t v, FShared& S) {
-  v = wave_max(v);
-  if ((threadIdx.x & 63) == 0) S.r64[threadIdx.x >> 6] = v;
+template <typename T, typename Op>
+__device__ __forceinline__ T bcombine(T v, T* slot, Op op) {  // v wave-uniform
+  if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = v;
   __syncthreads();
-  uint64_t r = S.r64[0];
-#pragma unroll
-  for (int i = 1; i < FW; i++) r = S.r64[i] > r ? S.r64[i] : r;
-  __syncthreads();
-  return r;
+  return op(op(slot[0], slot[1]), op(slot[2], slot[3]));
 }
-__device__ __forceinline__ uint64_t fsum_u64(uint64_t v, FShared& S) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) S.r64[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t r = 0;
-#pragma unroll
-  for (int i = 0; i < FW; i++) r += S.r64[i];
-  __syncthreads();
-  return r;
-}
-__device__ __forceinline__ uint32_t fsum_u32(uint32_t v, FShared& S) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) S.r32[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint32_t r = 0;
-#pragma unroll
-  for (int i = 0; i < FW; i++) r += S.r32[i];
-  __syncthreads();
-  return r;
-}
-__device__ __forceinline__ double fsum_f64(double v, FShared& S) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) S.rd[threadIdx.x >> 6] = v;
-  __syncthreads();
-  double r = 0;
-#pragma unroll
-  for (int i = 0; i < FW; i++) r += S.rd[i];
-  __syncthreads();
-  return r;
-}
+// Exclusive prefix over the block (thread order) of v; *total gets the sum.
 template <typename T>
-__device__ __forceinline__ T fexcl_scan(T v, T* total, T* scratch) {
-  T inc = wave_incl_scan(v);
+__device__ __forceinline__ T bscan_excl(T v, T* total, T* slot) {
+  const T inc = wscan_incl(v);
   const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 63) scratch[w] = inc;
+  if ((threadIdx.x & 63) == 63) slot[w] = inc;
   __syncthreads();
   T off = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < FW; i++) {
-    T s = scratch[i];
+    const T s = slot[i];
     off += (i < w) ? s : (T)0;
     tot += s;
   }
-  __syncthreads();
   *total = tot;
   return off + inc - v;
 }
 
+// Absolute histogram bin of a logit: floor(x c 8), c = log2(e) / T.
+__device__ __forceinline__ int wbin(float x, float c) { return (int)floorf(__fmul_rn(__fmul_rn(x, c), (float)HS)); }
+
 // ---------------------------------------------------------------------------
-// Per-chunk history table (counts of distinct in-range ids).
+// Chunk loads and the per-chunk history count table.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t fhash(int id) { return ((uint32_t)id * 2654435761u) >> (32 - 10); }
-
-struct FPen {
-  bool active;
-  float rep, pres, freq;
-  int lo;
-  const FShared* S;
-  __device__ __forceinline__ int count(int id) const {
-    uint32_t s = fhash(id);
-    for (int p = 0; p < FHASH; p++) {
-      const int k = S->hkey[s];
-      if (k == id) return (int)((S->hcnt[s >> 1] >> ((s & 1) * 16)) & 0xFFFFu);
-      if (k < 0) return 0;
-      s = (s + 1) & (FHASH - 1);
-    }
-    return 0;
-  }
-  // x holds VEC consecutive logits starting at absolute id i0 (inside the chunk).
-  template <int VEC>
-  __device__ __forceinline__ void apply(int i0, float (&x)[VEC]) const {
-    if (!active) return;
-    const int l = i0 - lo;
-    uint32_t w = S->bits[l >> 5] >> (l & 31);
-    if (VEC < 32) w &= (1u << VEC) - 1u;
-    if (!w) return;
-#pragma unroll
-    for (int e = 0; e < VEC; e++)
-      if ((w >> e) & 1u) {
-        const int c = count(i0 + e);
-        if (c) x[e] = penalize(x[e], c, rep, pres, freq);
-      }
-  }
-};
-
-// Builds the table for ids in [lo, lo + n); returns false on overflow.
-__device__ bool build_pen(FShared& S, const int32_t* h, int hlen, int lo, int n) {
-  for (int i = threadIdx.x; i < FHASH; i += FT) S.hkey[i] = -1;
-  for (int i = threadIdx.x; i < FHASH / 2; i += FT) S.hcnt[i] = 0u;
-  for (int i = threadIdx.x; i < FBITS; i += FT) S.bits[i] = 0u;
-  __syncthreads();
-  uint32_t fail = 0;
-  for (int j = threadIdx.x; j < hlen; j += FT) {
-    const int id = h[j];
-    if (id < lo || id >= lo + n) continue;
-    uint32_t s = fhash(id);
-    bool done = false;
-    for (int p = 0; p < FHASH && !done; p++) {
-      const int old = atomicCAS(&S.hkey[s], -1, id);
-      if (old == -1 || old == id) {
-        atomicAdd(&S.hcnt[s >> 1], 1u << ((s & 1) * 16));
-        done = true;
-      } else {
-        s = (s + 1) & (FHASH - 1);
-      }
-    }
-    if (!done) fail = 1;
-    atomicOr(&S.bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
-  }
-  __syncthreads();
-  uint32_t used = 0;
-  for (int i = threadIdx.x; i < FHASH; i += FT) used += S.hkey[i] >= 0 ? 1u : 0u;
-  used = fsum_u32(used, S);
-  fail = fsum_u32(fail, S);
-  return fail == 0 && used <= FHASH_MAX;
-}
-
-// Chunk load: element slot (v, e) of thread t is chunk-local index
-// (v * FT + t) * VEC + e.
+// Element slot (v, e) of thread t is chunk-local index (v * FT + t) * VEC + e;
+// slots at or beyond n hold -inf.
 template <int DT, int VEC>
-__device__ __forceinline__ void load_chunk(const void* row, int lo, int n, const FPen& pen, float (&x)[FE]) {
+__device__ __forceinline__ void load_chunk(const void* row, int lo, int n, float (&x)[FE]) {
   constexpr int NV = FE / VEC;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
@@ -305,7 +205,6 @@ __device__ __forceinline__ void load_chunk(const void* row, int lo, int n, const
 #pragma unroll
       for (int e = 0; e < VEC; e++) t[e] = (l0 + e < n) ? load1<DT>(row, (int64_t)(lo + l0 + e)) : -INFINITY;
     }
-    if (l0 < n) pen.apply<VEC>(lo + l0, t);
 #pragma unroll
     for (int e = 0; e < VEC; e++) x[v * VEC + e] = t[e];
   }
@@ -313,6 +212,70 @@ __device__ __forceinline__ void load_chunk(const void* row, int lo, int n, const
 template <int VEC>
 __device__ __forceinline__ int slot_local(int s) {  // register slot -> chunk-local index
   return ((s / VEC) * FT + (int)threadIdx.x) * VEC + (s % VEC);
+}
+
+// History ids of the row, the first HPF * FT of them, read before the chunk so
+// that the table can be built while the chunk loads are in flight (reads stay
+// inside the row's history_stride).
+struct HistPrefetch {
+  int32_t id[HPF];
+};
+__device__ __forceinline__ void prefetch_history(const int32_t* hrow, int64_t stride, HistPrefetch& hp) {
+#pragma unroll
+  for (int i = 0; i < HPF; i++) {
+    const int jj = i * FT + (int)threadIdx.x;
+    hp.id[i] = (hrow && jj < stride) ? hrow[jj] : -1;
+  }
+}
+// Counts of the history ids inside [lo, lo + n) (hlen <= 65535).  Ends with a barrier.
+__device__ __forceinline__ void build_counts(uint32_t* hc, const int32_t* hrow, int hlen, const HistPrefetch& hp,
+                                             int lo, int n) {
+  u32x4* h4 = reinterpret_cast<u32x4*>(hc);
+#pragma unroll
+  for (int i = 0; i < FCH / 8 / FT; i++) h4[i * FT + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < HPF; i++) {
+    const int jj = i * FT + (int)threadIdx.x;
+    const int id = hp.id[i];
+    if (jj < hlen && id >= lo && id < lo + n) atomicAdd(&hc[(id - lo) >> 1], 1u << (16 * ((id - lo) & 1)));
+  }
+  for (int jj = HPF * FT + (int)threadIdx.x; jj < hlen; jj += FT) {
+    const int id = hrow[jj];
+    if (id >= lo && id < lo + n) atomicAdd(&hc[(id - lo) >> 1], 1u << (16 * ((id - lo) & 1)));
+  }
+  __syncthreads();
+}
+// Applies the penalties of the count table to the chunk in registers.
+template <int VEC>
+__device__ __forceinline__ void apply_counts(const uint32_t* hc, int n, float rep, float pres, float freq,
+                                             float (&x)[FE]) {
+  constexpr int NV = FE / VEC;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int l0 = (v * FT + (int)threadIdx.x) * VEC;
+    if (l0 >= n) continue;
+    uint32_t w[(VEC + 1) / 2];
+    if constexpr (VEC == 8) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(hc + (l0 >> 1));
+      w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+    } else if constexpr (VEC == 4) {
+      const uint2 q = *reinterpret_cast<const uint2*>(hc + (l0 >> 1));
+      w[0] = q.x; w[1] = q.y;
+    } else {
+      w[0] = hc[l0 >> 1] >> (16 * (l0 & 1));
+    }
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < (VEC + 1) / 2; i++) any |= w[i];
+    if (VEC == 1) any &= 0xFFFFu;
+    if (!any) continue;
+#pragma unroll
+    for (int e = 0; e < VEC; e++) {
+      const uint32_t cnt = VEC == 1 ? (w[0] & 0xFFFFu) : ((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      if (cnt) x[v * VEC + e] = penalize(x[v * VEC + e], (int)cnt, rep, pres, freq);
+    }
+  }
 }
 
 // Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end
@@ -331,38 +294,77 @@ __device__ __forceinline__ float collision_lo(float x0, float T) {
   return x;
 }
 
-// kk-th largest (1-based, counting multiplicity, kk <= n) of n keys produced by
-// key_at(i), i in [0, n), by MSB-first 8-bit radix select with S.rh.
-template <typename KA>
-__device__ uint32_t block_select_kth(int n, uint32_t kk, KA key_at, FShared& S) {
-  uint32_t prefix = 0, hmask = 0;
-  for (int l = 0; l < 4; l++) {
-    const int sh = 24 - 8 * l;
-    S.rh[threadIdx.x] = 0;
-    if (threadIdx.x == 0) { S.mi[0] = 0; S.mi[1] = 0; }
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += FT) {
-      const uint32_t k = key_at(i);
-      if ((k & hmask) == prefix) atomicAdd(&S.rh[(k >> sh) & 255u], 1u);
-    }
-    __syncthreads();
-    // descending: thread t owns bin 255 - t
-    const uint32_t c = S.rh[255 - threadIdx.x];
-    uint32_t tot;
-    const uint32_t ex = fexcl_scan<uint32_t>(c, &tot, S.r32);
-    if (ex < kk && kk <= ex + c) { S.mi[0] = 255 - (int)threadIdx.x; S.mi[1] = (int)ex; }
-    __syncthreads();
-    prefix |= (uint32_t)S.mi[0] << sh;
-    kk -= (uint32_t)S.mi[1];
-    hmask |= 255u << sh;
-    __syncthreads();
-  }
-  return prefix;
+// ---------------------------------------------------------------------------
+// Selections over register-resident candidates (FCPT per thread; slot e of a
+// thread is present when e < np).  MSB-first radix over key - kmin with
+// SELD-bit digits; the histogram scan gives each thread SELB / FT bins.
+// ---------------------------------------------------------------------------
+struct SelLevel {
+  uint32_t base;   // kmin
+  int bits;        // bit length of kmax - kmin
+};
+__device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np, FShared& S) {
+  uint32_t mn = 0xFFFFFFFFu, mx = 0;
+#pragma unroll
+  for (int e = 0; e < FCPT; e++)
+    if (e < np) { mn = ck[e] < mn ? ck[e] : mn; mx = ck[e] > mx ? ck[e] : mx; }
+  mn = wmin(mn);
+  mx = wmax(mx);
+  if ((threadIdx.x & 63) == 0) { S.xc[threadIdx.x >> 6] = mn; S.xf[threadIdx.x >> 6] = mx; }
+  __syncthreads();
+  mn = min(min(S.xc[0], S.xc[1]), min(S.xc[2], S.xc[3]));
+  mx = max(max(S.xf[0], S.xf[1]), max(S.xf[2], S.xf[3]));
+  SelLevel L;
+  L.base = mn;
+  L.bits = mx > mn ? 32 - __clz(mx - mn) : 0;
+  return L;
 }
 
-// Mass-weighted MSB-first radix select over n candidates produced by cand(i)
-// -> (key, mass): the largest key v with A + mass(key >= v) > P.  Requires
-// A <= P < A + total mass (ok = 0 otherwise).  above = A + mass(key > v).
+// kk-th largest present key (1 <= kk <= number present).
+__device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np, uint32_t kk, FShared& S) {
+  const SelLevel L = sel_range(ck, np, S);
+  if (L.bits == 0) return L.base;
+  constexpr int PER = SELB / FT;
+  uint32_t hi = 0;      // digits matched so far
+  int top = L.bits;     // bits not yet resolved: [0, top)
+  uint32_t need = kk;
+  while (top > 0) {
+    const int sh = top > SELD ? top - SELD : 0;
+    const int dw = top - sh;
+    for (int i = threadIdx.x; i < SELB; i += FT) S.u.f.x.sel.cnt[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < FCPT; e++) {
+      if (e < np) {
+        const uint32_t d = ck[e] - L.base;
+        const uint32_t up = top >= 32 ? 0u : (d >> top);
+        if (up == hi) atomicAdd(&S.u.f.x.sel.cnt[(d >> sh) & ((1u << dw) - 1u)], 1u);
+      }
+    }
+    __syncthreads();
+    // descending digits: thread t owns digits SELB-1-PER*t ... SELB-PER-PER*t
+    uint32_t c[PER], loc = 0;
+#pragma unroll
+    for (int i = 0; i < PER; i++) { c[i] = S.u.f.x.sel.cnt[SELB - 1 - (PER * (int)threadIdx.x + i)]; loc += c[i]; }
+    uint32_t tot;
+    uint32_t ex = bscan_excl<uint32_t>(loc, &tot, S.xg);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      if (ex < need && need <= ex + c[i]) { S.mi[0] = SELB - 1 - (PER * (int)threadIdx.x + i); S.mi[1] = (int)ex; }
+      ex += c[i];
+    }
+    __syncthreads();
+    hi = (hi << dw) | (uint32_t)S.mi[0];
+    need -= (uint32_t)S.mi[1];
+    top = sh;
+    __syncthreads();
+  }
+  return L.base + hi;
+}
+
+// Mass-weighted select: the largest present key v with A + mass(key >= v) > P,
+// requiring A <= P < A + total (ok = 0 otherwise).  above = A + mass(key > v);
+// ceq / meq = count and mass of key == v.
 struct MassSel {
   uint32_t key;
   uint64_t above;
@@ -370,47 +372,67 @@ struct MassSel {
   uint64_t meq;
   int ok;
 };
-template <typename CA>
-__device__ MassSel block_mass_select(int n, uint64_t A, uint64_t P, CA cand, uint64_t* mh, FShared& S) {
-  MassSel ms{0, A, 0, 0, 1};
-  uint32_t prefix = 0, hmask = 0;
-  for (int l = 0; l < 4; l++) {
-    const int sh = 24 - 8 * l;
-    S.rh[threadIdx.x] = 0;
-    mh[threadIdx.x] = 0;
+// Candidate masses are mass_fixed(mass_f(z, zmax)) of their z keys, recomputed per level.
+__device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, float zmax, uint64_t A, uint64_t P,
+                                            FShared& S) {
+  MassSel ms{0, A, 0, 0, 0};
+  const SelLevel L = sel_range(ck, np, S);
+  constexpr int PER = SELB / FT;
+  uint32_t hi = 0;
+  int top = L.bits;
+  for (;;) {
+    const int sh = top > SELD ? top - SELD : 0;
+    const int dw = top - sh;
+    for (int i = threadIdx.x; i < SELB; i += FT) { S.u.f.x.sel.cnt[i] = 0; S.u.f.x.sel.mass[i] = 0ull; }
     if (threadIdx.x == 0) S.mi[0] = -1;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += FT) {
-      uint32_t k;
-      uint64_t m;
-      cand(i, &k, &m);
-      if ((k & hmask) == prefix) {
-        atomicAdd(&S.rh[(k >> sh) & 255u], 1u);
-        if (m) atomicAdd((unsigned long long*)&mh[(k >> sh) & 255u], (unsigned long long)m);
+#pragma unroll
+    for (int e = 0; e < FCPT; e++) {
+      if (e < np) {
+        const uint32_t d = ck[e] - L.base;
+        const uint32_t up = top >= 32 ? 0u : (d >> top);
+        if (up == hi) {
+          const uint32_t b = dw > 0 ? ((d >> sh) & ((1u << dw) - 1u)) : 0u;
+          atomicAdd(&S.u.f.x.sel.cnt[b], 1u);
+          const uint64_t m = mass_fixed(mass_f(key2f(ck[e]), zmax));
+          if (m) atomicAdd(&S.u.f.x.sel.mass[b], (unsigned long long)m);
+        }
       }
     }
     __syncthreads();
-    const int b = 255 - (int)threadIdx.x;
-    const uint32_t c = S.rh[b];
-    const uint64_t m = mh[b];
+    uint32_t c[PER];
+    uint64_t m[PER], loc = 0;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int b = SELB - 1 - (PER * (int)threadIdx.x + i);
+      c[i] = S.u.f.x.sel.cnt[b];
+      m[i] = S.u.f.x.sel.mass[b];
+      loc += m[i];
+    }
     uint64_t tot;
-    const uint64_t ex = fexcl_scan<uint64_t>(m, &tot, S.r64);
-    if (ms.above + ex <= P && P < ms.above + ex + m) {
-      S.mi[0] = b;
-      S.mi[1] = (int)c;
-      S.m64[0] = ex;
-      S.m64[1] = m;
+    uint64_t ex = ms.above + bscan_excl<uint64_t>(loc, &tot, S.xa);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      if (ex <= P && P < ex + m[i]) {
+        S.mi[0] = SELB - 1 - (PER * (int)threadIdx.x + i);
+        S.mi[1] = (int)c[i];
+        S.m64[0] = ex;
+        S.m64[1] = m[i];
+      }
+      ex += m[i];
     }
     __syncthreads();
-    if (S.mi[0] < 0) { ms.ok = 0; return ms; }
-    prefix |= (uint32_t)S.mi[0] << sh;
-    ms.above += S.m64[0];
+    if (S.mi[0] < 0) return ms;
+    hi = (hi << dw) | (uint32_t)S.mi[0];
+    ms.above = S.m64[0];
     ms.ceq = (uint32_t)S.mi[1];
     ms.meq = S.m64[1];
-    hmask |= 255u << sh;
+    top = sh;
     __syncthreads();
+    if (top == 0) break;
   }
-  ms.key = prefix;
+  ms.key = L.base + hi;
+  ms.ok = 1;
   return ms;
 }
 
