@@ -78,6 +78,36 @@ def build_args(w, dev, logits_dev, out, lib_mod):
     return a
 
 
+def hbm_traffic(config: str):
+    """HBM bytes per launch of the sampling kernel for a workload, as measured by
+    rocprofv3 FETCH_SIZE + WRITE_SIZE passes and scaled by the same counters on a
+    plain copy of known size (profiles/fast_kernel_<config>_hbm_traffic.md,
+    line 'traffic_bytes_per_launch: N'); None when no such measurement exists."""
+    path = os.path.join(REPO, "profiles", f"fast_kernel_{config}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().replace(",", ""))
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration(nbytes: int = 256 << 20, reps: int = 4):
+    """A plain device-to-device copy of known size, for scaling the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE read nbytes each per copy when exact)."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": reps}), flush=True)
+
+
 def cpu_baseline(w, max_rows=None, repeats=3):
     """Reference-as-written sampler (oracle restatement), one call per row with
     that row's parameters and history (continuous_batching.py:394-401)."""
@@ -116,7 +146,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sampler shards rows across "
               f"GPUs with no exchange, which this single-GPU build does not launch.", file=sys.stderr)
@@ -246,7 +281,8 @@ def main():
         "data": "synthetic",
         "config": cfg,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None if args.generic else hbm_traffic(args.config)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
