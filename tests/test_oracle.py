@@ -308,3 +308,65 @@ def test_spec_verify_accept_rule_matches_verify_drafts():
     for b in range(B):
         j = int(n[b])
         assert j == (k if bits[b].all() else int(torch.nonzero(bits[b] == 0)[0]))
+
+
+def test_mirostat_v2_closed_form():
+    # uniform logits over V: H = ln V, every id ties at the k-th value (top-k keeps all)
+    V, tau, eta = 8, 5.0, 0.1
+    x = torch.zeros(1, V)
+    tok, prev, k = O.mirostat_v2_ref(x, 1.0, tau, eta, None, 0.99)
+    H = math.log(V)
+    assert abs(prev - (H - eta * (H - tau))) < 1e-6
+    assert k == max(1, int(math.exp(prev)))
+    assert tok == 7  # inverse CDF of u = 0.99 over 8 equal masses
+    # two-level distribution: entropy from an explicit loop, k from the update rule
+    x = torch.tensor([[3.0, 3.0, 0.0, 0.0, 0.0, -1.0]])
+    T = 0.5
+    p = torch.softmax(x / T, -1).double().reshape(-1).tolist()
+    H = -sum(pi * math.log(pi) for pi in p)
+    tok, prev, k = O.mirostat_v2_ref(x, T, 0.2, 0.5, 0.9, 0.3)
+    assert abs(prev - (0.9 - 0.5 * (H - 0.2))) < 1e-6
+    assert k == max(1, int(math.exp(prev))) and k == 1
+    assert tok == 0  # k = 1 keeps the first maximum (lower index wins the tie)
+    # non-positive running estimate: no top-k, a plain draw
+    tok, prev, k = O.mirostat_v2_ref(x, T, 0.0, 1.0, 0.1, 0.999999)
+    assert prev <= 0 and k == 0 and tok == 5
+
+
+def test_top_p_truth_brute_force():
+    # fp64 keep rule by an explicit loop over every id, ties lower-index-first
+    g = torch.Generator().manual_seed(21)
+    for trial in range(40):
+        V = int(torch.randint(1, 12, (1,), generator=g))
+        z = torch.round(torch.randn(V, generator=g) * 2) / 2  # repeated values
+        if trial % 5 == 0:
+            z[int(torch.randint(0, V, (1,), generator=g))] = float("-inf")
+        p = float(torch.rand(1, generator=g)) * 0.999  # p >= 1 turns the filter off
+        vals = [float(v) for v in z]
+        m = max(vals)
+        w = [math.exp(v - m) if v != float("-inf") else 0.0 for v in vals]
+        tot = sum(w)
+        idx = sorted(range(V), key=lambda i: (-vals[i], i))
+        n, run = 0, 0.0
+        for pos, i in enumerate(idx):
+            if pos == 0 or run / tot <= p:
+                n += 1
+            else:
+                break
+            run += w[i]
+        order, excl, n_truth = O.top_p_truth(z, p)
+        assert list(order) == idx
+        assert n_truth == n, (trial, vals, p)
+
+
+def test_top_p_reference_cum_invariants():
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(4000, generator=g) * 3
+    ref = O.top_p_reference_cum(z)
+    _, excl, _ = O.top_p_truth(z, 0.9)
+    assert ref[0] == 0.0                                    # exclusive: nothing precedes the maximum
+    p0 = float(torch.softmax(z.double(), 0).max())
+    assert abs(ref[1] - p0) < 1e-6                          # then the largest probability
+    assert np.all(np.diff(ref) >= 0)                        # descending order gives a non-decreasing prefix
+    assert np.max(np.abs(ref - excl)) < 4000 * 2.0 ** -24   # fp32 accumulation of the fp64 truth
+    assert np.max(np.abs(ref - excl)) > 0                   # and it is the fp32 one, not the truth
