@@ -64,7 +64,7 @@ constexpr int FAST_MAX_ROWS = 8192;
 
 FastWs fast_layout(void* base, int R, int V) {
   FastWs w{};
-  const int G = (V + FCH - 1) / FCH;
+  const int G = (V + FCH_MIN - 1) / FCH_MIN;  // the most chunks any dtype uses
   if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
   w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
   w.h_stride = (int64_t)round_up((size_t)G * HB, 32);                // floats
@@ -141,7 +141,10 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   const FastWs w = fast_layout(ws, P.R, P.V);
   FParams F{};
   F.k = P;
-  F.G = (P.V + FCH - 1) / FCH;
+  // chunk size of the kernel variant: 16384 for 16-bit logits read in 16-byte
+  // vectors (two logits per register), else 8192
+  const int ch = (LPS_PACK16 && dtype != LPS_DTYPE_F32 && vec) ? 2 * FCH_MIN : FCH_MIN;
+  F.G = (P.V + ch - 1) / ch;
   F.counters = w.counters;
   F.status = w.status;
   F.sum1 = w.sum1;

@@ -44,8 +44,7 @@ namespace lps {
 
 constexpr int FT = 256;                 // threads per workgroup
 constexpr int FW = FT / 64;             // waves per workgroup
-constexpr int FE = 32;                  // elements per thread
-constexpr int FCH = FT * FE;            // chunk size (8192)
+constexpr int FCH_MIN = FT * 32;        // smallest chunk (fp32 and element-read rows): sizes the workspace
 constexpr int FAST_KMAX = 256;          // largest top_k / top-N handled by the fast path
 constexpr int PUBCAP = 512;             // published candidates per chunk
 constexpr int FCPT = 16;                // finaliser candidates per thread (registers)
@@ -53,9 +52,12 @@ constexpr int FCAP = FT * FCPT;         // finaliser candidate capacity (4096)
 constexpr int KEPTCAP = 512;            // finaliser kept list
 constexpr int HB = 256;                 // histogram bins per chunk (1/8 log2 unit each)
 constexpr int HS = 8;                   // bins per log2 unit
-constexpr int SELD = 11;                // select digit bits
-constexpr int SELB = 1 << SELD;         // select histogram bins
+constexpr int SELD = 12;                // count-select digit bits
+constexpr int SELB = 1 << SELD;         // count-select histogram bins
+constexpr int SELDM = 10;               // mass-select digit bits
+constexpr int SELBM = 1 << SELDM;       // mass-select histogram bins
 constexpr int HPF = 4;                  // history ids prefetched per thread
+constexpr int WCAP = 256;               // per-wave candidate list capacity
 constexpr int MAXG = 64;                // chunks per row (V <= 524287)
 
 enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEFER = 4 };
@@ -65,11 +67,11 @@ constexpr int32_t LPS_ROW_DEFERRED = 8;  // internal: finished by the general al
 struct ChunkSum1 {   // published before the barrier / handoff
   uint32_t mkey;     // max key of the penalised logits of the chunk (NaN -> 0xFFFFFFFF)
   int32_t amax;      // greedy rows: first index of that key
-  float zsum;        // sum over the chunk of exp2(x c - xmax_chunk c), c = log2(e) / T
+  double zsum;       // sum over the chunk of exp2(x c - xmax_chunk c), c = log2(e) / T
   int32_t btop;      // histogram top bin (absolute) of the chunk
   uint32_t ninf;     // -inf logits in the chunk (when counted)
   uint32_t flags;    // CF_*
-  uint32_t pad[2];
+  uint32_t pad;
 };
 struct ChunkSum2 {   // published at the handoff
   uint32_t ncand;    // candidates published
@@ -95,34 +97,36 @@ struct FParams {
 struct FShared {
   union {
     struct {                              // chunk phase
-      uint32_t hc[FCH / 2];               // history counts, two 16-bit counts per word
+      uint32_t hc[4096];                  // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
       unsigned long long hm[HB];          // chunk mass histogram, fixed point
+      unsigned long long gm[HB];          // nucleus region: merged row histogram, fixed point
       double scale[MAXG];                 // nucleus region: chunk -> row reference
       int32_t btop[MAXG];
+      uint2 cl[FW][WCAP];                 // per-wave candidate lists (x key, index)
     } c;
     struct {                              // finaliser
       union {
+        uint32_t cnt[2][SELB];            // count select, double-buffered digit histograms
         struct {
-          uint32_t cnt[SELB];
-          unsigned long long mass[SELB];
-        } sel;                            // select histograms
+          uint32_t cnt[2][SELBM];
+          unsigned long long mass[2][SELBM];
+        } selm;                           // mass select
         struct {
-          uint32_t kkey[KEPTCAP];         // z keys
-          uint32_t kx[KEPTCAP];           // x keys
-          int32_t kidx[KEPTCAP];
+          uint64_t skey[KEPTCAP];         // (z key << 32) | ~index: larger = earlier in sorted order
           unsigned long long km[KEPTCAP];
+          int32_t kidx[KEPTCAP];
           int32_t kord[KEPTCAP];          // sorted position -> slot
           int32_t iord[KEPTCAP];          // index-order position -> slot
           unsigned long long cum[KEPTCAP];
         } k;                              // kept list
-        uint32_t hc[FCH / 2];             // rescan history counts
+        uint32_t hc[4096];                // rescan history counts
       } x;
       uint32_t pre[MAXG + 1];             // candidate prefix over chunks
       double scale[MAXG];                 // chunk -> row reference
+      float wm[MAXG];                     // chunk max * c (the chunk's mass reference)
       double keptm[MAXG];                 // kept mass per chunk
       double abvm[MAXG];                  // nucleus: mass above the region per chunk
-      unsigned long long epre[MAXG];      // nucleus: kept candidate mass prefix at chunk starts
-      unsigned long long eend[MAXG];      // ... and after each chunk's last candidate
+      unsigned long long keptf[MAXG];     // nucleus: kept candidate mass per chunk, fixed point
     } f;
   } u;
   // cross-wave exchange slots (each slot is reused only after an intervening barrier)
@@ -188,31 +192,119 @@ __device__ __forceinline__ T bscan_excl(T v, T* total, T* slot) {
 __device__ __forceinline__ int wbin(float x, float c) { return (int)floorf(__fmul_rn(__fmul_rn(x, c), (float)HS)); }
 
 // ---------------------------------------------------------------------------
-// Chunk loads and the per-chunk history count table.
+// A thread's share of a chunk, held in 32 registers r[].
+//   fp32 in 16-byte vectors of 4, and every dtype read element by element
+//   (unaligned rows): 32 logits as fp32 bits; penalties applied in place.
+//   bf16 / fp16 in 16-byte vectors of 8 (PACKED): 64 logits, two per register
+//   in the input format; slots whose id has a history count are flagged in
+//   pmask and penalised (exactly, in fp32) whenever they are read.
+// Slot s of thread t is chunk-local index ((s / VEC) * FT + t) * VEC + s % VEC;
+// slots at or beyond the chunk end hold -inf.
 // ---------------------------------------------------------------------------
-// Element slot (v, e) of thread t is chunk-local index (v * FT + t) * VEC + e;
-// slots at or beyond n hold -inf.
+template <bool B> struct BoolT { static constexpr bool value = B; };
+
+struct PenArgs {        // penalties of the row, and the chunk's count table in LDS
+  const uint32_t* hc;   // 16-bit counts (fp32 chunks) or 8-bit counts (packed chunks)
+  float rep, pres, freq;
+};
+
+// Packed 16-bit chunks (64 logits per thread, 16384 per chunk) halve the
+// workgroup count but add an unpack per pass; measured slower on MI355X, so off.
+#ifndef LPS_PACK16
+#define LPS_PACK16 0
+#endif
 template <int DT, int VEC>
-__device__ __forceinline__ void load_chunk(const void* row, int lo, int n, float (&x)[FE]) {
-  constexpr int NV = FE / VEC;
-#pragma unroll
-  for (int v = 0; v < NV; v++) {
-    const int l0 = (v * FT + (int)threadIdx.x) * VEC;
-    float t[VEC];
-    if (l0 + VEC <= n) {
-      loadv<DT, VEC>(row, (int64_t)(lo + l0), t);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; e++) t[e] = (l0 + e < n) ? load1<DT>(row, (int64_t)(lo + l0 + e)) : -INFINITY;
-    }
-#pragma unroll
-    for (int e = 0; e < VEC; e++) x[v * VEC + e] = t[e];
+struct Chunk {
+  static constexpr bool PACKED = LPS_PACK16 && DT != LPS_DTYPE_F32 && VEC == 8;
+  static constexpr int NE = PACKED ? 64 : 32;   // logits per thread (fp32 registers hold 32)
+  static constexpr int CH = FT * NE;            // logits per chunk
+  static constexpr int NV = NE / VEC;           // vectors per thread
+  static constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
+  static constexpr uint32_t NEG16 = DT == LPS_DTYPE_BF16 ? 0xFF80u : 0xFC00u;  // -inf, 16-bit
+  uint32_t r[32];
+  uint64_t pmask;
+
+  __device__ static __forceinline__ int local(int s) {
+    return ((s / VEC) * FT + (int)threadIdx.x) * VEC + (s % VEC);
   }
-}
-template <int VEC>
-__device__ __forceinline__ int slot_local(int s) {  // register slot -> chunk-local index
-  return ((s / VEC) * FT + (int)threadIdx.x) * VEC + (s % VEC);
-}
+  __device__ static __forceinline__ float h2f(uint32_t h) {
+    return DT == LPS_DTYPE_BF16 ? __uint_as_float(h << 16) : f16_to_f32(h);
+  }
+  // Logit of slot s (penalised when PEN and the slot is flagged).
+  template <bool PEN>
+  __device__ __forceinline__ float val(int s, const PenArgs& pa) const {
+    if constexpr (!PACKED) {
+      return __uint_as_float(r[s]);
+    } else {
+      const uint32_t w = r[s >> 1];
+      float f;
+      if constexpr (DT == LPS_DTYPE_BF16) f = __uint_as_float((s & 1) ? (w & 0xFFFF0000u) : (w << 16));
+      else f = f16_to_f32((s & 1) ? (w >> 16) : (w & 0xFFFFu));
+      if constexpr (PEN) {
+        if ((pmask >> s) & 1ull) {
+          // this thread's 8-bit counts: one base, a constant offset per slot
+          const uint8_t* hb = reinterpret_cast<const uint8_t*>(pa.hc) + threadIdx.x * VEC;
+          const uint32_t cnt = hb[(s / VEC) * (FT * VEC) + (s % VEC)];
+          f = penalize(f, (int)cnt, pa.rep, pa.pres, pa.freq);
+        }
+      }
+      return f;
+    }
+  }
+
+  // Every full 16-byte vector load is issued before any value is used
+  // (positions clamped to the chunk's last full vector, no branch between the
+  // loads); the at most one partial vector of a chunk is read element by element.
+  __device__ __forceinline__ void load(const void* row, int lo, int n) {
+    pmask = 0ull;
+    const char* base = reinterpret_cast<const char*>(row);
+    if constexpr (VEC == 1) {
+      float raw[32];
+#pragma unroll
+      for (int s = 0; s < 32; s++) raw[s] = load1<DT>(row, (int64_t)(lo + min(s * FT + (int)threadIdx.x, n - 1)));
+#pragma unroll
+      for (int s = 0; s < 32; s++) r[s] = __float_as_uint((s * FT + (int)threadIdx.x) < n ? raw[s] : -INFINITY);
+    } else {
+      static_assert(VEC * ES == 16, "vector slots are 16 bytes");
+      const int lastv = (n / VEC - 1) * VEC;  // start of the last full vector; < 0 when none
+      u32x4 raw[NV];
+      if (lastv >= 0) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+          const int lv = min((v * FT + (int)threadIdx.x) * VEC, lastv);
+          raw[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (int64_t)(lo + lv) * ES));
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const int l0 = (v * FT + (int)threadIdx.x) * VEC;
+        uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
+        if (l0 + VEC > n) {  // partial or empty vector
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            if constexpr (DT == LPS_DTYPE_F32) {
+              w[q] = __float_as_uint(l0 + q < n ? load1<DT>(row, (int64_t)(lo + l0 + q)) : -INFINITY);
+            } else {
+              const int a = l0 + 2 * q, b = a + 1;
+              const uint32_t ha = a < n ? (uint32_t)__builtin_nontemporal_load(
+                                              reinterpret_cast<const unsigned short*>(base) + lo + a) : NEG16;
+              const uint32_t hb = b < n ? (uint32_t)__builtin_nontemporal_load(
+                                              reinterpret_cast<const unsigned short*>(base) + lo + b) : NEG16;
+              w[q] = ha | (hb << 16);
+            }
+          }
+        }
+        if constexpr (PACKED || DT == LPS_DTYPE_F32) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) r[v * 4 + q] = w[q];
+        } else {  // 16-bit logits kept as fp32 registers
+#pragma unroll
+          for (int e = 0; e < 8; e++) r[v * 8 + e] = __float_as_uint(h2f((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+        }
+      }
+    }
+  }
+};
 
 // History ids of the row, the first HPF * FT of them, read before the chunk so
 // that the table can be built while the chunk loads are in flight (reads stay
@@ -227,56 +319,90 @@ __device__ __forceinline__ void prefetch_history(const int32_t* hrow, int64_t st
     hp.id[i] = (hrow && jj < stride) ? hrow[jj] : -1;
   }
 }
-// Counts of the history ids inside [lo, lo + n) (hlen <= 65535).  Ends with a barrier.
-__device__ __forceinline__ void build_counts(uint32_t* hc, const int32_t* hrow, int hlen, const HistPrefetch& hp,
-                                             int lo, int n) {
+// Counts of the history ids inside [lo, lo + n), BITS (16 or 8) bits per id in
+// hc (8192 or 16384 ids in 4096 words).  Returns false when a count does not
+// fit (16-bit: hlen > 65535 is refused by the caller; 8-bit: a count reached
+// 255).  Ends with a barrier.
+template <int BITS>
+__device__ __forceinline__ bool build_counts(uint32_t* hc, const int32_t* hrow, int hlen, const HistPrefetch& hp,
+                                             int lo, int n, FShared& S) {
+  constexpr int PER = 32 / BITS;  // ids per word
   u32x4* h4 = reinterpret_cast<u32x4*>(hc);
 #pragma unroll
-  for (int i = 0; i < FCH / 8 / FT; i++) h4[i * FT + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < 1024 / FT; i++) h4[i * FT + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+  if (threadIdx.x == 0) S.mi[30] = 0;
   __syncthreads();
+  bool sat = false;
+  auto add = [&](int id) {
+    if (id >= lo && id < lo + n) {
+      const int l = id - lo;
+      const int sh = BITS * (l % PER);
+      const uint32_t old = atomicAdd(&hc[l / PER], 1u << sh);
+      if (BITS == 8 && ((old >> sh) & 0xFFu) >= 254u) sat = true;
+    }
+  };
 #pragma unroll
-  for (int i = 0; i < HPF; i++) {
-    const int jj = i * FT + (int)threadIdx.x;
-    const int id = hp.id[i];
-    if (jj < hlen && id >= lo && id < lo + n) atomicAdd(&hc[(id - lo) >> 1], 1u << (16 * ((id - lo) & 1)));
-  }
-  for (int jj = HPF * FT + (int)threadIdx.x; jj < hlen; jj += FT) {
-    const int id = hrow[jj];
-    if (id >= lo && id < lo + n) atomicAdd(&hc[(id - lo) >> 1], 1u << (16 * ((id - lo) & 1)));
-  }
+  for (int i = 0; i < HPF; i++)
+    if (i * FT + (int)threadIdx.x < hlen) add(hp.id[i]);
+  for (int jj = HPF * FT + (int)threadIdx.x; jj < hlen; jj += FT) add(hrow[jj]);
+  if (sat) S.mi[30] = 1;
   __syncthreads();
+  return S.mi[30] == 0;
 }
-// Applies the penalties of the count table to the chunk in registers.
-template <int VEC>
-__device__ __forceinline__ void apply_counts(const uint32_t* hc, int n, float rep, float pres, float freq,
-                                             float (&x)[FE]) {
-  constexpr int NV = FE / VEC;
+// fp32 chunks: apply the 16-bit count table in place.
+template <int DT, int VEC>
+__device__ __forceinline__ void apply_counts(Chunk<DT, VEC>& C, int n, const PenArgs& pa) {
+  static_assert(!Chunk<DT, VEC>::PACKED, "in-place penalties are for fp32 registers");
+  constexpr int NV = Chunk<DT, VEC>::NV;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
     const int l0 = (v * FT + (int)threadIdx.x) * VEC;
     if (l0 >= n) continue;
     uint32_t w[(VEC + 1) / 2];
     if constexpr (VEC == 8) {
-      const u32x4 q = *reinterpret_cast<const u32x4*>(hc + (l0 >> 1));
+      const u32x4 q = *reinterpret_cast<const u32x4*>(pa.hc + (l0 >> 1));
       w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
     } else if constexpr (VEC == 4) {
-      const uint2 q = *reinterpret_cast<const uint2*>(hc + (l0 >> 1));
+      const uint2 q = *reinterpret_cast<const uint2*>(pa.hc + (l0 >> 1));
       w[0] = q.x; w[1] = q.y;
     } else {
-      w[0] = hc[l0 >> 1] >> (16 * (l0 & 1));
+      w[0] = (pa.hc[l0 >> 1] >> (16 * (l0 & 1))) & 0xFFFFu;
     }
     uint32_t any = 0;
 #pragma unroll
     for (int i = 0; i < (VEC + 1) / 2; i++) any |= w[i];
-    if (VEC == 1) any &= 0xFFFFu;
     if (!any) continue;
 #pragma unroll
     for (int e = 0; e < VEC; e++) {
-      const uint32_t cnt = VEC == 1 ? (w[0] & 0xFFFFu) : ((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-      if (cnt) x[v * VEC + e] = penalize(x[v * VEC + e], (int)cnt, rep, pres, freq);
+      const uint32_t cnt = VEC == 1 ? w[0] : ((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      const int s = v * VEC + e;
+      if (cnt) C.r[s] = __float_as_uint(penalize(__uint_as_float(C.r[s]), (int)cnt, pa.rep, pa.pres, pa.freq));
     }
   }
 }
+// Packed chunks: flag the slots with an 8-bit count.
+template <int DT, int VEC>
+__device__ __forceinline__ void mark_counts(Chunk<DT, VEC>& C, int n, const PenArgs& pa) {
+  static_assert(Chunk<DT, VEC>::PACKED, "flags are for packed registers");
+  constexpr int NV = Chunk<DT, VEC>::NV;
+  uint64_t m = 0;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int l0 = (v * FT + (int)threadIdx.x) * VEC;  // 8 ids = 2 words
+    const uint2 q = *reinterpret_cast<const uint2*>(pa.hc + (l0 >> 2));
+    const uint64_t c = ((uint64_t)q.y << 32) | q.x;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m |= ((c >> (8 * e)) & 0xFFull) ? (1ull << (v * 8 + e)) : 0ull;
+  }
+  (void)n;
+  C.pmask = m;
+}
+
+// Candidate lists: each wave appends its elements to its own LDS list (no
+// atomics), then the block copies the lists to global memory in order.
+struct WaveList {
+  uint32_t count;  // wave-uniform running count
+};
 
 // Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end
 // of the division-collision group of x0, so that "z >= fl(x0 / T)" is
@@ -295,15 +421,20 @@ __device__ __forceinline__ float collision_lo(float x0, float T) {
 }
 
 // ---------------------------------------------------------------------------
-// Selections over register-resident candidates (FCPT per thread; slot e of a
-// thread is present when e < np).  MSB-first radix over key - kmin with
-// SELD-bit digits; the histogram scan gives each thread SELB / FT bins.
+// Selections over register-resident candidates: thread t holds candidate
+// e * FT + t in slot e, present when e < np.  MSB-first radix over
+// key - kmin; the digit histograms are double-buffered so that one level costs
+// three barriers (histogram, scan, result).  Each thread scans SELB / FT (or
+// SELBM / FT) consecutive bins, highest digit first.
 // ---------------------------------------------------------------------------
 struct SelLevel {
   uint32_t base;   // kmin
   int bits;        // bit length of kmax - kmin
 };
-__device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np, FShared& S) {
+// Key range of the present candidates; clears histogram buffer 0 (nb bins of
+// cnt0, and of m0 when given) before its barrier.
+__device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np, uint32_t* cnt0, int nb,
+                                              unsigned long long* m0, FShared& S) {
   uint32_t mn = 0xFFFFFFFFu, mx = 0;
 #pragma unroll
   for (int e = 0; e < FCPT; e++)
@@ -311,6 +442,10 @@ __device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np
   mn = wmin(mn);
   mx = wmax(mx);
   if ((threadIdx.x & 63) == 0) { S.xc[threadIdx.x >> 6] = mn; S.xf[threadIdx.x >> 6] = mx; }
+  for (int i = threadIdx.x; i < nb; i += FT) {
+    cnt0[i] = 0u;
+    if (m0) m0[i] = 0ull;
+  }
   __syncthreads();
   mn = min(min(S.xc[0], S.xc[1]), min(S.xc[2], S.xc[3]));
   mx = max(max(S.xf[0], S.xf[1]), max(S.xf[2], S.xf[3]));
@@ -322,30 +457,30 @@ __device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np
 
 // kk-th largest present key (1 <= kk <= number present).
 __device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np, uint32_t kk, FShared& S) {
-  const SelLevel L = sel_range(ck, np, S);
+  auto& H = S.u.f.x.cnt;
+  const SelLevel L = sel_range(ck, np, H[0], SELB, nullptr, S);
   if (L.bits == 0) return L.base;
   constexpr int PER = SELB / FT;
   uint32_t hi = 0;      // digits matched so far
   int top = L.bits;     // bits not yet resolved: [0, top)
   uint32_t need = kk;
+  int buf = 0;
   while (top > 0) {
     const int sh = top > SELD ? top - SELD : 0;
     const int dw = top - sh;
-    for (int i = threadIdx.x; i < SELB; i += FT) S.u.f.x.sel.cnt[i] = 0;
-    __syncthreads();
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       if (e < np) {
         const uint32_t d = ck[e] - L.base;
         const uint32_t up = top >= 32 ? 0u : (d >> top);
-        if (up == hi) atomicAdd(&S.u.f.x.sel.cnt[(d >> sh) & ((1u << dw) - 1u)], 1u);
+        if (up == hi) atomicAdd(&H[buf][(d >> sh) & ((1u << dw) - 1u)], 1u);
       }
     }
+    for (int i = threadIdx.x; i < SELB; i += FT) H[buf ^ 1][i] = 0u;  // next level's buffer
     __syncthreads();
-    // descending digits: thread t owns digits SELB-1-PER*t ... SELB-PER-PER*t
     uint32_t c[PER], loc = 0;
 #pragma unroll
-    for (int i = 0; i < PER; i++) { c[i] = S.u.f.x.sel.cnt[SELB - 1 - (PER * (int)threadIdx.x + i)]; loc += c[i]; }
+    for (int i = 0; i < PER; i++) { c[i] = H[buf][SELB - 1 - (PER * (int)threadIdx.x + i)]; loc += c[i]; }
     uint32_t tot;
     uint32_t ex = bscan_excl<uint32_t>(loc, &tot, S.xg);
 #pragma unroll
@@ -357,14 +492,15 @@ __device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np
     hi = (hi << dw) | (uint32_t)S.mi[0];
     need -= (uint32_t)S.mi[1];
     top = sh;
-    __syncthreads();
+    buf ^= 1;
   }
+  __syncthreads();
   return L.base + hi;
 }
 
 // Mass-weighted select: the largest present key v with A + mass(key >= v) > P,
 // requiring A <= P < A + total (ok = 0 otherwise).  above = A + mass(key > v);
-// ceq / meq = count and mass of key == v.
+// ceq / meq = count and mass of key == v.  mass(e) gives a candidate's mass.
 struct MassSel {
   uint32_t key;
   uint64_t above;
@@ -372,20 +508,20 @@ struct MassSel {
   uint64_t meq;
   int ok;
 };
-// Candidate masses are mass_fixed(mass_f(z, zmax)) of their z keys, recomputed per level.
-__device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, float zmax, uint64_t A, uint64_t P,
+template <typename MF>
+__device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, MF mass, uint64_t A, uint64_t P,
                                             FShared& S) {
   MassSel ms{0, A, 0, 0, 0};
-  const SelLevel L = sel_range(ck, np, S);
-  constexpr int PER = SELB / FT;
+  auto& H = S.u.f.x.selm;
+  const SelLevel L = sel_range(ck, np, H.cnt[0], SELBM, H.mass[0], S);
+  constexpr int PER = SELBM / FT;
   uint32_t hi = 0;
   int top = L.bits;
+  int buf = 0;
   for (;;) {
-    const int sh = top > SELD ? top - SELD : 0;
+    const int sh = top > SELDM ? top - SELDM : 0;
     const int dw = top - sh;
-    for (int i = threadIdx.x; i < SELB; i += FT) { S.u.f.x.sel.cnt[i] = 0; S.u.f.x.sel.mass[i] = 0ull; }
     if (threadIdx.x == 0) S.mi[0] = -1;
-    __syncthreads();
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       if (e < np) {
@@ -393,20 +529,21 @@ __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, 
         const uint32_t up = top >= 32 ? 0u : (d >> top);
         if (up == hi) {
           const uint32_t b = dw > 0 ? ((d >> sh) & ((1u << dw) - 1u)) : 0u;
-          atomicAdd(&S.u.f.x.sel.cnt[b], 1u);
-          const uint64_t m = mass_fixed(mass_f(key2f(ck[e]), zmax));
-          if (m) atomicAdd(&S.u.f.x.sel.mass[b], (unsigned long long)m);
+          atomicAdd(&H.cnt[buf][b], 1u);
+          const uint64_t m = mass(e);
+          if (m) atomicAdd(&H.mass[buf][b], (unsigned long long)m);
         }
       }
     }
+    for (int i = threadIdx.x; i < SELBM; i += FT) { H.cnt[buf ^ 1][i] = 0u; H.mass[buf ^ 1][i] = 0ull; }
     __syncthreads();
     uint32_t c[PER];
     uint64_t m[PER], loc = 0;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      const int b = SELB - 1 - (PER * (int)threadIdx.x + i);
-      c[i] = S.u.f.x.sel.cnt[b];
-      m[i] = S.u.f.x.sel.mass[b];
+      const int b = SELBM - 1 - (PER * (int)threadIdx.x + i);
+      c[i] = H.cnt[buf][b];
+      m[i] = H.mass[buf][b];
       loc += m[i];
     }
     uint64_t tot;
@@ -414,7 +551,7 @@ __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, 
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       if (ex <= P && P < ex + m[i]) {
-        S.mi[0] = SELB - 1 - (PER * (int)threadIdx.x + i);
+        S.mi[0] = SELBM - 1 - (PER * (int)threadIdx.x + i);
         S.mi[1] = (int)c[i];
         S.m64[0] = ex;
         S.m64[1] = m[i];
@@ -422,13 +559,14 @@ __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, 
       ex += m[i];
     }
     __syncthreads();
-    if (S.mi[0] < 0) return ms;
+    if (S.mi[0] < 0) { __syncthreads(); return ms; }
     hi = (hi << dw) | (uint32_t)S.mi[0];
     ms.above = S.m64[0];
     ms.ceq = (uint32_t)S.mi[1];
     ms.meq = S.m64[1];
     top = sh;
-    __syncthreads();
+    buf ^= 1;
+    __syncthreads();  // S.mi[0] is reset by the next level
     if (top == 0) break;
   }
   ms.key = L.base + hi;

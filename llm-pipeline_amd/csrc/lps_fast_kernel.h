@@ -32,20 +32,39 @@ __device__ float penalized_logit(const void* row, int id, const int32_t* h, int 
   return x;
 }
 
-// Rank sort of the kept list by (z desc, idx asc): kord[rank] = slot.
+// Rank sort of the kept list by (z desc, idx asc), i.e. by skey desc:
+// kord[rank] = slot.  LDS reads are batched 8 at a time (independent loads).
 __device__ void rank_sort_kept(int K, FShared& S) {
   auto& k = S.u.f.x.k;
   for (int i = threadIdx.x; i < K; i += FT) {
-    const uint32_t ki = k.kkey[i];
-    const int ii = k.kidx[i];
+    const uint64_t ki = k.skey[i];
     int rank = 0;
-    for (int q = 0; q < K; q++) {
-      const uint32_t kq = k.kkey[q];
-      rank += (kq > ki || (kq == ki && k.kidx[q] < ii)) ? 1 : 0;
+    int q = 0;
+    for (; q + 8 <= K; q += 8) {
+      uint64_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) t[u] = k.skey[q + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) rank += t[u] > ki ? 1 : 0;
     }
+    for (; q < K; q++) rank += k.skey[q] > ki ? 1 : 0;
     k.kord[rank] = i;
   }
   __syncthreads();
+}
+
+// Number of entries of a[0, n) below v (batched LDS reads).
+__device__ __forceinline__ int count_below(const int32_t* a, int n, int v) {
+  int c = 0, q = 0;
+  for (; q + 8 <= n; q += 8) {
+    int32_t t[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) t[u] = a[q + u];
+#pragma unroll
+    for (int u = 0; u < 8; u++) c += t[u] < v ? 1 : 0;
+  }
+  for (; q < n; q++) c += a[q] < v ? 1 : 0;
+  return c;
 }
 
 // Inclusive prefix of km over the sorted order into cum, K <= KEPTCAP (slot xb).
@@ -71,13 +90,44 @@ __device__ void sorted_prefix(int K, FShared& S) {
   __syncthreads();
 }
 
-__device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+// Runs fn(BoolT<true>) when the wave holds penalised packed slots, else
+// fn(BoolT<false>) (fp32 chunks carry their penalties in place).
+template <bool PK, typename Fn>
+__device__ __forceinline__ void with_pen(bool wpen, Fn&& fn) {
+  if constexpr (PK) {
+    if (wpen) fn(BoolT<true>{});
+    else fn(BoolT<false>{});
+  } else {
+    fn(BoolT<false>{});
+  }
+}
+
+// Copies the per-wave candidate lists (counts in slot[0..3]) to out[0, min(tot, PUBCAP))
+// in wave order; returns the total.  The caller has passed a barrier after the
+// lists and counts were written.
+__device__ __forceinline__ uint32_t copy_lists(const FShared& S, const uint32_t* cnt, uint2* out, uint32_t* over) {
+  const uint32_t c0 = cnt[0], c1 = cnt[1], c2 = cnt[2], c3 = cnt[3];
+  const uint32_t tot = c0 + c1 + c2 + c3;
+  *over = (c0 > WCAP || c1 > WCAP || c2 > WCAP || c3 > WCAP || tot > (uint32_t)PUBCAP) ? 1u : 0u;
+  if (!*over) {
+    const uint32_t o1 = c0, o2 = c0 + c1, o3 = c0 + c1 + c2;
+    for (uint32_t i = threadIdx.x; i < tot; i += FT) {
+      const int w = (i >= o1) + (i >= o2) + (i >= o3);
+      const uint32_t k = i - (w == 0 ? 0u : w == 1 ? o1 : w == 2 ? o2 : o3);
+      out[i] = S.u.c.cl[w][k];
+    }
+  }
+  return tot;
+}
 
 // The fast path for the row / chunk of this workgroup.  Returns 0 when the
 // workgroup is done, or a positive reason code when it must run the general
 // algorithm on its row (the condition is workgroup-uniform).
 template <int DT, int VEC>
 __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
+  using CK = Chunk<DT, VEC>;
+  constexpr int NE = CK::NE, CH = CK::CH, NV = CK::NV;
+  constexpr bool PK = CK::PACKED;
   const KParams& P = F.k;
   const int G = F.G;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -86,10 +136,9 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   LPS_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int V = P.V;
-  const int lo = j * FCH;
-  const int n = (V - lo) < FCH ? (V - lo) : FCH;
-  constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
-  constexpr int NV = FE / VEC;
+  const int lo = j * CH;
+  const int n = (V - lo) < CH ? (V - lo) : CH;
+  constexpr int ES = CK::ES;
   const void* row = reinterpret_cast<const char*>(P.logits) +
                     ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
   ChunkSum1* s1 = F.sum1 + (int64_t)r * F.s_stride;
@@ -102,8 +151,8 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   const int32_t* hrow = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
   HistPrefetch hp;
   prefetch_history(hrow, P.history_stride, hp);
-  float x[FE];
-  load_chunk<DT, VEC>(row, lo, n, x);
+  CK C;
+  C.load(row, lo, n);
 
   const float T = P.temperature ? P.temperature[r] : P.temperature_def;
   const int topk = P.top_k ? P.top_k[r] : P.top_k_def;
@@ -116,6 +165,11 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (topp != topp) topp = 1.0f;
   const bool greedy = !(T > 0.0f);
   const int ntop = (P.n_top > 0 && P.top_logprobs) ? P.n_top : 0;
+  // needed only by the row's finaliser; read with the other row parameters
+  const float u_row = P.uniforms ? P.uniforms[r] : 0.5f;
+  const int64_t qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
+                           ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
+                           : -1;
 
   int mode;
   if (greedy) mode = MODE_GREEDY;
@@ -134,38 +188,62 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;
   const bool pen = hlen > 0 && (rep != 1.0f || pres != 0.0f || freq != 0.0f);
   uint32_t cflags = 0;
+  const PenArgs pa{S.u.c.hc, rep, pres, freq};
   if (pen) {
-    if (hlen > 65535) cflags |= CF_HISTORY;  // 16-bit counts: such rows take the general path
-    build_counts(S.u.c.hc, hrow, hlen, hp, lo, n);
-    apply_counts<VEC>(S.u.c.hc, n, rep, pres, freq, x);
+    if (hlen > 65535) cflags |= CF_HISTORY;  // counts are at most 16-bit: such rows take the general path
+    if constexpr (PK) {
+      if (!build_counts<8>(S.u.c.hc, hrow, hlen, hp, lo, n, S)) cflags |= CF_HISTORY;
+      mark_counts(C, n, pa);
+    } else {
+      build_counts<16>(S.u.c.hc, hrow, hlen, hp, lo, n, S);
+      apply_counts(C, n, pa);
+    }
   }
+  const bool wpen = PK && pen && wballot(C.pmask != 0ull) != 0ull;  // this wave holds penalised slots
   LPS_STAMP(1);
 
   // ---- chunk max (NaN aside), NaN flag, greedy argmax, -inf count (slots xd xc xa xf) ----
-  float tm = -INFINITY;
-  uint32_t tnan = 0;
-#pragma unroll
-  for (int s = 0; s < FE; s++) {
-    tm = fmaxf(tm, x[s]);
-    tnan |= x[s] != x[s] ? 1u : 0u;
-  }
-  const float tm_thread = tm;
+  float tm = -INFINITY, tm2 = -INFINITY;  // thread max and (top-k' > 64) second max
+  uint32_t tnan = 0, ninf = 0;
   uint64_t gbest = 0;
-  if (greedy) {
+  const bool want_ninf = mode == MODE_PURE && P.kept_count;
+  const bool want_top2 = kprime > 64;
+  with_pen<PK>(wpen, [&](auto PT) {
+    constexpr bool PEN = decltype(PT)::value;
+    // one loop per case: no per-element branch on a row-uniform condition
+    if (want_top2) {
 #pragma unroll
-    for (int s = 0; s < FE; s++) {
-      const int l = slot_local<VEC>(s);
-      if (l < n) {
-        const uint64_t pk = ((uint64_t)f2key(x[s]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)(lo + l));
-        gbest = pk > gbest ? pk : gbest;
+      for (int s = 0; s < NE; s++) {
+        const float v = C.template val<PEN>(s, pa);
+        tnan |= v != v ? 1u : 0u;
+        if (v > tm) { tm2 = tm; tm = v; }
+        else if (v > tm2) tm2 = v;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NE; s++) {
+        const float v = C.template val<PEN>(s, pa);
+        tnan |= v != v ? 1u : 0u;
+        tm = fmaxf(tm, v);
       }
     }
-  }
-  uint32_t ninf = 0;
-  if (mode == MODE_PURE && P.kept_count) {
+    if (greedy) {
 #pragma unroll
-    for (int s = 0; s < FE; s++) ninf += (slot_local<VEC>(s) < n && x[s] == -INFINITY) ? 1u : 0u;
-  }
+      for (int s = 0; s < NE; s++) {
+        const int l = CK::local(s);
+        if (l < n) {
+          const uint64_t pk = ((uint64_t)f2key(C.template val<PEN>(s, pa)) << 32) |
+                              (uint64_t)(0xFFFFFFFFu - (uint32_t)(lo + l));
+          gbest = pk > gbest ? pk : gbest;
+        }
+      }
+    }
+    if (want_ninf) {
+#pragma unroll
+      for (int s = 0; s < NE; s++) ninf += (CK::local(s) < n && C.template val<PEN>(s, pa) == -INFINITY) ? 1u : 0u;
+    }
+  });
+  const float tm_thread = tm;
   {
     const float wmx = wmax(tm);
     const uint32_t wnan = wreduce(tnan, OpOr{});
@@ -199,21 +277,24 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (need_sum && xm_finite) {
     const float wm = __fmul_rn(xm, c);
     btop = (int)floorf(__fmul_rn(wm, (float)HS));
-    if (mode == MODE_NUCLEUS) {
+    with_pen<PK>(wpen, [&](auto PT) {
+      constexpr bool PEN = decltype(PT)::value;
+      if (mode == MODE_NUCLEUS) {
 #pragma unroll
-      for (int s = 0; s < FE; s++) {
-        const float w = __fmul_rn(x[s], c);
-        const float e = exp2f(__fsub_rn(w, wm));
-        acc += (double)e;
-        if (e > 0.0f) {
-          const int hb = btop - (int)floorf(__fmul_rn(w, (float)HS));
-          if (hb < HB) atomicAdd(&S.u.c.hm[hb], (unsigned long long)mass_fixed(e));
+        for (int s = 0; s < NE; s++) {
+          const float w = __fmul_rn(C.template val<PEN>(s, pa), c);
+          const float e = exp2f(__fsub_rn(w, wm));
+          acc += (double)e;
+          if (e > 0.0f) {
+            const int hb = btop - (int)floorf(__fmul_rn(w, (float)HS));
+            if (hb < HB) atomicAdd(&S.u.c.hm[hb], (unsigned long long)mass_fixed(e));
+          }
         }
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int s = 0; s < FE; s++) acc += (double)exp2f(__fsub_rn(__fmul_rn(x[s], c), wm));
-    }
+        for (int s = 0; s < NE; s++) acc += (double)exp2f(__fsub_rn(__fmul_rn(C.template val<PEN>(s, pa), c), wm));
+      }
+    });
   }
   LPS_STAMP(3);
 
@@ -225,24 +306,18 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (kprime > 0) {
     const uint32_t m = (uint32_t)((kprime + FW - 1) / FW);
     uint32_t th;
-    if (kprime <= 64) {
+    if (!want_top2) {
       const uint32_t v1[1] = {f2key(tm_thread)};
       th = wave_kth_largest<1>(v1, m);
     } else {
-      float m1 = -INFINITY, m2 = -INFINITY;
-#pragma unroll
-      for (int s = 0; s < FE; s++) {
-        const float xv = x[s];
-        if (xv > m1) { m2 = m1; m1 = xv; }
-        else if (xv > m2) m2 = xv;
-      }
-      const uint32_t v2[2] = {f2key(m1), f2key(m2)};
+      const uint32_t v2[2] = {f2key(tm_thread), f2key(tm2)};
       th = wave_kth_largest<2>(v2, m);
     }
     if (lane == 0) S.xg[wv] = th;
   }
+  LPS_STAMP(25);
   __syncthreads();
-  const float zsum = (float)(S.xe[0] + S.xe[1] + S.xe[2] + S.xe[3]);
+  const double zsum = S.xe[0] + S.xe[1] + S.xe[2] + S.xe[3];
 
   // ---- local candidates: every element >= the weakest wave threshold (slot xh) ----
   uint32_t ncand = 0;
@@ -250,19 +325,30 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     uint32_t th = min(min(S.xg[0], S.xg[1]), min(S.xg[2], S.xg[3]));
     if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
     const float xth = key2f(th);
+    LPS_STAMP(26);
     uint32_t cnt = 0;
+    with_pen<PK>(wpen, [&](auto PT) {
+      constexpr bool PEN = decltype(PT)::value;
 #pragma unroll
-    for (int s = 0; s < FE; s++) cnt += (slot_local<VEC>(s) < n && x[s] >= xth) ? 1u : 0u;
+      for (int s = 0; s < NE; s++) cnt += (CK::local(s) < n && C.template val<PEN>(s, pa) >= xth) ? 1u : 0u;
+    });
     uint32_t tot;
     uint32_t p = bscan_excl<uint32_t>(cnt, &tot, S.xh);
+    LPS_STAMP(27);
     uint2* out = cands + (int64_t)j * PUBCAP;
+    if (cnt) {
+      with_pen<PK>(wpen, [&](auto PT) {
+        constexpr bool PEN = decltype(PT)::value;
 #pragma unroll
-    for (int s = 0; s < FE; s++) {
-      const int l = slot_local<VEC>(s);
-      if (l < n && x[s] >= xth) {
-        if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(x[s]), (uint32_t)(lo + l));
-        p++;
-      }
+        for (int s = 0; s < NE; s++) {
+          const float v = C.template val<PEN>(s, pa);
+          const int l = CK::local(s);
+          if (l < n && v >= xth) {
+            if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(v), (uint32_t)(lo + l));
+            p++;
+          }
+        }
+      });
     }
     ncand = tot > (uint32_t)PUBCAP ? (uint32_t)PUBCAP : tot;
     if (tot > (uint32_t)PUBCAP) cflags |= CF_OVERFLOW;
@@ -273,7 +359,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (tid == 0) {
     ChunkSum1 a;
     a.mkey = mkey; a.amax = amax; a.zsum = zsum; a.btop = btop; a.ninf = ninf; a.flags = cflags;
-    a.pad[0] = a.pad[1] = 0;
+    a.pad = 0;
     s1[j] = a;
   }
 
@@ -298,7 +384,14 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     }
     __syncthreads();
     LPS_STAMP(5);
-    // wave 0: chunk reference -> row reference factors, the row mass Z
+    // Every chunk's relative bin tid (up to 32 chunks per round) is loaded together
+    // with the chunk summaries; the bins are then merged in absolute position,
+    // rescaled to the row maximum, in fixed point (order-independent sums).
+    float hv[32];
+    const int g0 = G < 32 ? G : 32;
+#pragma unroll
+    for (int k = 0; k < 32; k++)
+      if (k < g0) hv[k] = hist[(int64_t)k * HB + tid];
     if (wv == 0) {
       ChunkSum1 a{};
       if (lane < G) a = s1[lane];
@@ -309,25 +402,36 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       const float xq = key2f(a.mkey);
       const bool qfin = lane < G && a.mkey != 0xFFFFFFFFu && xq != INFINITY && xq != -INFINITY;
       const double sc = (rfin && qfin) ? exp2((double)__fmul_rn(xq, c) - (double)wg) : 0.0;
-      const double Z = wsum((double)a.zsum * sc);
+      const double Z = wsum(a.zsum * sc);
       if (lane < G) { S.u.c.scale[lane] = sc; S.u.c.btop[lane] = a.btop; }
       if (lane == 0) { S.md[0] = Z; S.mi[10] = rfin ? (int)floorf(__fmul_rn(wg, (float)HS)) : 0; S.mi[11] = rfin ? 1 : 0; }
     }
+    S.u.c.gm[tid] = 0ull;
     __syncthreads();
     const bool rfin = S.mi[11] != 0;
     const int btg = S.mi[10];
     const double Z = S.md[0];
     const double Pm = (double)topp * Z;
-    // merged mass of absolute bin btg - tid (slot xd)
-    double m = 0.0;
+    constexpr double kGm = 1099511627776.0;  // 2^40
     if (rfin) {
-#pragma unroll 8
-      for (int q = 0; q < G; q++) {
-        const int idx = tid - (btg - S.u.c.btop[q]);
+#pragma unroll
+      for (int k = 0; k < 32; k++) {
+        if (k < g0) {
+          const int a = tid + (btg - S.u.c.btop[k]);
+          const double sc = S.u.c.scale[k];
+          if (sc > 0.0 && a < HB && hv[k] > 0.0f) atomicAdd(&S.u.c.gm[a], (unsigned long long)((double)hv[k] * sc * kGm));
+        }
+      }
+      for (int q = 32; q < G; q++) {  // rows of more than 32 chunks
+        const int a = tid + (btg - S.u.c.btop[q]);
         const double sc = S.u.c.scale[q];
-        if (sc > 0.0 && idx >= 0 && idx < HB) m += (double)hist[(int64_t)q * HB + idx] * sc;
+        const float h = hist[(int64_t)q * HB + tid];
+        if (sc > 0.0 && a < HB && h > 0.0f) atomicAdd(&S.u.c.gm[a], (unsigned long long)((double)h * sc * kGm));
       }
     }
+    __syncthreads();
+    // merged mass of absolute bin btg - tid (slot xd)
+    const double m = (double)S.u.c.gm[tid] / kGm;
     double mtot;
     const double ex = bscan_excl<double>(m, &mtot, S.xd);
     // bins whose cumulative interval meets [Pm - eps, Pm + eps] (slots xg xh)
@@ -351,16 +455,20 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       const int hbt = btop - (bhi + 1);  // chunk histogram bins 0..hbt lie above the region
       uint64_t am = (xm_finite && tid <= hbt) ? (uint64_t)S.u.c.hm[tid] : 0ull;
       uint32_t na = 0, nc = 0, inreg = 0;
+      with_pen<PK>(wpen, [&](auto PT) {
+        constexpr bool PEN = decltype(PT)::value;
 #pragma unroll
-      for (int s = 0; s < FE; s++) {
-        if (x[s] != -INFINITY) {
-          const int b = wbin(x[s], c);
-          na += b > bhi ? 1u : 0u;
-          const bool in = b >= blo && b <= bhi;
-          nc += in ? 1u : 0u;
-          inreg |= in ? (1u << s) : 0u;
+        for (int s = 0; s < NE; s++) {
+          const float v = C.template val<PEN>(s, pa);
+          if (v != -INFINITY) {
+            const int b = wbin(v, c);
+            na += b > bhi ? 1u : 0u;
+            const bool in = b >= blo && b <= bhi;
+            nc += in ? 1u : 0u;
+            if (NE <= 32) inreg |= in ? (1u << (s & 31)) : 0u;
+          }
         }
-      }
+      });
       am = wsum(am);
       na = wsum(na);
       if (lane == 0) { S.xa[wv] = am; S.xb[wv] = na; }
@@ -369,12 +477,27 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       above = S.xa[0] + S.xa[1] + S.xa[2] + S.xa[3];
       nabove = (uint32_t)(S.xb[0] + S.xb[1] + S.xb[2] + S.xb[3]);
       uint2* out = cands + (int64_t)j * PUBCAP;
+      if (nc) {
+        with_pen<PK>(wpen, [&](auto PT) {
+          constexpr bool PEN = decltype(PT)::value;
 #pragma unroll
-      for (int s = 0; s < FE; s++) {
-        if ((inreg >> s) & 1u) {
-          if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(x[s]), (uint32_t)(lo + slot_local<VEC>(s)));
-          p++;
-        }
+          for (int s = 0; s < NE; s++) {
+            bool in;
+            float v;
+            if constexpr (NE <= 32) {
+              in = (inreg >> s) & 1u;
+              v = in ? C.template val<PEN>(s, pa) : 0.0f;
+            } else {
+              v = C.template val<PEN>(s, pa);
+              const int b = v != -INFINITY ? wbin(v, c) : (blo - 1);
+              in = b >= blo && b <= bhi;
+            }
+            if (in) {
+              if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(v), (uint32_t)(lo + CK::local(s)));
+              p++;
+            }
+          }
+        });
       }
       ncand = ctot > (uint32_t)PUBCAP ? (uint32_t)PUBCAP : ctot;
       if (ctot > (uint32_t)PUBCAP) cflags |= CF_OVERFLOW;
@@ -424,15 +547,18 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     const double wgd = rfin ? (double)__fmul_rn(xg, c) : 0.0;
     const float xq = key2f(a.mkey);
     const bool qfin = lane < G && a.mkey != 0xFFFFFFFFu && xq != INFINITY && xq != -INFINITY;
-    const double sc = (rfin && qfin) ? exp2((double)__fmul_rn(xq, c) - wgd) : 0.0;
-    const double Zfull = wsum((double)a.zsum * sc);
+    const float wq = (rfin && qfin) ? __fmul_rn(xq, c) : 0.0f;
+    const double sc = (rfin && qfin) ? exp2((double)wq - wgd) : 0.0;
+    const double Zfull = wsum(a.zsum * sc);
     const double abv = (double)b.above / (double)kMassScale * sc;
     const double A = wsum(abv);
     if (lane < G) {
       S.u.f.pre[lane] = ncinc - nc;
       S.u.f.scale[lane] = sc;
+      S.u.f.wm[lane] = wq;
       S.u.f.abvm[lane] = abv;
-      S.u.f.keptm[lane] = (double)a.zsum * sc;
+      S.u.f.keptm[lane] = a.zsum * sc;
+      S.u.f.keptf[lane] = 0ull;
     }
     if (lane == 0) {
       S.u.f.pre[G] = NC;
@@ -472,10 +598,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     else if (xmax == -INFINITY) status |= LPS_ROW_EMPTY;
   }
   const double lnZ = Zfull > 0.0 ? log(Zfull) : 0.0;
-  const int64_t qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
-                           ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
-                           : -1;
-  float u = P.uniforms ? P.uniforms[r] : 0.5f;
+  float u = u_row;
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0.99999994f;
 
@@ -484,34 +607,32 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   int32_t ties = -1, kept_n = 0;
   int ntop_out = 0;  // entries of the sorted kept list that are top logprobs
 
-  // Candidates in registers: thread t holds concatenated positions [t*FCPT, t*FCPT + np).
-  uint32_t ck[FCPT], cx[FCPT];
-  int32_t ci[FCPT];
-  int np = 0;
-  auto load_cands = [&]() {
-    const int i0 = tid * FCPT;
-    np = NC - i0;
-    np = np < 0 ? 0 : (np > FCPT ? FCPT : np);
+  // Candidate i (concatenated over chunks in chunk order) sits in slot
+  // i - pre[q] of chunk q, the last chunk with pre[q] <= i.
+  auto cand_at = [&](int i) -> uint2 {
     int q = 0;
-    if (np > 0) {
-      int a = 0, b = G - 1;  // last chunk with pre <= i0
-      while (a < b) {
-        const int mid = (a + b + 1) >> 1;
-        if ((int)S.u.f.pre[mid] <= i0) a = mid; else b = mid - 1;
-      }
-      q = a;
-    }
-    int nb = np > 0 ? (int)S.u.f.pre[q + 1] : 0;
+#pragma unroll
+    for (int step = MAXG / 2; step > 0; step >>= 1)
+      if (q + step < G && (int)S.u.f.pre[q + step] <= i) q += step;
+    return cands[(int64_t)q * PUBCAP + (i - (int)S.u.f.pre[q])];
+  };
+  // Candidates in registers: thread t holds candidate e * FT + t in slot e (z key, index).
+  uint32_t ck[FCPT];
+  int32_t ci[FCPT];
+  const int np = NC > tid ? min((NC - tid + FT - 1) / FT, FCPT) : 0;
+  // All loads first (clamped to a valid candidate, no branch between them), then the keys.
+  auto load_cands = [&]() {
+    const int npmax = min((NC + FT - 1) / FT, FCPT);  // slots any thread uses
+    uint2 cv[FCPT];
+#pragma unroll
+    for (int e = 0; e < FCPT; e++)
+      if (e < npmax) cv[e] = cand_at(min(e * FT + tid, NC - 1));
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
-      cx[e] = 0u;
-      ci[e] = -1;
-      if (e < np) {
-        while (i0 + e >= nb) { q++; nb = (int)S.u.f.pre[q + 1]; }
-        const uint2 cv = cands[(int64_t)q * PUBCAP + (i0 + e - (int)S.u.f.pre[q])];
-        cx[e] = cv.x;
-        ci[e] = (int32_t)cv.y;
-      }
+      const bool pr = e < np;
+      const float xv = key2f(pr ? cv[e].x : 0u);
+      ck[e] = pr ? f2key(greedy ? xv : __fdiv_rn(xv, T)) : 0u;
+      ci[e] = pr ? (int32_t)cv[e].y : -1;
     }
   };
 
@@ -519,16 +640,13 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     // ---------------- top-k (and top-N logprobs) ----------------
     if (NC > FCAP) return 512;
     load_cands();
-#pragma unroll
-    for (int e = 0; e < FCPT; e++) {
-      const float xv = key2f(cx[e]);
-      ck[e] = e < np ? f2key(greedy ? xv : __fdiv_rn(xv, T)) : 0u;
-    }
+    LPS_STAMP(22);
     const int keff = mode == MODE_TOPK ? (topk < V ? topk : V) : 0;
     int kc = keff > ntop ? keff : ntop;
     if (kc > NC) kc = NC;
     if (kc <= 0) return 16;
     const uint32_t zc = sel_count(ck, np, (uint32_t)kc, S);
+    LPS_STAMP(23);
     // collect z >= zc into the kept list (slot xh)
     uint32_t cnt = 0;
 #pragma unroll
@@ -540,16 +658,17 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       if (e < np && ck[e] >= zc) {
-        kl.kkey[p] = ck[e];
-        kl.kx[p] = cx[e];
+        kl.skey[p] = ((uint64_t)ck[e] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)ci[e]);
         kl.kidx[p] = ci[e];
         kl.km[p] = mass_fixed(mass_f(key2f(ck[e]), zmax));
         p++;
       }
     }
     __syncthreads();
+    LPS_STAMP(24);
     const int K = (int)Kall;
     rank_sort_kept(K, S);
+    auto kz = [&](int slot) -> uint32_t { return (uint32_t)(kl.skey[slot] >> 32); };
     ntop_out = ntop < K ? ntop : K;
     LPS_STAMP(16);
     if (mode == MODE_GREEDY) {
@@ -562,11 +681,11 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     } else {
       // the top-k set: sorted positions whose key reaches the keff-th largest
       if (keff > K) return 16;
-      const uint32_t kth = kl.kkey[kl.kord[keff - 1]];
+      const uint32_t kth = kz(kl.kord[keff - 1]);
       if (tid == 0) S.mi[20] = K;
       __syncthreads();
       for (int pz = tid; pz < K; pz += FT)
-        if (kl.kkey[kl.kord[pz]] >= kth && (pz == K - 1 || kl.kkey[kl.kord[pz + 1]] < kth)) S.mi[20] = pz + 1;
+        if (kz(kl.kord[pz]) >= kth && (pz == K - 1 || kz(kl.kord[pz + 1]) < kth)) S.mi[20] = pz + 1;
       __syncthreads();
       const int nk = S.mi[20];
       sorted_prefix(nk, S);
@@ -587,8 +706,8 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         if (tid == 0) S.mi[22] = nf;
         __syncthreads();
         for (int pz = tid; pz < nf; pz += FT) {
-          const bool ok = mass_f(key2f(kl.kkey[kl.kord[pz]]), zmax) >= minp;
-          const bool okp = pz == 0 || mass_f(key2f(kl.kkey[kl.kord[pz - 1]]), zmax) >= minp;
+          const bool ok = mass_f(key2f(kz(kl.kord[pz])), zmax) >= minp;
+          const bool okp = pz == 0 || mass_f(key2f(kz(kl.kord[pz - 1])), zmax) >= minp;
           if (!ok && okp) S.mi[22] = pz;
         }
         __syncthreads();
@@ -599,12 +718,12 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       if (status == 0 && typp < 1.0f) nf = 1;
       if (status == 0) {
         const uint64_t Zf = kl.cum[nf - 1];
-        const uint32_t ckey = kl.kkey[kl.kord[nf - 1]];
+        const uint32_t ckey = kz(kl.kord[nf - 1]);
         cut = key2f(ckey);
         if (P.kept_ties || P.kept_count) {  // (slots xc xf xg)
           uint32_t ea = 0, ek = 0, nfin = 0;
           for (int q = tid; q < K; q += FT) {
-            const uint32_t kq = kl.kkey[kl.kord[q]];
+            const uint32_t kq = kz(kl.kord[q]);
             ea += kq == ckey ? 1u : 0u;
             ek += (kq == ckey && q < nf) ? 1u : 0u;
             nfin += (q < nf && kq != kNegInfKey) ? 1u : 0u;
@@ -618,14 +737,18 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
           ties = ek == ea ? -1 : (int32_t)ek;
           kept_n = (int32_t)nfin;
         }
-        // vocabulary order over the kept prefix
+        // vocabulary order over the kept prefix: the kept indices in sorted order
+        // (in iord), then each one's rank among them
+        for (int pz = tid; pz < nf; pz += FT) kl.iord[pz] = kl.kidx[kl.kord[pz]];
+        __syncthreads();
+        int rk0 = -1, rk1 = -1;
         for (int pz = tid; pz < nf; pz += FT) {
-          const int si = kl.kord[pz];
-          const int ii = kl.kidx[si];
-          int rk = 0;
-          for (int q = 0; q < nf; q++) rk += kl.kidx[kl.kord[q]] < ii ? 1 : 0;
-          kl.iord[rk] = si;
+          const int rk = count_below(kl.iord, nf, kl.iord[pz]);
+          if (pz == tid) rk0 = rk; else rk1 = rk;
         }
+        __syncthreads();
+        if (tid < nf) kl.iord[rk0] = kl.kord[tid];
+        if (tid + FT < nf) kl.iord[rk1] = kl.kord[tid + FT];
         if (tid == 0) { S.mi[23] = -1; S.mi[24] = -1; }
         __syncthreads();
         // inverse CDF in vocabulary order: thread t holds positions 2t, 2t+1 (slot xb)
@@ -645,7 +768,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         __syncthreads();
         const int ps = S.mi[23] >= 0 ? S.mi[23] : kl.iord[nf - 1];
         token = kl.kidx[ps];
-        chosen_z = key2f(kl.kkey[ps]);
+        chosen_z = key2f(kz(ps));
         if (S.mi[24] >= 0) qprob = (float)((double)kl.km[S.mi[24]] / (double)Zf);
       }
     }
@@ -667,13 +790,11 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       // exact cut among the region candidates, above-region masses rescaled to the row
       if (NC > FCAP) return 64;
       load_cands();
-#pragma unroll
-      for (int e = 0; e < FCPT; e++) ck[e] = e < np ? f2key(__fdiv_rn(key2f(cx[e]), T)) : 0u;
       auto cmass = [&](int e) -> uint64_t { return mass_fixed(mass_f(key2f(ck[e]), zmax)); };
       const uint64_t Af = (uint64_t)(Aabove * (double)kMassScale);
       const uint64_t Pf = (uint64_t)((double)topp * Zfull * (double)kMassScale);
       LPS_STAMP(16);
-      const MassSel ms = sel_mass(ck, np, zmax, Af, Pf, S);
+      const MassSel ms = sel_mass(ck, np, cmass, Af, Pf, S);
       LPS_STAMP(17);
       if (!ms.ok || ms.ceq == 0) return 64;
       vkey = ms.key;
@@ -697,15 +818,13 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         __syncthreads();
         for (int i = tid; i < (int)ttot; i += FT) {
           const int ii = kl.kidx[i];
-          int rk = 0;
-          for (int q = 0; q < (int)ttot; q++) rk += kl.kidx[q] < ii ? 1 : 0;
-          if (rk == (int)n_tie - 1) S.mi[25] = ii;
+          if (count_below(kl.kidx, (int)ttot, ii) == (int)n_tie - 1) S.mi[25] = ii;
         }
       }
-      // any x of the cut's collision group
+      // any x of the cut's collision group (reloaded: x keys are not kept in registers)
 #pragma unroll
       for (int e = 0; e < FCPT; e++)
-        if (e < np && ck[e] == vkey) S.mi[26] = (int)cx[e];
+        if (e < np && ck[e] == vkey) S.mi[26] = (int)cand_at(e * FT + tid).x;
       __syncthreads();
       tie_lim = S.mi[25];
       LPS_STAMP(18);
@@ -724,43 +843,26 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         const int bl = wbin(xl, c), bh = wbin(xh, c);
         S.mi[27] = (bl >= blo && bh <= bhi) ? 1 : 0;
       }
-      // kept candidate mass and count; prefix at chunk boundaries (slots xa xg)
-      uint64_t lm = 0;
+      // kept candidate mass per chunk and count (slot xg)
       uint32_t lc = 0;
 #pragma unroll
       for (int e = 0; e < FCPT; e++) {
         const bool kept = e < np && (ck[e] > vkey || (ck[e] == vkey && ci[e] <= tie_lim));
-        const uint64_t m = kept ? cmass(e) : 0ull;
-        lm += m;
-        lc += kept ? 1u : 0u;
-        if (kept && (int64_t)ci[e] == qtok) S.md[6] = (double)m / (double)kMassScale;
-      }
-      {
-        const uint32_t wl = wsum(lc);
-        if (lane == 0) S.xg[wv] = wl;
-      }
-      uint64_t mtot;
-      uint64_t run = bscan_excl<uint64_t>(lm, &mtot, S.xa);
-      const int i0 = tid * FCPT;
-#pragma unroll
-      for (int e = 0; e < FCPT; e++) {
-        if (e < np) {
-          const int q = ci[e] / FCH;
-          if (i0 + e == (int)S.u.f.pre[q]) S.u.f.epre[q] = run;
-          const bool kept = ck[e] > vkey || (ck[e] == vkey && ci[e] <= tie_lim);
-          run += kept ? cmass(e) : 0ull;
-          if (i0 + e == (int)S.u.f.pre[q + 1] - 1) S.u.f.eend[q] = run;
+        if (kept) {
+          const uint64_t m = cmass(e);
+          atomicAdd(&S.u.f.keptf[ci[e] / CH], (unsigned long long)m);
+          if ((int64_t)ci[e] == qtok) S.md[6] = (double)m / (double)kMassScale;
+          lc++;
         }
       }
+      lc = wsum(lc);
+      if (lane == 0) S.xg[wv] = lc;
       __syncthreads();
       if (!S.mi[27]) return 128;
       kept_n = (int32_t)(nab_all + S.xg[0] + S.xg[1] + S.xg[2] + S.xg[3]);
       qmass = S.md[6];
-      if (wv == 0 && lane < G) {
-        const uint32_t ncq = S.u.f.pre[lane + 1] - S.u.f.pre[lane];
-        const double cmq = ncq ? (double)(S.u.f.eend[lane] - S.u.f.epre[lane]) / (double)kMassScale : 0.0;
-        S.u.f.keptm[lane] = S.u.f.abvm[lane] + cmq;
-      }
+      if (wv == 0 && lane < G)
+        S.u.f.keptm[lane] = S.u.f.abvm[lane] + (double)S.u.f.keptf[lane] / (double)kMassScale;
       __syncthreads();
       ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
       cut = key2f(vkey);
@@ -782,34 +884,44 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     const int js = S.mi[28];
     const double start = S.md[3], Zf = S.md[4], target = S.md[5];
     if (!P.skip_draw) {
-      const int lo2 = js * FCH;
-      const int n2 = (V - lo2) < FCH ? (V - lo2) : FCH;
+      const int lo2 = js * CH;
+      const int n2 = (V - lo2) < CH ? (V - lo2) : CH;
+      const float wmj = S.u.f.wm[js];
+      const double scj = S.u.f.scale[js];
       HistPrefetch hp2;
       prefetch_history(hrow, P.history_stride, hp2);
-      float y[FE];
-      load_chunk<DT, VEC>(row, lo2, n2, y);
-      if (pen) {
-        build_counts(S.u.f.x.hc, hrow, hlen, hp2, lo2, n2);
-        apply_counts<VEC>(S.u.f.x.hc, n2, rep, pres, freq, y);
+      CK Y;
+      Y.load(row, lo2, n2);
+      const PenArgs pa2{S.u.f.x.hc, rep, pres, freq};
+      if (pen) {  // (a row whose counts did not fit never reaches the finaliser)
+        if constexpr (PK) {
+          build_counts<8>(S.u.f.x.hc, hrow, hlen, hp2, lo2, n2, S);
+          mark_counts(Y, n2, pa2);
+        } else {
+          build_counts<16>(S.u.f.x.hc, hrow, hlen, hp2, lo2, n2, S);
+          apply_counts(Y, n2, pa2);
+        }
       }
       LPS_STAMP(21);
-      auto kept_of = [&](float yv, float z) -> bool {
-        if (z == -INFINITY || yv != yv) return false;
-        if (mode == MODE_PURE) return true;
-        const int b = wbin(yv, c);
-        if (b > bhi) return true;
-        if (b < blo) return false;
-        const uint32_t kz = f2key(z);
-        return kz > vkey;  // ties at the cut handled by index below
-      };
-      auto kept_m = [&](int v, int e) -> double {  // kept mass of slot (v, e), 0 if not kept
-        const float yv = y[v * VEC + e];
-        const float z = __fdiv_rn(yv, T);
-        const int gi = lo2 + (v * FT + tid) * VEC + e;
-        const bool kept = kept_of(yv, z) ||
-                          (mode == MODE_NUCLEUS && z != -INFINITY && f2key(z) == vkey && gi <= tie_lim &&
-                           wbin(yv, c) >= blo && wbin(yv, c) <= bhi);
-        return kept ? (double)mass_f(z, zmax) : 0.0;
+      // Kept mass of slot (v, e) with the formulas that built the chunk's kept
+      // mass: exp2(x c - wm) * scale outside the cut region (as the chunk pass
+      // summed it), the finaliser's exp(z - zmax) for region candidates.
+      auto kept_m = [&](int v, int e) -> double {
+        const float yv = Y.template val<true>(v * VEC + e, pa2);
+        if (yv == -INFINITY || yv != yv) return 0.0;
+        const float w = __fmul_rn(yv, c);
+        if (mode == MODE_NUCLEUS) {
+          const int b = (int)floorf(__fmul_rn(w, (float)HS));
+          if (b < blo) return 0.0;
+          if (b <= bhi) {
+            const float z = __fdiv_rn(yv, T);
+            const uint32_t kz = f2key(z);
+            const int gi = lo2 + (v * FT + tid) * VEC + e;
+            if (!(kz > vkey || (kz == vkey && gi <= tie_lim))) return 0.0;
+            return (double)mass_fixed(mass_f(z, zmax)) / (double)kMassScale;
+          }
+        }
+        return (double)exp2f(__fsub_rn(w, wmj)) * scj;
       };
       // Vocabulary order is (v, thread, e).  Groups are scanned in batches of NB;
       // each thread keeps its first group whose cumulative end passes the target
@@ -879,7 +991,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
             const double m = kept_m(vv, e);
             if (m > 0.0) {
               lp = lo2 + (vv * FT + tid) * VEC + e;
-              lz = __fdiv_rn(y[vv * VEC + e], T);
+              lz = __fdiv_rn(Y.template val<true>(vv * VEC + e, pa2), T);
               if (found && target < a + m) done = true;
               a += m;
             }
@@ -919,7 +1031,8 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     for (int q = tid; q < P.n_top; q += FT) {
       if (q < ntop_out) {
         const int si = kl.kord[q];
-        P.top_logprobs[(int64_t)r * P.n_top + q] = (float)((double)__fsub_rn(key2f(kl.kkey[si]), zmax) - lnZ);
+        P.top_logprobs[(int64_t)r * P.n_top + q] =
+            (float)((double)__fsub_rn(key2f((uint32_t)(kl.skey[si] >> 32)), zmax) - lnZ);
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = kl.kidx[si];
       } else {
         P.top_logprobs[(int64_t)r * P.n_top + q] = -INFINITY;
