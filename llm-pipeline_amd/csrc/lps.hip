@@ -81,10 +81,34 @@ FastWs fast_layout(void* base, int R, int V) {
   return w;
 }
 
+// Grids of at most this many chunk workgroups take the fused kernel (row
+// finalisers overlap other rows' chunk work); larger ones the split pair,
+// whose chunk kernel keeps more workgroups resident per CU.
+#ifndef LPS_FUSED_MAX_WG
+#define LPS_FUSED_MAX_WG 2048
+#endif
+
 template <int DT, int VEC>
 hipError_t launch_fast(const FParams& F, int rows_pad, hipStream_t s) {
-  hipLaunchKernelGGL((fast_kernel<DT, VEC>), dim3((unsigned)(rows_pad * F.G)), dim3(FT), 0, s, F);
-  return hipGetLastError();
+  const unsigned grid = (unsigned)(rows_pad * F.G);
+  hipError_t e;
+  if (VEC > 1 && grid <= (unsigned)LPS_FUSED_MAX_WG) {  // (element-wise variants: split, fewer registers)
+    hipLaunchKernelGGL((fused_kernel<DT, VEC>), dim3(grid), dim3(FT), 0, s, F);
+    e = hipGetLastError();
+  } else {
+    hipLaunchKernelGGL((chunk_kernel<DT, VEC>), dim3(grid), dim3(FT), 0, s, F);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((final_kernel<DT, VEC>), dim3((unsigned)F.k.R), dim3(FT), 0, s, F);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  // rows the finaliser deferred: the general algorithm, one 1024-thread
+  // workgroup per row (the others return at once)
+  KParams G = F.k;
+  G.only_status = F.status;
+  G.plans = nullptr;
+  return launch_gen<DT, VEC>(G, s);
 }
 
 hipError_t dispatch_fast(int dtype, bool vec, const FParams& F, int rows_pad, hipStream_t s) {
@@ -123,8 +147,9 @@ KParams row_block(const KParams& P, int r0, int nr, int es) {
   return B;
 }
 
-// Runs the fast kernel (rows it cannot finish exactly fall back to the general
-// algorithm inside it), or the general kernel when asked or without workspace.
+// Runs the fast kernels (rows they cannot finish exactly go to the general
+// kernel launched after them), or only the general kernel when asked or
+// without workspace.
 hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws_bytes, int flags, hipStream_t s) {
   const FastWs need = fast_layout(nullptr, P.R, P.V);
   if ((flags & LPS_FLAG_GENERIC) || !ws || ws_bytes < need.bytes) return dispatch_gen(dtype, vec, P, s);

@@ -1,15 +1,17 @@
-// Fast row sampler: every row is split into G chunks of 8192 logits, one
+// Fast row sampler in two kernels.
+//
+// chunk_kernel: every row is split into G chunks of 8192 logits, one
 // 256-thread workgroup per chunk, the chunk held in registers (the logits are
 // read from HBM once; only the chunk that holds the draw of a nucleus / pure
 // row is read a second time, by the row's finaliser, normally from the L2).
+// Each chunk publishes a summary (max, mass, histogram top bin) and, depending
+// on the row's mode, candidates.  Workgroup ids are dispatched round-robin over
+// the XCDs, and chunk workgroups of a row are given ids congruent modulo 8, so
+// a row's chunks share one L2: nucleus rows pass one intra-row barrier there.
 //
-// Placement: workgroup ids are dispatched round-robin over the XCDs, so chunk
-// workgroups of a row are given ids congruent modulo 8.  They then share one
-// L2, and their partial results meet there: a workgroup publishes with plain
-// stores (write-through L1 -> L2), waits for them, and counts its arrival with
-// a global atomic; the last arrival of a row finalises it.  No agent-scope
-// release fence (an L2 write-back) is ever issued.  A row whose chunks were
-// not all seen on one XCD is finished by the general algorithm instead.
+// final_kernel: one workgroup per row reads the row's chunk summaries and
+// candidates (published by the previous kernel, so visible to every XCD) and
+// finishes the row.
 //
 // Row modes (decided per row from its parameters):
 //   GREEDY  T <= 0: first argmax (plus logprobs).
@@ -21,23 +23,27 @@
 //   PURE    top_k off and no other filter: no cut; the finaliser picks the
 //           chunk holding the draw from per-chunk masses and rescans it.
 //   NUCLEUS top_k off, top_p < 1: chunks publish a fine mass histogram, pass
-//           one intra-XCD barrier, all derive the same cut region (the bins
+//           one intra-row barrier, all derive the same cut region (the bins
 //           whose cumulative mass meets top_p within a tolerance band), and
 //           publish the candidates inside it plus their exact mass above it;
 //           the finaliser makes the exact cut by a mass-weighted radix select
 //           and rescans the chunk holding the draw.
 // A row the fast path cannot finish exactly (e.g. a flat row whose cut region
 // holds more candidates than fit, min-p / typical-p without top-k, top_k above
-// FAST_KMAX) is flagged LPS_ROW_DEFERRED and runs the general algorithm in the
-// same workgroup.
+// FAST_KMAX) is flagged LPS_ROW_DEFERRED in the workspace status and sampled by
+// the general kernel, launched after the finaliser with that status as filter.
 #pragma once
 
 #include "lps_generic.h"
 #include "lps_wave.h"
 
-// Phase marks inside the fast kernel; empty unless a timing build defines it.
+// Phase marks inside the chunk and finaliser code (LPS_FSTAMP refers to the
+// finalised row r of its scope); empty unless a timing build defines them.
 #ifndef LPS_STAMP
 #define LPS_STAMP(i) ((void)0)
+#endif
+#ifndef LPS_FSTAMP
+#define LPS_FSTAMP(i) ((void)0)
 #endif
 
 namespace lps {
@@ -57,34 +63,33 @@ constexpr int SELB = 1 << SELD;         // count-select histogram bins
 constexpr int SELDM = 10;               // mass-select digit bits
 constexpr int SELBM = 1 << SELDM;       // mass-select histogram bins
 constexpr int HPF = 4;                  // history ids prefetched per thread
-constexpr int WCAP = 256;               // per-wave candidate list capacity
 constexpr int MAXG = 64;                // chunks per row (V <= 524287)
 
 enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEFER = 4 };
 enum { CF_OVERFLOW = 1, CF_HISTORY = 2, CF_SPLIT = 4, CF_REGION = 8 };
-constexpr int32_t LPS_ROW_DEFERRED = 8;  // internal: finished by the general algorithm
 
-struct ChunkSum1 {   // published before the barrier / handoff
+struct ChunkSum1 {   // per chunk, for the finaliser
   uint32_t mkey;     // max key of the penalised logits of the chunk (NaN -> 0xFFFFFFFF)
   int32_t amax;      // greedy rows: first index of that key
   double zsum;       // sum over the chunk of exp2(x c - xmax_chunk c), c = log2(e) / T
   int32_t btop;      // histogram top bin (absolute) of the chunk
   uint32_t ninf;     // -inf logits in the chunk (when counted)
   uint32_t flags;    // CF_*
-  uint32_t pad;
+  uint32_t xcc;      // XCD that ran the chunk
 };
-struct ChunkSum2 {   // published at the handoff
+struct ChunkSum2 {   // published at the end of phase 1
   uint32_t ncand;    // candidates published
   uint32_t flags;    // CF_*
   uint64_t above;    // nucleus: fixed-point mass above the cut region (chunk reference)
   uint32_t nabove;   // nucleus: count above the cut region
-  uint32_t pad[3];
+  int32_t blo, bhi;  // nucleus: the cut region (absolute bins), the same in every chunk
+  uint32_t pad;
 };
 
 struct FParams {
   KParams k;           // per-row parameters and outputs (shared with the general kernel)
   int G;               // chunks per row
-  uint32_t* counters;  // [R * 32]: u64 handoff word at [0..1], barrier arrivals at [2]
+  uint32_t* counters;  // [R * 32]: fused handoff arrivals at [0], nucleus barrier arrivals at [2]; zero between launches
   int32_t* status;     // [R]
   ChunkSum1* sum1;     // row r at sum1 + r * s_stride
   ChunkSum2* sum2;
@@ -94,42 +99,8 @@ struct FParams {
 };
 
 // LDS.  The chunk phase and the finaliser never overlap in one workgroup.
-struct FShared {
-  union {
-    struct {                              // chunk phase
-      uint32_t hc[4096];                  // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
-      unsigned long long hm[HB];          // chunk mass histogram, fixed point
-      unsigned long long gm[HB];          // nucleus region: merged row histogram, fixed point
-      double scale[MAXG];                 // nucleus region: chunk -> row reference
-      int32_t btop[MAXG];
-      uint2 cl[FW][WCAP];                 // per-wave candidate lists (x key, index)
-    } c;
-    struct {                              // finaliser
-      union {
-        uint32_t cnt[2][SELB];            // count select, double-buffered digit histograms
-        struct {
-          uint32_t cnt[2][SELBM];
-          unsigned long long mass[2][SELBM];
-        } selm;                           // mass select
-        struct {
-          uint64_t skey[KEPTCAP];         // (z key << 32) | ~index: larger = earlier in sorted order
-          unsigned long long km[KEPTCAP];
-          int32_t kidx[KEPTCAP];
-          int32_t kord[KEPTCAP];          // sorted position -> slot
-          int32_t iord[KEPTCAP];          // index-order position -> slot
-          unsigned long long cum[KEPTCAP];
-        } k;                              // kept list
-        uint32_t hc[4096];                // rescan history counts
-      } x;
-      uint32_t pre[MAXG + 1];             // candidate prefix over chunks
-      double scale[MAXG];                 // chunk -> row reference
-      float wm[MAXG];                     // chunk max * c (the chunk's mass reference)
-      double keptm[MAXG];                 // kept mass per chunk
-      double abvm[MAXG];                  // nucleus: mass above the region per chunk
-      unsigned long long keptf[MAXG];     // nucleus: kept candidate mass per chunk, fixed point
-    } f;
-  } u;
-  // cross-wave exchange slots (each slot is reused only after an intervening barrier)
+// Cross-wave exchange slots (each slot is reused only after an intervening barrier).
+struct XShared {
   uint64_t xa[FW], xb[FW];
   double xd[FW], xe[FW];
   uint32_t xc[FW], xf[FW], xg[FW], xh[FW];
@@ -137,6 +108,39 @@ struct FShared {
   int32_t mi[32];
   uint64_t m64[8];
   double md[8];
+};
+// chunk_kernel's shared block.
+struct CShared : XShared {
+  uint32_t hc[4096];                      // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
+  unsigned long long hm[HB];              // chunk mass histogram, fixed point
+  unsigned long long gm[HB];              // nucleus region: merged row histogram, fixed point
+  double scale[MAXG];                     // nucleus region: chunk -> row reference
+  int32_t btop[MAXG];
+};
+// final_kernel's shared block.
+struct FShared : XShared {
+  union {
+    uint32_t cnt[2][SELB];                // count select, double-buffered digit histograms
+    struct {
+      uint32_t cnt[2][SELBM];
+      unsigned long long mass[2][SELBM];
+    } selm;                               // mass select
+    struct {
+      uint64_t skey[KEPTCAP];             // (z key << 32) | ~index: larger = earlier in sorted order
+      unsigned long long km[KEPTCAP];
+      int32_t kidx[KEPTCAP];
+      int32_t kord[KEPTCAP];              // sorted position -> slot
+      int32_t iord[KEPTCAP];              // index-order position -> slot
+      unsigned long long cum[KEPTCAP];
+    } k;                                  // kept list
+    uint32_t hc[4096];                    // rescan history counts
+  } x;
+  uint32_t pre[MAXG + 1];                 // candidate prefix over chunks
+  double scale[MAXG];                     // chunk -> row reference
+  float wm[MAXG];                         // chunk max * c (the chunk's mass reference)
+  double keptm[MAXG];                     // kept mass per chunk
+  double abvm[MAXG];                      // nucleus: mass above the region per chunk
+  unsigned long long keptf[MAXG];         // nucleus: kept candidate mass per chunk, fixed point
 };
 
 // ---------------------------------------------------------------------------
@@ -152,10 +156,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
 __device__ __forceinline__ uint32_t ld_l2_u32(uint32_t* p) {
   return atomicCAS(p, 0xFFFFFFFFu, 0xFFFFFFFFu);
 }
-// Atomic adds that return the old value.
-__device__ __forceinline__ uint64_t l2_fetch_add64(uint64_t* p, uint64_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Atomic add that returns the old value.
 __device__ __forceinline__ uint32_t l2_fetch_add(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -325,7 +326,7 @@ __device__ __forceinline__ void prefetch_history(const int32_t* hrow, int64_t st
 // 255).  Ends with a barrier.
 template <int BITS>
 __device__ __forceinline__ bool build_counts(uint32_t* hc, const int32_t* hrow, int hlen, const HistPrefetch& hp,
-                                             int lo, int n, FShared& S) {
+                                             int lo, int n, XShared& S) {
   constexpr int PER = 32 / BITS;  // ids per word
   u32x4* h4 = reinterpret_cast<u32x4*>(hc);
 #pragma unroll
@@ -398,12 +399,6 @@ __device__ __forceinline__ void mark_counts(Chunk<DT, VEC>& C, int n, const PenA
   C.pmask = m;
 }
 
-// Candidate lists: each wave appends its elements to its own LDS list (no
-// atomics), then the block copies the lists to global memory in order.
-struct WaveList {
-  uint32_t count;  // wave-uniform running count
-};
-
 // Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end
 // of the division-collision group of x0, so that "z >= fl(x0 / T)" is
 // "x >= result" for every x.
@@ -457,7 +452,7 @@ __device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np
 
 // kk-th largest present key (1 <= kk <= number present).
 __device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np, uint32_t kk, FShared& S) {
-  auto& H = S.u.f.x.cnt;
+  auto& H = S.x.cnt;
   const SelLevel L = sel_range(ck, np, H[0], SELB, nullptr, S);
   if (L.bits == 0) return L.base;
   constexpr int PER = SELB / FT;
@@ -512,7 +507,7 @@ template <typename MF>
 __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, MF mass, uint64_t A, uint64_t P,
                                             FShared& S) {
   MassSel ms{0, A, 0, 0, 0};
-  auto& H = S.u.f.x.selm;
+  auto& H = S.x.selm;
   const SelLevel L = sel_range(ck, np, H.cnt[0], SELBM, H.mass[0], S);
   constexpr int PER = SELBM / FT;
   uint32_t hi = 0;

@@ -1,12 +1,15 @@
-// The fast row-sampling kernel (layout, modes and protocol: lps_fast.h).
+// The fast row-sampling kernels (layout, modes and protocol: lps_fast.h).
 //
-// Visibility of published data: a row's summaries, histograms and candidates
-// live in per-row regions padded to whole 128-byte lines.  Each item is
-// written once per launch and read only after its writer has waited for its
-// stores and then passed the barrier or the handoff atomic.  A workgroup never
-// reads a line before its final value is in the L2, so plain loads cannot hit
-// a stale L1 line (the L1 is invalidated at every kernel start).  Counters are
-// only touched with atomics, which execute at the L2.
+// Visibility of published data: within a kernel, a row's histograms (and, in
+// the fused kernel, its summaries and candidates) are written once, followed
+// by a wait for the stores, and read by the row's other workgroups only after
+// the barrier or handoff atomic that counts every chunk's arrival.  All of a
+// row's chunks run on one XCD (checked: the finaliser defers the row
+// otherwise), so the data meet in its L2; the L1 is invalidated at every
+// kernel start and no workgroup reads those lines before the count completes.
+// final_kernel reads what chunk_kernel wrote after the kernel boundary.
+// Counters are only touched with atomics, which execute at the L2, except
+// their reset to zero, plain stores by the row's finaliser.
 //
 // Cross-wave exchange slots of FShared (xa ... xh, xv, mi, m64, md) are each
 // rewritten only after a barrier that follows every read of their previous
@@ -35,7 +38,7 @@ __device__ float penalized_logit(const void* row, int id, const int32_t* h, int 
 // Rank sort of the kept list by (z desc, idx asc), i.e. by skey desc:
 // kord[rank] = slot.  LDS reads are batched 8 at a time (independent loads).
 __device__ void rank_sort_kept(int K, FShared& S) {
-  auto& k = S.u.f.x.k;
+  auto& k = S.x.k;
   for (int i = threadIdx.x; i < K; i += FT) {
     const uint64_t ki = k.skey[i];
     int rank = 0;
@@ -69,7 +72,7 @@ __device__ __forceinline__ int count_below(const int32_t* a, int n, int v) {
 
 // Inclusive prefix of km over the sorted order into cum, K <= KEPTCAP (slot xb).
 __device__ void sorted_prefix(int K, FShared& S) {
-  auto& k = S.u.f.x.k;
+  auto& k = S.x.k;
   constexpr int PER = KEPTCAP / FT;
   uint64_t loc[PER];
   uint64_t t = 0;
@@ -102,37 +105,69 @@ __device__ __forceinline__ void with_pen(bool wpen, Fn&& fn) {
   }
 }
 
-// Copies the per-wave candidate lists (counts in slot[0..3]) to out[0, min(tot, PUBCAP))
-// in wave order; returns the total.  The caller has passed a barrier after the
-// lists and counts were written.
-__device__ __forceinline__ uint32_t copy_lists(const FShared& S, const uint32_t* cnt, uint2* out, uint32_t* over) {
-  const uint32_t c0 = cnt[0], c1 = cnt[1], c2 = cnt[2], c3 = cnt[3];
-  const uint32_t tot = c0 + c1 + c2 + c3;
-  *over = (c0 > WCAP || c1 > WCAP || c2 > WCAP || c3 > WCAP || tot > (uint32_t)PUBCAP) ? 1u : 0u;
-  if (!*over) {
-    const uint32_t o1 = c0, o2 = c0 + c1, o3 = c0 + c1 + c2;
-    for (uint32_t i = threadIdx.x; i < tot; i += FT) {
-      const int w = (i >= o1) + (i >= o2) + (i >= o3);
-      const uint32_t k = i - (w == 0 ? 0u : w == 1 ? o1 : w == 2 ? o2 : o3);
-      out[i] = S.u.c.cl[w][k];
-    }
-  }
-  return tot;
+// Per-row parameters and the row's mode, as both kernels derive them.
+struct RowCfg {
+  float T, topp, minp, typp, rep, pres, freq, u;
+  int topk, ntop, mode, kprime, hlen;
+  int64_t qtok;
+  bool greedy, pen;
+  const int32_t* hrow;
+};
+__device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
+  RowCfg g;
+  g.T = P.temperature ? P.temperature[r] : P.temperature_def;
+  g.topk = P.top_k ? P.top_k[r] : P.top_k_def;
+  g.topp = P.top_p ? P.top_p[r] : P.top_p_def;
+  g.minp = P.min_p ? P.min_p[r] : P.min_p_def;
+  g.typp = P.typical_p ? P.typical_p[r] : P.typical_p_def;
+  g.rep = P.rep ? P.rep[r] : P.rep_def;
+  g.pres = P.pres ? P.pres[r] : P.pres_def;
+  g.freq = P.freq ? P.freq[r] : P.freq_def;
+  g.u = P.uniforms ? P.uniforms[r] : 0.5f;
+  g.qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
+               ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
+               : -1;
+  if (g.topp != g.topp) g.topp = 1.0f;
+  g.greedy = !(g.T > 0.0f);
+  g.ntop = (P.n_top > 0 && P.top_logprobs) ? P.n_top : 0;
+  int mode;
+  if (g.greedy) mode = MODE_GREEDY;
+  else if (!(g.T >= 1e-4f)) mode = MODE_DEFER;
+  else if (g.topk > 0) mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
+  else if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
+  else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
+  if (P.entropy) mode = MODE_DEFER;
+  if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
+  g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
+  if (g.kprime > FAST_KMAX) mode = MODE_DEFER;
+  g.mode = mode;
+  g.hrow = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
+  int hlen = (g.hrow && P.history_len) ? P.history_len[r] : 0;
+  if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;
+  g.hlen = hlen;
+  g.pen = hlen > 0 && (g.rep != 1.0f || g.pres != 0.0f || g.freq != 0.0f);
+  return g;
 }
 
-// The fast path for the row / chunk of this workgroup.  Returns 0 when the
-// workgroup is done, or a positive reason code when it must run the general
-// algorithm on its row (the condition is workgroup-uniform).
+// Workgroup id -> (row, chunk): ids are dispatched round-robin over the 8
+// XCDs, so the chunks of a row (ids congruent modulo 8) share one XCD.
+struct ChunkId {
+  int r, j;
+};
+__device__ __forceinline__ ChunkId chunk_id(int G) {
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  return ChunkId{(slot / G) * 8 + xcd, slot % G};
+}
+
+// Phase 1: chunk j of row r (r < R).  Returns the row's mode; a deferred row
+// (MODE_DEFER) publishes nothing.
 template <int DT, int VEC>
-__device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
+__device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const int r, const int j) {
   using CK = Chunk<DT, VEC>;
-  constexpr int NE = CK::NE, CH = CK::CH, NV = CK::NV;
+  constexpr int NE = CK::NE, CH = CK::CH;
   constexpr bool PK = CK::PACKED;
   const KParams& P = F.k;
   const int G = F.G;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int r = (slot / G) * 8 + xcd, j = slot % G;
-  if (r >= P.R) return 0;
   LPS_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int V = P.V;
@@ -148,54 +183,28 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   uint32_t* ctr = F.counters + (int64_t)r * 32;
 
   // ---- history ids, then the chunk: both in flight together ----
-  const int32_t* hrow = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
   HistPrefetch hp;
-  prefetch_history(hrow, P.history_stride, hp);
+  prefetch_history(P.history ? P.history + (int64_t)r * P.history_stride : nullptr, P.history_stride, hp);
   CK C;
   C.load(row, lo, n);
 
-  const float T = P.temperature ? P.temperature[r] : P.temperature_def;
-  const int topk = P.top_k ? P.top_k[r] : P.top_k_def;
-  float topp = P.top_p ? P.top_p[r] : P.top_p_def;
-  const float minp = P.min_p ? P.min_p[r] : P.min_p_def;
-  const float typp = P.typical_p ? P.typical_p[r] : P.typical_p_def;
-  const float rep = P.rep ? P.rep[r] : P.rep_def;
-  const float pres = P.pres ? P.pres[r] : P.pres_def;
-  const float freq = P.freq ? P.freq[r] : P.freq_def;
-  if (topp != topp) topp = 1.0f;
-  const bool greedy = !(T > 0.0f);
-  const int ntop = (P.n_top > 0 && P.top_logprobs) ? P.n_top : 0;
-  // needed only by the row's finaliser; read with the other row parameters
-  const float u_row = P.uniforms ? P.uniforms[r] : 0.5f;
-  const int64_t qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
-                           ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
-                           : -1;
-
-  int mode;
-  if (greedy) mode = MODE_GREEDY;
-  else if (!(T >= 1e-4f)) mode = MODE_DEFER;
-  else if (topk > 0) mode = topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
-  else if (minp > 0.0f || typp < 1.0f || ntop > 0) mode = MODE_DEFER;
-  else mode = topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
-  if (P.entropy) mode = MODE_DEFER;
-  if (mode == MODE_TOPK && typp < 1.0f && topk >= V) mode = MODE_DEFER;
-  const int kprime = mode == MODE_TOPK ? (topk > ntop ? topk : ntop) : (mode == MODE_GREEDY ? ntop : 0);
-  if (kprime > FAST_KMAX) mode = MODE_DEFER;
-  if (mode == MODE_DEFER) return j == 0 ? 1 : 0;
+  const RowCfg g = row_cfg(P, r);
+  const float T = g.T, topp = g.topp, rep = g.rep, pres = g.pres, freq = g.freq;
+  const bool greedy = g.greedy, pen = g.pen;
+  const int ntop = g.ntop, mode = g.mode, kprime = g.kprime, hlen = g.hlen;
+  const int32_t* hrow = g.hrow;
+  if (mode == MODE_DEFER) return mode;  // the general algorithm samples the row
 
   // ---- penalties from a per-chunk count table ----
-  int hlen = (hrow && P.history_len) ? P.history_len[r] : 0;
-  if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;
-  const bool pen = hlen > 0 && (rep != 1.0f || pres != 0.0f || freq != 0.0f);
   uint32_t cflags = 0;
-  const PenArgs pa{S.u.c.hc, rep, pres, freq};
+  const PenArgs pa{S.hc, rep, pres, freq};
   if (pen) {
     if (hlen > 65535) cflags |= CF_HISTORY;  // counts are at most 16-bit: such rows take the general path
     if constexpr (PK) {
-      if (!build_counts<8>(S.u.c.hc, hrow, hlen, hp, lo, n, S)) cflags |= CF_HISTORY;
+      if (!build_counts<8>(S.hc, hrow, hlen, hp, lo, n, S)) cflags |= CF_HISTORY;
       mark_counts(C, n, pa);
     } else {
-      build_counts<16>(S.u.c.hc, hrow, hlen, hp, lo, n, S);
+      build_counts<16>(S.hc, hrow, hlen, hp, lo, n, S);
       apply_counts(C, n, pa);
     }
   }
@@ -216,8 +225,10 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       for (int s = 0; s < NE; s++) {
         const float v = C.template val<PEN>(s, pa);
         tnan |= v != v ? 1u : 0u;
-        if (v > tm) { tm2 = tm; tm = v; }
-        else if (v > tm2) tm2 = v;
+        // branch-free top two (NaN counts as -inf here; the flag reports it)
+        const float w = v != v ? -INFINITY : v;
+        tm2 = fmaxf(tm2, fminf(tm, w));
+        tm = fmaxf(tm, w);
       }
     } else {
 #pragma unroll
@@ -251,7 +262,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     const uint32_t wni = wsum(ninf);
     if (lane == 0) { S.xd[wv] = (double)wmx; S.xc[wv] = wnan; S.xa[wv] = wg; S.xf[wv] = wni; }
   }
-  if (mode == MODE_NUCLEUS) S.u.c.hm[tid] = 0ull;  // HB == FT
+  if (mode == MODE_NUCLEUS) S.hm[tid] = 0ull;  // HB == FT
   __syncthreads();
   const float cmax = (float)fmax(fmax(S.xd[0], S.xd[1]), fmax(S.xd[2], S.xd[3]));
   const bool anynan = (S.xc[0] | S.xc[1] | S.xc[2] | S.xc[3]) != 0u;
@@ -287,7 +298,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
           acc += (double)e;
           if (e > 0.0f) {
             const int hb = btop - (int)floorf(__fmul_rn(w, (float)HS));
-            if (hb < HB) atomicAdd(&S.u.c.hm[hb], (unsigned long long)mass_fixed(e));
+            if (hb < HB) atomicAdd(&S.hm[hb], (unsigned long long)mass_fixed(e));
           }
         }
       } else {
@@ -359,7 +370,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   if (tid == 0) {
     ChunkSum1 a;
     a.mkey = mkey; a.amax = amax; a.zsum = zsum; a.btop = btop; a.ninf = ninf; a.flags = cflags;
-    a.pad = 0;
+    a.xcc = xcc_id();
     s1[j] = a;
   }
 
@@ -368,7 +379,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   uint32_t nabove = 0;
   int blo = 0, bhi = -1;
   if (mode == MODE_NUCLEUS) {
-    hist[(int64_t)j * HB + tid] = (float)((double)S.u.c.hm[tid] / (double)kMassScale);
+    hist[(int64_t)j * HB + tid] = (float)((double)S.hm[tid] / (double)kMassScale);
     wait_stores();
     __syncthreads();
     if (tid == 0) {
@@ -403,10 +414,10 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       const bool qfin = lane < G && a.mkey != 0xFFFFFFFFu && xq != INFINITY && xq != -INFINITY;
       const double sc = (rfin && qfin) ? exp2((double)__fmul_rn(xq, c) - (double)wg) : 0.0;
       const double Z = wsum(a.zsum * sc);
-      if (lane < G) { S.u.c.scale[lane] = sc; S.u.c.btop[lane] = a.btop; }
+      if (lane < G) { S.scale[lane] = sc; S.btop[lane] = a.btop; }
       if (lane == 0) { S.md[0] = Z; S.mi[10] = rfin ? (int)floorf(__fmul_rn(wg, (float)HS)) : 0; S.mi[11] = rfin ? 1 : 0; }
     }
-    S.u.c.gm[tid] = 0ull;
+    S.gm[tid] = 0ull;
     __syncthreads();
     const bool rfin = S.mi[11] != 0;
     const int btg = S.mi[10];
@@ -417,21 +428,21 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
 #pragma unroll
       for (int k = 0; k < 32; k++) {
         if (k < g0) {
-          const int a = tid + (btg - S.u.c.btop[k]);
-          const double sc = S.u.c.scale[k];
-          if (sc > 0.0 && a < HB && hv[k] > 0.0f) atomicAdd(&S.u.c.gm[a], (unsigned long long)((double)hv[k] * sc * kGm));
+          const int a = tid + (btg - S.btop[k]);
+          const double sc = S.scale[k];
+          if (sc > 0.0 && a < HB && hv[k] > 0.0f) atomicAdd(&S.gm[a], (unsigned long long)((double)hv[k] * sc * kGm));
         }
       }
       for (int q = 32; q < G; q++) {  // rows of more than 32 chunks
-        const int a = tid + (btg - S.u.c.btop[q]);
-        const double sc = S.u.c.scale[q];
+        const int a = tid + (btg - S.btop[q]);
+        const double sc = S.scale[q];
         const float h = hist[(int64_t)q * HB + tid];
-        if (sc > 0.0 && a < HB && h > 0.0f) atomicAdd(&S.u.c.gm[a], (unsigned long long)((double)h * sc * kGm));
+        if (sc > 0.0 && a < HB && h > 0.0f) atomicAdd(&S.gm[a], (unsigned long long)((double)h * sc * kGm));
       }
     }
     __syncthreads();
     // merged mass of absolute bin btg - tid (slot xd)
-    const double m = (double)S.u.c.gm[tid] / kGm;
+    const double m = (double)S.gm[tid] / kGm;
     double mtot;
     const double ex = bscan_excl<double>(m, &mtot, S.xd);
     // bins whose cumulative interval meets [Pm - eps, Pm + eps] (slots xg xh)
@@ -453,7 +464,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       blo = btg - tmax;
       // this chunk: mass and count above the region, candidates inside (slots xa xb xc)
       const int hbt = btop - (bhi + 1);  // chunk histogram bins 0..hbt lie above the region
-      uint64_t am = (xm_finite && tid <= hbt) ? (uint64_t)S.u.c.hm[tid] : 0ull;
+      uint64_t am = (xm_finite && tid <= hbt) ? (uint64_t)S.hm[tid] : 0ull;
       uint32_t na = 0, nc = 0, inreg = 0;
       with_pen<PK>(wpen, [&](auto PT) {
         constexpr bool PEN = decltype(PT)::value;
@@ -505,36 +516,59 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     LPS_STAMP(20);
   }
 
-  // ---- handoff: the last chunk workgroup of the row finalises it ----
+  // ---- the chunk's summary for the row's finaliser (next kernel) ----
   LPS_STAMP(6);
-  wait_stores();
-  __syncthreads();
   if (tid == 0) {
     ChunkSum2 a;
-    a.ncand = ncand; a.flags = cflags; a.above = above; a.nabove = nabove;
-    a.pad[0] = a.pad[1] = a.pad[2] = 0;
+    a.ncand = ncand; a.flags = cflags; a.above = above; a.nabove = nabove; a.blo = blo; a.bhi = bhi; a.pad = 0;
     s2[j] = a;
-    wait_stores();
-    // handoff word: arrivals in bits 0-7, arrivals per XCD in 7-bit fields from bit 8
-    const uint64_t add = 1ull + (1ull << (8 + 7 * (xcc_id() & 7u)));
-    const uint64_t now = l2_fetch_add64(reinterpret_cast<uint64_t*>(ctr), add) + add;
-    int xcds = 0;
-    for (int q = 0; q < 8; q++) xcds += ((now >> (8 + 7 * q)) & 0x7Full) ? 1 : 0;
-    S.mi[5] = (now & 0xFFull) == (uint64_t)G ? 1 : 0;
-    S.mi[6] = xcds;  // more than one XCD: the L2-local exchange cannot be trusted
   }
-  __syncthreads();
-  LPS_STAMP(7);
-  if (!S.mi[5]) return 0;
+  return mode;
+}
+
+// The finaliser of row r, after every chunk of the row has published.  fused:
+// it runs in the row's last chunk workgroup, in the chunks' kernel, and reads
+// their data through the XCD's L2.  Returns 0 when the row is done, or a
+// positive reason code when the general algorithm must sample it.
+template <int DT, int VEC>
+__device__ __forceinline__ int final_body(const FParams& F, FShared& S, const int r, const bool fused) {
+  using CK = Chunk<DT, VEC>;
+  constexpr int CH = CK::CH, NV = CK::NV;
+  constexpr bool PK = CK::PACKED;
+  const KParams& P = F.k;
+  const int G = F.G;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int V = P.V;
+  constexpr int ES = CK::ES;
+  const void* row = reinterpret_cast<const char*>(P.logits) +
+                    ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
+  ChunkSum1* s1 = F.sum1 + (int64_t)r * F.s_stride;
+  ChunkSum2* s2 = F.sum2 + (int64_t)r * F.s_stride;
+  uint2* cands = F.cands + (int64_t)r * F.c_stride;
+  if (tid == 0) {  // the row's counters back to zero for the next launch
+    F.counters[(int64_t)r * 32] = 0u;
+    F.counters[(int64_t)r * 32 + 2] = 0u;
+  }
+  const RowCfg g = row_cfg(P, r);
+  if (g.mode == MODE_DEFER) return 1;
+  const float T = g.T, topp = g.topp, minp = g.minp, typp = g.typp, rep = g.rep, pres = g.pres, freq = g.freq;
+  const bool greedy = g.greedy, pen = g.pen;
+  const int topk = g.topk, ntop = g.ntop, mode = g.mode, kprime = g.kprime, hlen = g.hlen;
+  const int64_t qtok = g.qtok;
+  const int32_t* hrow = g.hrow;
+  const float c = __fdiv_rn(kLog2e, greedy ? 1.0f : T);
+  LPS_FSTAMP(7);
 
   // =========================== finaliser ===========================
   // F1: wave 0 gathers the per-chunk summaries.
-  const bool split = S.mi[6] > 1;
   if (wv == 0) {
     ChunkSum1 a{};
     ChunkSum2 b{};
     if (lane < G) { a = s1[lane]; b = s2[lane]; }
-    const uint32_t fl = wreduce(lane < G ? (a.flags | b.flags) : 0u, OpOr{});
+    // chunks that exchanged data through one L2 must have run on one XCD
+    const uint32_t xm = wreduce(lane < G ? (1u << a.xcc) : 0u, OpOr{});
+    const bool split = __builtin_popcount(xm) > 1 && (fused || g.mode == MODE_NUCLEUS);
+    const uint32_t fl = wreduce(lane < G ? (a.flags | b.flags) : 0u, OpOr{}) | (split ? (uint32_t)CF_SPLIT : 0u);
     const uint32_t ninf_all = wsum(lane < G ? a.ninf : 0u);
     const uint32_t nc = lane < G ? b.ncand : 0u;
     const uint32_t ncinc = wscan_incl(nc);
@@ -553,15 +587,17 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     const double abv = (double)b.above / (double)kMassScale * sc;
     const double A = wsum(abv);
     if (lane < G) {
-      S.u.f.pre[lane] = ncinc - nc;
-      S.u.f.scale[lane] = sc;
-      S.u.f.wm[lane] = wq;
-      S.u.f.abvm[lane] = abv;
-      S.u.f.keptm[lane] = a.zsum * sc;
-      S.u.f.keptf[lane] = 0ull;
+      S.pre[lane] = ncinc - nc;
+      S.scale[lane] = sc;
+      S.wm[lane] = wq;
+      S.abvm[lane] = abv;
+      S.keptm[lane] = a.zsum * sc;
+      S.keptf[lane] = 0ull;
     }
     if (lane == 0) {
-      S.u.f.pre[G] = NC;
+      S.pre[G] = NC;
+      S.mi[18] = b.blo;  // every chunk derived the same cut region
+      S.mi[19] = b.bhi;
       S.mi[12] = (int)fl;
       S.mi[13] = (int)NC;
       S.mi[14] = (int)ninf_all;
@@ -572,13 +608,9 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       S.md[2] = A;
     }
   }
-  if (tid == 0) {
-    // counters back to zero for the next launch (stream-ordered)
-    atomicExch(reinterpret_cast<unsigned long long*>(ctr), 0ull);
-    atomicExch(ctr + 2, 0u);
-  }
   __syncthreads();
-  const uint32_t fl = (uint32_t)S.mi[12] | (split ? (uint32_t)CF_SPLIT : 0u);
+  const uint32_t fl = (uint32_t)S.mi[12];
+  const int blo = S.mi[18], bhi = S.mi[19];
   if (fl & (CF_OVERFLOW | CF_HISTORY | CF_SPLIT | CF_REGION)) return (int)fl;
   const int NC = S.mi[13];
   const uint32_t ninf_all = (uint32_t)S.mi[14];
@@ -587,7 +619,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
   const int gam = S.mi[17];
   const double Zfull = S.md[1];
   const double Aabove = S.md[2];
-  LPS_STAMP(8);
+  LPS_FSTAMP(8);
 
   const float xmax = key2f(gkey);
   const bool has_nan = gkey == 0xFFFFFFFFu;
@@ -598,7 +630,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     else if (xmax == -INFINITY) status |= LPS_ROW_EMPTY;
   }
   const double lnZ = Zfull > 0.0 ? log(Zfull) : 0.0;
-  float u = u_row;
+  float u = g.u;
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0.99999994f;
 
@@ -613,8 +645,8 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     int q = 0;
 #pragma unroll
     for (int step = MAXG / 2; step > 0; step >>= 1)
-      if (q + step < G && (int)S.u.f.pre[q + step] <= i) q += step;
-    return cands[(int64_t)q * PUBCAP + (i - (int)S.u.f.pre[q])];
+      if (q + step < G && (int)S.pre[q + step] <= i) q += step;
+    return cands[(int64_t)q * PUBCAP + (i - (int)S.pre[q])];
   };
   // Candidates in registers: thread t holds candidate e * FT + t in slot e (z key, index).
   uint32_t ck[FCPT];
@@ -640,13 +672,13 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     // ---------------- top-k (and top-N logprobs) ----------------
     if (NC > FCAP) return 512;
     load_cands();
-    LPS_STAMP(22);
+    LPS_FSTAMP(22);
     const int keff = mode == MODE_TOPK ? (topk < V ? topk : V) : 0;
     int kc = keff > ntop ? keff : ntop;
     if (kc > NC) kc = NC;
     if (kc <= 0) return 16;
     const uint32_t zc = sel_count(ck, np, (uint32_t)kc, S);
-    LPS_STAMP(23);
+    LPS_FSTAMP(23);
     // collect z >= zc into the kept list (slot xh)
     uint32_t cnt = 0;
 #pragma unroll
@@ -654,7 +686,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     uint32_t Kall;
     uint32_t p = bscan_excl<uint32_t>(cnt, &Kall, S.xh);
     if (Kall > (uint32_t)KEPTCAP) return 32;
-    auto& kl = S.u.f.x.k;
+    auto& kl = S.x.k;
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       if (e < np && ck[e] >= zc) {
@@ -665,12 +697,12 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       }
     }
     __syncthreads();
-    LPS_STAMP(24);
+    LPS_FSTAMP(24);
     const int K = (int)Kall;
     rank_sort_kept(K, S);
     auto kz = [&](int slot) -> uint32_t { return (uint32_t)(kl.skey[slot] >> 32); };
     ntop_out = ntop < K ? ntop : K;
-    LPS_STAMP(16);
+    LPS_FSTAMP(16);
     if (mode == MODE_GREEDY) {
       token = gam;
       cut = xmax;
@@ -793,16 +825,16 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       auto cmass = [&](int e) -> uint64_t { return mass_fixed(mass_f(key2f(ck[e]), zmax)); };
       const uint64_t Af = (uint64_t)(Aabove * (double)kMassScale);
       const uint64_t Pf = (uint64_t)((double)topp * Zfull * (double)kMassScale);
-      LPS_STAMP(16);
+      LPS_FSTAMP(16);
       const MassSel ms = sel_mass(ck, np, cmass, Af, Pf, S);
-      LPS_STAMP(17);
+      LPS_FSTAMP(17);
       if (!ms.ok || ms.ceq == 0) return 64;
       vkey = ms.key;
       const uint64_t e1 = ms.meq / ms.ceq;
       const uint64_t nt = e1 ? (Pf - ms.above) / e1 + 1 : (uint64_t)ms.ceq;
       n_tie = nt >= ms.ceq ? kNoTie : (uint32_t)nt;
       // ties at the cut: the kept ones are the n_tie lowest indices (slot xh)
-      auto& kl = S.u.f.x.k;
+      auto& kl = S.x.k;
       if (tid == 0) { S.mi[25] = 0x7FFFFFFF; S.mi[26] = 0; S.md[6] = -1.0; }
       __syncthreads();
       if (n_tie != kNoTie) {
@@ -827,7 +859,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         if (e < np && ck[e] == vkey) S.mi[26] = (int)cand_at(e * FT + tid).x;
       __syncthreads();
       tie_lim = S.mi[25];
-      LPS_STAMP(18);
+      LPS_FSTAMP(18);
       if (tid == 0) {
         // the cut's whole division-collision group must lie inside the region
         const float xv = key2f((uint32_t)S.mi[26]);
@@ -850,7 +882,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
         const bool kept = e < np && (ck[e] > vkey || (ck[e] == vkey && ci[e] <= tie_lim));
         if (kept) {
           const uint64_t m = cmass(e);
-          atomicAdd(&S.u.f.keptf[ci[e] / CH], (unsigned long long)m);
+          atomicAdd(&S.keptf[ci[e] / CH], (unsigned long long)m);
           if ((int64_t)ci[e] == qtok) S.md[6] = (double)m / (double)kMassScale;
           lc++;
         }
@@ -862,15 +894,15 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
       kept_n = (int32_t)(nab_all + S.xg[0] + S.xg[1] + S.xg[2] + S.xg[3]);
       qmass = S.md[6];
       if (wv == 0 && lane < G)
-        S.u.f.keptm[lane] = S.u.f.abvm[lane] + (double)S.u.f.keptf[lane] / (double)kMassScale;
+        S.keptm[lane] = S.abvm[lane] + (double)S.keptf[lane] / (double)kMassScale;
       __syncthreads();
       ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
       cut = key2f(vkey);
     }
-    LPS_STAMP(9);
+    LPS_FSTAMP(9);
     // the chunk holding u * Zf (wave 0), then its exact scan in vocabulary order
     if (wv == 0) {
-      const double km = lane < G ? S.u.f.keptm[lane] : 0.0;
+      const double km = lane < G ? S.keptm[lane] : 0.0;
       const double inc = wscan_incl(km);
       const double Zf = rdlane(inc, 63);
       const double target = (double)u * Zf;
@@ -886,23 +918,23 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     if (!P.skip_draw) {
       const int lo2 = js * CH;
       const int n2 = (V - lo2) < CH ? (V - lo2) : CH;
-      const float wmj = S.u.f.wm[js];
-      const double scj = S.u.f.scale[js];
+      const float wmj = S.wm[js];
+      const double scj = S.scale[js];
       HistPrefetch hp2;
       prefetch_history(hrow, P.history_stride, hp2);
       CK Y;
       Y.load(row, lo2, n2);
-      const PenArgs pa2{S.u.f.x.hc, rep, pres, freq};
+      const PenArgs pa2{S.x.hc, rep, pres, freq};
       if (pen) {  // (a row whose counts did not fit never reaches the finaliser)
         if constexpr (PK) {
-          build_counts<8>(S.u.f.x.hc, hrow, hlen, hp2, lo2, n2, S);
+          build_counts<8>(S.x.hc, hrow, hlen, hp2, lo2, n2, S);
           mark_counts(Y, n2, pa2);
         } else {
-          build_counts<16>(S.u.f.x.hc, hrow, hlen, hp2, lo2, n2, S);
+          build_counts<16>(S.x.hc, hrow, hlen, hp2, lo2, n2, S);
           apply_counts(Y, n2, pa2);
         }
       }
-      LPS_STAMP(21);
+      LPS_FSTAMP(21);
       // Kept mass of slot (v, e) with the formulas that built the chunk's kept
       // mass: exp2(x c - wm) * scale outside the cut region (as the chunk pass
       // summed it), the finaliser's exp(z - zmax) for region candidates.
@@ -1017,7 +1049,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     }
   }
   if (P.skip_draw && !greedy) token = -1;
-  LPS_STAMP(10);
+  LPS_FSTAMP(10);
 
   // ---- outputs ----
   if (P.chosen_logprob && tid == 0) {
@@ -1027,7 +1059,7 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     P.chosen_logprob[r] = lp;
   }
   if (ntop > 0 && status == 0) {
-    auto& kl = S.u.f.x.k;
+    auto& kl = S.x.k;
     for (int q = tid; q < P.n_top; q += FT) {
       if (q < ntop_out) {
         const int si = kl.kord[q];
@@ -1050,33 +1082,55 @@ __device__ __forceinline__ int fast_body(const FParams& F, FShared& S) {
     if (P.kept_count) P.kept_count[r] = kept_n;
     if (P.row_path) P.row_path[r] = 0;
   }
-  LPS_STAMP(11);
+  LPS_FSTAMP(11);
   return 0;
 }
 
+// Split path, phase 1: grid of ceil(R / 8) * 8 * G workgroups.
 template <int DT, int VEC>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(3, 8))) void fast_kernel(FParams F) {
-  // the fast path's LDS, or the general path's when a row falls back to it
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(FParams F) {
+  __shared__ CShared S;
+  const ChunkId c = chunk_id(F.G);
+  if (c.r >= F.k.R) return;
+  chunk_body<DT, VEC>(F, S, c.r, c.j);
+}
+
+// Split path, phase 2: one workgroup per row.  A row the fast path cannot
+// finish exactly is marked deferred in the workspace status (reason code in
+// bits 8 and up); the general kernel, launched next with that status as its
+// filter, samples it.
+template <int DT, int VEC>
+__global__ __launch_bounds__(FT) void final_kernel(FParams F) {
+  __shared__ FShared S;
+  const int r = blockIdx.x;
+  const int reason = final_body<DT, VEC>(F, S, r, false);
+  if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
+}
+
+// Fused path (grids that fit on the GPU at once): the chunk kernel whose last
+// workgroup of each row to finish, counted by an L2 atomic, finalises the row
+// while other rows are still in their chunk phase.
+template <int DT, int VEC>
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(3, 8))) void fused_kernel(FParams F) {
   __shared__ union {
+    CShared c;
     FShared f;
-    GenShared g;
   } SU;
-  const int reason = fast_body<DT, VEC>(F, SU.f);
-  if (reason > 0) {
-    // a row the fast path cannot finish exactly: this whole workgroup runs the
-    // general algorithm on it (no fast-path value is live here)
-    const int slot = blockIdx.x >> 3;
-    const int r = (slot / F.G) * 8 + (blockIdx.x & 7);
-    if (threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
-    __syncthreads();
-    // a copy local to this branch: the general path's uses of its parameters
-    // then cost nothing on the fast path (no private copy of the kernel arguments)
-    KParams Pk = F.k;
-    Pk.plans = nullptr;        // plans serve speculative verification, which uses the general kernel
-    Pk.only_status = nullptr;  // the general kernel's own launch filter
-    gen_row<DT, 1>(Pk, r, SU.g);  // element loads: the lean variant of the general path
-    LPS_STAMP(12);
+  const ChunkId c = chunk_id(F.G);
+  if (c.r >= F.k.R) return;
+  const int mode = chunk_body<DT, VEC>(F, SU.c, c.r, c.j);
+  if (mode == MODE_DEFER) {
+    if (c.j == 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (1 << 8);
+    return;
   }
+  // handoff: every thread's stores have reached the L2 before the arrival is counted
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) SU.c.mi[5] = l2_fetch_add(F.counters + (int64_t)c.r * 32, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
+  __syncthreads();
+  if (!SU.c.mi[5]) return;
+  const int reason = final_body<DT, VEC>(F, SU.f, c.r, true);
+  if (reason > 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (reason << 8);
 }
 
 }  // namespace lps

@@ -63,9 +63,12 @@ struct KParams {
   int32_t* kept_ties;
   int32_t* kept_count;
   RowPlan* plans;
-  const int32_t* only_status;  // non-null: process only rows whose entry has bit 8 (deferred by the fast kernel)
+  const int32_t* only_status;  // non-null: process only rows whose entry has LPS_ROW_DEFERRED (8) set
   int32_t* row_path;           // optional: 0 fast kernel, 1 general kernel
 };
+// Workspace row status bit (beside the LPS_ROW_* bits): the fast kernels
+// deferred the row to the general kernel.
+constexpr int32_t LPS_ROW_DEFERRED = 8;
 
 struct GenShared {
   uint32_t bloom[BLOOM_WORDS];
@@ -709,8 +712,11 @@ template <int DT, int VEC>
 __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
   __shared__ GenShared S;
   const int r = blockIdx.x;
-  if (P.only_status && !(P.only_status[r] & 8)) return;
-  gen_row<DT, VEC>(P, r, S);
+  if (P.only_status && !(P.only_status[r] & LPS_ROW_DEFERRED)) return;
+  // a copy local to the rows that run: the general path takes the parameters
+  // by reference, and a skipped row then never copies them to scratch memory
+  KParams Pl = P;
+  gen_row<DT, VEC>(Pl, r, S);
 }
 
 }  // namespace lps

@@ -120,9 +120,9 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
     synchronised and ``status`` is returned as a device tensor.
 
-    ``path``: ``"auto"`` runs the multi-workgroup kernel (a row it cannot
-    finish exactly falls back to the general algorithm inside it; ``row_path``
-    reports which); ``"generic"`` runs only the general
+    ``path``: ``"auto"`` runs the multi-workgroup kernels (a row they cannot
+    finish exactly is sampled by the general kernel launched after them;
+    ``row_path`` reports which); ``"generic"`` runs only the general
     one-workgroup-per-row kernel."""
     if path not in ("auto", "generic"):
         raise ValueError("path must be 'auto' or 'generic'")
