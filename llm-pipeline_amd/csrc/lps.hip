@@ -68,7 +68,12 @@ FastWs fast_layout(void* base, int R, int V) {
   if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
   w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
   w.h_stride = (int64_t)round_up((size_t)G * HB, 32);                // floats
-  w.c_stride = (int64_t)G * PUBCAP;                                  // uint2, multiple of 16
+  // candidates: G chunks of PUB slots, for either chunk variant
+  constexpr int NR2 = fused_nr<LPS_DTYPE_BF16>();
+  const int G2 = (V + FT * NR2 - 1) / (FT * NR2);
+  const int64_t c32 = (int64_t)G * Chunk<LPS_DTYPE_F32, 1, 32>::PUB;
+  const int64_t c2 = (int64_t)G2 * Chunk<LPS_DTYPE_BF16, 1, NR2>::PUB;
+  w.c_stride = c32 > c2 ? c32 : c2;                                  // uint2, multiple of 16
   size_t off = 0;
   char* p = reinterpret_cast<char*>(base);
   w.counters = reinterpret_cast<uint32_t*>(p + off); off = (size_t)FAST_MAX_ROWS * 128;
@@ -81,21 +86,27 @@ FastWs fast_layout(void* base, int R, int V) {
   return w;
 }
 
-// Grids of at most this many chunk workgroups take the fused kernel (row
-// finalisers overlap other rows' chunk work); larger ones the split pair,
-// whose chunk kernel keeps more workgroups resident per CU.
+// Grids of at most this many chunk workgroups take the fused kernel (three
+// workgroups per CU: row finalisers overlap other rows' chunk work).  Larger
+// grids take the split pair (five chunk workgroups per CU, then one finaliser
+// workgroup per row).
 #ifndef LPS_FUSED_MAX_WG
 #define LPS_FUSED_MAX_WG 2048
 #endif
+// Fused grids above one resident wave (three workgroups per CU) reorder rows
+// so that the longest finalisers start first.
+#ifndef LPS_HEAVY_FIRST_WG
+#define LPS_HEAVY_FIRST_WG 768
+#endif
 
 template <int DT, int VEC>
-hipError_t launch_fast(const FParams& F, int rows_pad, hipStream_t s) {
-  const unsigned grid = (unsigned)(rows_pad * F.G);
+hipError_t launch_fast(FParams F, int rows_pad, bool fused, hipStream_t s) {
   hipError_t e;
-  if (VEC > 1 && grid <= (unsigned)LPS_FUSED_MAX_WG) {  // (element-wise variants: split, fewer registers)
-    hipLaunchKernelGGL((fused_kernel<DT, VEC>), dim3(grid), dim3(FT), 0, s, F);
+  if (VEC > 1 && fused) {
+    if constexpr (VEC > 1) hipLaunchKernelGGL((fused_kernel<DT, VEC>), dim3((unsigned)(rows_pad * F.G)), dim3(FT), 0, s, F);
     e = hipGetLastError();
   } else {
+    const unsigned grid = (unsigned)(rows_pad * F.G);
     hipLaunchKernelGGL((chunk_kernel<DT, VEC>), dim3(grid), dim3(FT), 0, s, F);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -111,11 +122,14 @@ hipError_t launch_fast(const FParams& F, int rows_pad, hipStream_t s) {
   return launch_gen<DT, VEC>(G, s);
 }
 
-hipError_t dispatch_fast(int dtype, bool vec, const FParams& F, int rows_pad, hipStream_t s) {
+hipError_t dispatch_fast(int dtype, bool vec, const FParams& F, int rows_pad, bool fused, hipStream_t s) {
   switch (dtype) {
-    case LPS_DTYPE_F32: return vec ? launch_fast<LPS_DTYPE_F32, 4>(F, rows_pad, s) : launch_fast<LPS_DTYPE_F32, 1>(F, rows_pad, s);
-    case LPS_DTYPE_BF16: return vec ? launch_fast<LPS_DTYPE_BF16, 8>(F, rows_pad, s) : launch_fast<LPS_DTYPE_BF16, 1>(F, rows_pad, s);
-    default: return vec ? launch_fast<LPS_DTYPE_F16, 8>(F, rows_pad, s) : launch_fast<LPS_DTYPE_F16, 1>(F, rows_pad, s);
+    case LPS_DTYPE_F32:
+      return vec ? launch_fast<LPS_DTYPE_F32, 4>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_F32, 1>(F, rows_pad, false, s);
+    case LPS_DTYPE_BF16:
+      return vec ? launch_fast<LPS_DTYPE_BF16, 8>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_BF16, 1>(F, rows_pad, false, s);
+    default:
+      return vec ? launch_fast<LPS_DTYPE_F16, 8>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_F16, 1>(F, rows_pad, false, s);
   }
 }
 
@@ -166,10 +180,15 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   const FastWs w = fast_layout(ws, P.R, P.V);
   FParams F{};
   F.k = P;
-  // chunk size of the kernel variant: 16384 for 16-bit logits read in 16-byte
-  // vectors (two logits per register), else 8192
-  const int ch = (LPS_PACK16 && dtype != LPS_DTYPE_F32 && vec) ? 2 * FCH_MIN : FCH_MIN;
+  const int rows_pad = (P.R + 7) / 8 * 8;
+  // chunk size of the kernel variant: FT * (logit registers per thread); the
+  // split kernel's 16-bit rows read in 16-byte vectors take 16384 when packed
+  // two per register
+  const int chf = FT * (dtype == LPS_DTYPE_F32 ? fused_nr<LPS_DTYPE_F32>() : fused_nr<LPS_DTYPE_BF16>());
+  const bool fused = vec && (int64_t)rows_pad * ((P.V + chf - 1) / chf) <= LPS_FUSED_MAX_WG;
+  const int ch = fused ? chf : (LPS_PACK16 && dtype != LPS_DTYPE_F32 && vec) ? 2 * FCH_MIN : FCH_MIN;
   F.G = (P.V + ch - 1) / ch;
+  F.heavy_first = fused && P.R <= 128 && (int64_t)rows_pad * F.G > LPS_HEAVY_FIRST_WG ? 1 : 0;
   F.counters = w.counters;
   F.status = w.status;
   F.sum1 = w.sum1;
@@ -179,8 +198,7 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   F.s_stride = w.s_stride;
   F.h_stride = w.h_stride;
   F.c_stride = w.c_stride;
-  const int rows_pad = (P.R + 7) / 8 * 8;
-  return dispatch_fast(dtype, vec, F, rows_pad, s);
+  return dispatch_fast(dtype, vec, F, rows_pad, fused, s);
 }
 
 KParams neutral_params() {

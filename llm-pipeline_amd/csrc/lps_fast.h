@@ -52,13 +52,15 @@ constexpr int FT = 256;                 // threads per workgroup
 constexpr int FW = FT / 64;             // waves per workgroup
 constexpr int FCH_MIN = FT * 32;        // smallest chunk (fp32 and element-read rows): sizes the workspace
 constexpr int FAST_KMAX = 256;          // largest top_k / top-N handled by the fast path
-constexpr int PUBCAP = 512;             // published candidates per chunk
 constexpr int FCPT = 16;                // finaliser candidates per thread (registers)
 constexpr int FCAP = FT * FCPT;         // finaliser candidate capacity (4096)
 constexpr int KEPTCAP = 512;            // finaliser kept list
 constexpr int HB = 256;                 // histogram bins per chunk (1/8 log2 unit each)
 constexpr int HS = 8;                   // bins per log2 unit
-constexpr int SELD = 12;                // count-select digit bits
+#ifndef LPS_SELD
+#define LPS_SELD 12
+#endif
+constexpr int SELD = LPS_SELD;          // count-select digit bits
 constexpr int SELB = 1 << SELD;         // count-select histogram bins
 constexpr int SELDM = 10;               // mass-select digit bits
 constexpr int SELBM = 1 << SELDM;       // mass-select histogram bins
@@ -89,12 +91,13 @@ struct ChunkSum2 {   // published at the end of phase 1
 struct FParams {
   KParams k;           // per-row parameters and outputs (shared with the general kernel)
   int G;               // chunks per row
+  int heavy_first;     // fused kernel, R <= 128: dispatch rows without top-k first
   uint32_t* counters;  // [R * 32]: fused handoff arrivals at [0], nucleus barrier arrivals at [2]; zero between launches
   int32_t* status;     // [R]
   ChunkSum1* sum1;     // row r at sum1 + r * s_stride
   ChunkSum2* sum2;
   float* hist;         // row r at hist + r * h_stride: G x HB masses (chunk reference)
-  uint2* cands;        // row r at cands + r * c_stride: G x PUBCAP (x key, idx)
+  uint2* cands;        // row r at cands + r * c_stride: G x PUB (x key, idx), PUB of the chunk variant
   int64_t s_stride, h_stride, c_stride;
 };
 
@@ -108,17 +111,20 @@ struct XShared {
   int32_t mi[32];
   uint64_t m64[8];
   double md[8];
+  float mf[4];
 };
-// chunk_kernel's shared block.
-struct CShared : XShared {
-  uint32_t hc[4096];                      // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
+// Shared block of the chunk phase (NR: logit registers per thread).
+template <int NR>
+struct CSharedT : XShared {
+  uint32_t hc[NR * 128];                  // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
   unsigned long long hm[HB];              // chunk mass histogram, fixed point
   unsigned long long gm[HB];              // nucleus region: merged row histogram, fixed point
   double scale[MAXG];                     // nucleus region: chunk -> row reference
   int32_t btop[MAXG];
 };
-// final_kernel's shared block.
-struct FShared : XShared {
+// Shared block of the finaliser.
+template <int NR>
+struct FSharedT : XShared {
   union {
     uint32_t cnt[2][SELB];                // count select, double-buffered digit histograms
     struct {
@@ -133,7 +139,7 @@ struct FShared : XShared {
       int32_t iord[KEPTCAP];              // index-order position -> slot
       unsigned long long cum[KEPTCAP];
     } k;                                  // kept list
-    uint32_t hc[4096];                    // rescan history counts
+    uint32_t hc[NR * 128];                // rescan history counts
   } x;
   uint32_t pre[MAXG + 1];                 // candidate prefix over chunks
   double scale[MAXG];                     // chunk -> row reference
@@ -192,6 +198,12 @@ __device__ __forceinline__ T bscan_excl(T v, T* total, T* slot) {
 // Absolute histogram bin of a logit: floor(x c 8), c = log2(e) / T.
 __device__ __forceinline__ int wbin(float x, float c) { return (int)floorf(__fmul_rn(__fmul_rn(x, c), (float)HS)); }
 
+// The chunk-reference mass exp2(w - wm), w <= wm: the hardware exp2 alone.
+// Results below 2^-126 flush to zero; they are far below the 2^-44 resolution
+// of the fixed-point masses.  The chunk pass and the finaliser's rescan use
+// this same function, so their per-chunk sums agree.
+__device__ __forceinline__ float chunk_mass(float w, float wm) { return __builtin_amdgcn_exp2f(__fsub_rn(w, wm)); }
+
 // ---------------------------------------------------------------------------
 // A thread's share of a chunk, held in 32 registers r[].
 //   fp32 in 16-byte vectors of 4, and every dtype read element by element
@@ -214,15 +226,17 @@ struct PenArgs {        // penalties of the row, and the chunk's count table in 
 #ifndef LPS_PACK16
 #define LPS_PACK16 0
 #endif
-template <int DT, int VEC>
+template <int DT, int VEC, int NR = 32>
 struct Chunk {
-  static constexpr bool PACKED = LPS_PACK16 && DT != LPS_DTYPE_F32 && VEC == 8;
-  static constexpr int NE = PACKED ? 64 : 32;   // logits per thread (fp32 registers hold 32)
+  static_assert(NR == 32 || NR == 64, "32 or 64 logit registers per thread");
+  static constexpr bool PACKED = LPS_PACK16 && DT != LPS_DTYPE_F32 && VEC == 8 && NR == 32;
+  static constexpr int NE = PACKED ? 64 : NR;   // logits per thread (one per fp32 register)
   static constexpr int CH = FT * NE;            // logits per chunk
   static constexpr int NV = NE / VEC;           // vectors per thread
   static constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   static constexpr uint32_t NEG16 = DT == LPS_DTYPE_BF16 ? 0xFF80u : 0xFC00u;  // -inf, 16-bit
-  uint32_t r[32];
+  uint32_t r[NR];
+  static constexpr int PUB = 16 * NR;          // published candidates per chunk
   uint64_t pmask;
 
   __device__ static __forceinline__ int local(int s) {
@@ -260,11 +274,11 @@ struct Chunk {
     pmask = 0ull;
     const char* base = reinterpret_cast<const char*>(row);
     if constexpr (VEC == 1) {
-      float raw[32];
+      float raw[NR];
 #pragma unroll
-      for (int s = 0; s < 32; s++) raw[s] = load1<DT>(row, (int64_t)(lo + min(s * FT + (int)threadIdx.x, n - 1)));
+      for (int s = 0; s < NR; s++) raw[s] = load1<DT>(row, (int64_t)(lo + min(s * FT + (int)threadIdx.x, n - 1)));
 #pragma unroll
-      for (int s = 0; s < 32; s++) r[s] = __float_as_uint((s * FT + (int)threadIdx.x) < n ? raw[s] : -INFINITY);
+      for (int s = 0; s < NR; s++) r[s] = __float_as_uint((s * FT + (int)threadIdx.x) < n ? raw[s] : -INFINITY);
     } else {
       static_assert(VEC * ES == 16, "vector slots are 16 bytes");
       const int lastv = (n / VEC - 1) * VEC;  // start of the last full vector; < 0 when none
@@ -321,16 +335,17 @@ __device__ __forceinline__ void prefetch_history(const int32_t* hrow, int64_t st
   }
 }
 // Counts of the history ids inside [lo, lo + n), BITS (16 or 8) bits per id in
-// hc (8192 or 16384 ids in 4096 words).  Returns false when a count does not
-// fit (16-bit: hlen > 65535 is refused by the caller; 8-bit: a count reached
-// 255).  Ends with a barrier.
-template <int BITS>
-__device__ __forceinline__ bool build_counts(uint32_t* hc, const int32_t* hrow, int hlen, const HistPrefetch& hp,
+// hc (WORDS words: WORDS * 32 / BITS ids, at least n).  Returns false when a
+// count does not fit (16-bit: hlen > 65535 is refused by the caller; 8-bit: a
+// count reached 255).  Ends with a barrier.
+template <int BITS, int WORDS>
+__device__ __forceinline__ bool build_counts(uint32_t (&hc)[WORDS], const int32_t* hrow, int hlen, const HistPrefetch& hp,
                                              int lo, int n, XShared& S) {
   constexpr int PER = 32 / BITS;  // ids per word
+  static_assert(WORDS % (4 * FT) == 0, "whole 16-byte stores per thread");
   u32x4* h4 = reinterpret_cast<u32x4*>(hc);
 #pragma unroll
-  for (int i = 0; i < 1024 / FT; i++) h4[i * FT + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < WORDS / 4 / FT; i++) h4[i * FT + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
   if (threadIdx.x == 0) S.mi[30] = 0;
   __syncthreads();
   bool sat = false;
@@ -351,10 +366,10 @@ __device__ __forceinline__ bool build_counts(uint32_t* hc, const int32_t* hrow, 
   return S.mi[30] == 0;
 }
 // fp32 chunks: apply the 16-bit count table in place.
-template <int DT, int VEC>
-__device__ __forceinline__ void apply_counts(Chunk<DT, VEC>& C, int n, const PenArgs& pa) {
-  static_assert(!Chunk<DT, VEC>::PACKED, "in-place penalties are for fp32 registers");
-  constexpr int NV = Chunk<DT, VEC>::NV;
+template <int DT, int VEC, int NR>
+__device__ __forceinline__ void apply_counts(Chunk<DT, VEC, NR>& C, int n, const PenArgs& pa) {
+  static_assert(!Chunk<DT, VEC, NR>::PACKED, "in-place penalties are for fp32 registers");
+  constexpr int NV = Chunk<DT, VEC, NR>::NV;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
     const int l0 = (v * FT + (int)threadIdx.x) * VEC;
@@ -382,10 +397,10 @@ __device__ __forceinline__ void apply_counts(Chunk<DT, VEC>& C, int n, const Pen
   }
 }
 // Packed chunks: flag the slots with an 8-bit count.
-template <int DT, int VEC>
-__device__ __forceinline__ void mark_counts(Chunk<DT, VEC>& C, int n, const PenArgs& pa) {
-  static_assert(Chunk<DT, VEC>::PACKED, "flags are for packed registers");
-  constexpr int NV = Chunk<DT, VEC>::NV;
+template <int DT, int VEC, int NR>
+__device__ __forceinline__ void mark_counts(Chunk<DT, VEC, NR>& C, int n, const PenArgs& pa) {
+  static_assert(Chunk<DT, VEC, NR>::PACKED, "flags are for packed registers");
+  constexpr int NV = Chunk<DT, VEC, NR>::NV;
   uint64_t m = 0;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
@@ -428,8 +443,9 @@ struct SelLevel {
 };
 // Key range of the present candidates; clears histogram buffer 0 (nb bins of
 // cnt0, and of m0 when given) before its barrier.
+template <class FS>
 __device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np, uint32_t* cnt0, int nb,
-                                              unsigned long long* m0, FShared& S) {
+                                              unsigned long long* m0, FS& S) {
   uint32_t mn = 0xFFFFFFFFu, mx = 0;
 #pragma unroll
   for (int e = 0; e < FCPT; e++)
@@ -451,7 +467,8 @@ __device__ __forceinline__ SelLevel sel_range(const uint32_t (&ck)[FCPT], int np
 }
 
 // kk-th largest present key (1 <= kk <= number present).
-__device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np, uint32_t kk, FShared& S) {
+template <class FS>
+__device__ __forceinline__ uint32_t sel_count(const uint32_t (&ck)[FCPT], int np, uint32_t kk, FS& S) {
   auto& H = S.x.cnt;
   const SelLevel L = sel_range(ck, np, H[0], SELB, nullptr, S);
   if (L.bits == 0) return L.base;
@@ -503,9 +520,9 @@ struct MassSel {
   uint64_t meq;
   int ok;
 };
-template <typename MF>
+template <typename MF, class FS>
 __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, MF mass, uint64_t A, uint64_t P,
-                                            FShared& S) {
+                                            FS& S) {
   MassSel ms{0, A, 0, 0, 0};
   auto& H = S.x.selm;
   const SelLevel L = sel_range(ck, np, H.cnt[0], SELBM, H.mass[0], S);

@@ -11,7 +11,7 @@
 // Counters are only touched with atomics, which execute at the L2, except
 // their reset to zero, plain stores by the row's finaliser.
 //
-// Cross-wave exchange slots of FShared (xa ... xh, xv, mi, m64, md) are each
+// Cross-wave exchange slots of XShared (xa ... xh, xv, mi, m64, md, mf) are each
 // rewritten only after a barrier that follows every read of their previous
 // value; the comments name the slot each step uses.
 #pragma once
@@ -23,7 +23,7 @@ namespace lps {
 // Block-wide penalised logit of one id (history scanned by all threads).
 template <int DT>
 __device__ float penalized_logit(const void* row, int id, const int32_t* h, int hlen, bool pen, float rep,
-                                 float pres, float freq, FShared& S) {
+                                 float pres, float freq, XShared& S) {
   uint32_t c = 0;
   if (pen)
     for (int j = threadIdx.x; j < hlen; j += FT) c += h[j] == id ? 1u : 0u;
@@ -37,7 +37,8 @@ __device__ float penalized_logit(const void* row, int id, const int32_t* h, int 
 
 // Rank sort of the kept list by (z desc, idx asc), i.e. by skey desc:
 // kord[rank] = slot.  LDS reads are batched 8 at a time (independent loads).
-__device__ void rank_sort_kept(int K, FShared& S) {
+template <class FS>
+__device__ void rank_sort_kept(int K, FS& S) {
   auto& k = S.x.k;
   for (int i = threadIdx.x; i < K; i += FT) {
     const uint64_t ki = k.skey[i];
@@ -71,7 +72,8 @@ __device__ __forceinline__ int count_below(const int32_t* a, int n, int v) {
 }
 
 // Inclusive prefix of km over the sorted order into cum, K <= KEPTCAP (slot xb).
-__device__ void sorted_prefix(int K, FShared& S) {
+template <class FS>
+__device__ void sorted_prefix(int K, FS& S) {
   auto& k = S.x.k;
   constexpr int PER = KEPTCAP / FT;
   uint64_t loc[PER];
@@ -159,11 +161,37 @@ __device__ __forceinline__ ChunkId chunk_id(int G) {
   return ChunkId{(slot / G) * 8 + xcd, slot % G};
 }
 
+// Fused kernel row order (R <= 128): rows that sample without top-k (nucleus /
+// pure: the longest finalisers) are dispatched first, so that their
+// finalisers overlap the chunk work of the rows dispatched after them.
+// Virtual row vr -> row; a bijection on [0, R), the same in every workgroup.
+__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr) {
+  const int lane = threadIdx.x & 63;
+  auto heavy = [&](int r) -> bool {
+    if (r >= P.R) return false;
+    const float T = P.temperature ? P.temperature[r] : P.temperature_def;
+    const int k = P.top_k ? P.top_k[r] : P.top_k_def;
+    return T > 0.0f && k <= 0;
+  };
+  const uint64_t m1 = wballot(heavy(lane)), m2 = wballot(heavy(lane + 64));
+  const uint64_t v1 = wballot(lane < P.R), v2 = wballot(lane + 64 < P.R);
+  const int nh = __popcll(m1) + __popcll(m2);
+  const bool hv = vr < nh;
+  const uint64_t a = hv ? m1 : (v1 & ~m1), b = hv ? m2 : (v2 & ~m2);
+  const int k = hv ? vr : vr - nh;
+  const int pa = __popcll(a);
+  const uint64_t sel = k < pa ? a : b;
+  const int kk = k < pa ? k : k - pa;
+  const uint64_t w = wballot(((sel >> lane) & 1ull) && (int)lanes_below(sel) == kk);
+  return (k < pa ? 0 : 64) + (int)__builtin_ctzll(w);
+}
+
 // Phase 1: chunk j of row r (r < R).  Returns the row's mode; a deferred row
 // (MODE_DEFER) publishes nothing.
-template <int DT, int VEC>
-__device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const int r, const int j) {
-  using CK = Chunk<DT, VEC>;
+template <int DT, int VEC, int NR>
+__device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, const int r, const int j) {
+  using CK = Chunk<DT, VEC, NR>;
+  constexpr int PUB = CK::PUB;
   constexpr int NE = CK::NE, CH = CK::CH;
   constexpr bool PK = CK::PACKED;
   const KParams& P = F.k;
@@ -294,7 +322,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
 #pragma unroll
         for (int s = 0; s < NE; s++) {
           const float w = __fmul_rn(C.template val<PEN>(s, pa), c);
-          const float e = exp2f(__fsub_rn(w, wm));
+          const float e = chunk_mass(w, wm);
           acc += (double)e;
           if (e > 0.0f) {
             const int hb = btop - (int)floorf(__fmul_rn(w, (float)HS));
@@ -303,7 +331,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
         }
       } else {
 #pragma unroll
-        for (int s = 0; s < NE; s++) acc += (double)exp2f(__fsub_rn(__fmul_rn(C.template val<PEN>(s, pa), c), wm));
+        for (int s = 0; s < NE; s++) acc += (double)chunk_mass(__fmul_rn(C.template val<PEN>(s, pa), c), wm);
       }
     });
   }
@@ -346,7 +374,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
     uint32_t tot;
     uint32_t p = bscan_excl<uint32_t>(cnt, &tot, S.xh);
     LPS_STAMP(27);
-    uint2* out = cands + (int64_t)j * PUBCAP;
+    uint2* out = cands + (int64_t)j * PUB;
     if (cnt) {
       with_pen<PK>(wpen, [&](auto PT) {
         constexpr bool PEN = decltype(PT)::value;
@@ -355,14 +383,14 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
           const float v = C.template val<PEN>(s, pa);
           const int l = CK::local(s);
           if (l < n && v >= xth) {
-            if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(v), (uint32_t)(lo + l));
+            if (p < (uint32_t)PUB) out[p] = make_uint2(f2key(v), (uint32_t)(lo + l));
             p++;
           }
         }
       });
     }
-    ncand = tot > (uint32_t)PUBCAP ? (uint32_t)PUBCAP : tot;
-    if (tot > (uint32_t)PUBCAP) cflags |= CF_OVERFLOW;
+    ncand = tot > (uint32_t)PUB ? (uint32_t)PUB : tot;
+    if (tot > (uint32_t)PUB) cflags |= CF_OVERFLOW;
   }
   LPS_STAMP(4);
 
@@ -465,7 +493,8 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
       // this chunk: mass and count above the region, candidates inside (slots xa xb xc)
       const int hbt = btop - (bhi + 1);  // chunk histogram bins 0..hbt lie above the region
       uint64_t am = (xm_finite && tid <= hbt) ? (uint64_t)S.hm[tid] : 0ull;
-      uint32_t na = 0, nc = 0, inreg = 0;
+      uint32_t na = 0, nc = 0;
+      uint64_t inreg = 0;
       with_pen<PK>(wpen, [&](auto PT) {
         constexpr bool PEN = decltype(PT)::value;
 #pragma unroll
@@ -476,7 +505,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
             na += b > bhi ? 1u : 0u;
             const bool in = b >= blo && b <= bhi;
             nc += in ? 1u : 0u;
-            if (NE <= 32) inreg |= in ? (1u << (s & 31)) : 0u;
+            if (NE <= 64) inreg |= in ? (1ull << (s & 63)) : 0ull;
           }
         }
       });
@@ -487,7 +516,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
       uint32_t p = bscan_excl<uint32_t>(nc, &ctot, S.xc);
       above = S.xa[0] + S.xa[1] + S.xa[2] + S.xa[3];
       nabove = (uint32_t)(S.xb[0] + S.xb[1] + S.xb[2] + S.xb[3]);
-      uint2* out = cands + (int64_t)j * PUBCAP;
+      uint2* out = cands + (int64_t)j * PUB;
       if (nc) {
         with_pen<PK>(wpen, [&](auto PT) {
           constexpr bool PEN = decltype(PT)::value;
@@ -495,8 +524,8 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
           for (int s = 0; s < NE; s++) {
             bool in;
             float v;
-            if constexpr (NE <= 32) {
-              in = (inreg >> s) & 1u;
+            if constexpr (NE <= 64) {
+              in = (inreg >> s) & 1ull;
               v = in ? C.template val<PEN>(s, pa) : 0.0f;
             } else {
               v = C.template val<PEN>(s, pa);
@@ -504,14 +533,14 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
               in = b >= blo && b <= bhi;
             }
             if (in) {
-              if (p < (uint32_t)PUBCAP) out[p] = make_uint2(f2key(v), (uint32_t)(lo + CK::local(s)));
+              if (p < (uint32_t)PUB) out[p] = make_uint2(f2key(v), (uint32_t)(lo + CK::local(s)));
               p++;
             }
           }
         });
       }
-      ncand = ctot > (uint32_t)PUBCAP ? (uint32_t)PUBCAP : ctot;
-      if (ctot > (uint32_t)PUBCAP) cflags |= CF_OVERFLOW;
+      ncand = ctot > (uint32_t)PUB ? (uint32_t)PUB : ctot;
+      if (ctot > (uint32_t)PUB) cflags |= CF_OVERFLOW;
     }
     LPS_STAMP(20);
   }
@@ -530,9 +559,10 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CShared& S, const in
 // it runs in the row's last chunk workgroup, in the chunks' kernel, and reads
 // their data through the XCD's L2.  Returns 0 when the row is done, or a
 // positive reason code when the general algorithm must sample it.
-template <int DT, int VEC>
-__device__ __forceinline__ int final_body(const FParams& F, FShared& S, const int r, const bool fused) {
-  using CK = Chunk<DT, VEC>;
+template <int DT, int VEC, int NR>
+__device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, const int r, const bool fused) {
+  using CK = Chunk<DT, VEC, NR>;
+  constexpr int PUB = CK::PUB;
   constexpr int CH = CK::CH, NV = CK::NV;
   constexpr bool PK = CK::PACKED;
   const KParams& P = F.k;
@@ -646,19 +676,35 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
 #pragma unroll
     for (int step = MAXG / 2; step > 0; step >>= 1)
       if (q + step < G && (int)S.pre[q + step] <= i) q += step;
-    return cands[(int64_t)q * PUBCAP + (i - (int)S.pre[q])];
+    return cands[(int64_t)q * PUB + (i - (int)S.pre[q])];
   };
   // Candidates in registers: thread t holds candidate e * FT + t in slot e (z key, index).
   uint32_t ck[FCPT];
   int32_t ci[FCPT];
   const int np = NC > tid ? min((NC - tid + FT - 1) / FT, FCPT) : 0;
-  // All loads first (clamped to a valid candidate, no branch between them), then the keys.
+  // The chunk of every slot's candidate by one binary search over pre[], its
+  // steps interleaved over the slots (one LDS round trip per step), then all
+  // loads (clamped to a valid candidate, no branch between them), then the keys.
   auto load_cands = [&]() {
     const int npmax = min((NC + FT - 1) / FT, FCPT);  // slots any thread uses
+    auto idx = [&](int e) { return min(e * FT + tid, NC - 1); };
+    int q[FCPT];
+#pragma unroll
+    for (int e = 0; e < FCPT; e++) q[e] = 0;
+#pragma unroll
+    for (int step = MAXG / 2; step > 0; step >>= 1) {
+      int pv[FCPT];
+#pragma unroll
+      for (int e = 0; e < FCPT; e++) pv[e] = (int)S.pre[min(q[e] + step, G)];  // pre[G] = NC > any index
+#pragma unroll
+      for (int e = 0; e < FCPT; e++) q[e] += (q[e] + step < G && pv[e] <= idx(e)) ? step : 0;
+    }
+#pragma unroll
+    for (int e = 0; e < FCPT; e++) q[e] = q[e] * PUB + (idx(e) - (int)S.pre[q[e]]);  // slot in cands
     uint2 cv[FCPT];
 #pragma unroll
     for (int e = 0; e < FCPT; e++)
-      if (e < npmax) cv[e] = cand_at(min(e * FT + tid, NC - 1));
+      if (e < npmax) cv[e] = cands[q[e]];
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       const bool pr = e < np;
@@ -822,6 +868,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
       // exact cut among the region candidates, above-region masses rescaled to the row
       if (NC > FCAP) return 64;
       load_cands();
+      LPS_FSTAMP(25);
       auto cmass = [&](int e) -> uint64_t { return mass_fixed(mass_f(key2f(ck[e]), zmax)); };
       const uint64_t Af = (uint64_t)(Aabove * (double)kMassScale);
       const uint64_t Pf = (uint64_t)((double)topp * Zfull * (double)kMassScale);
@@ -848,32 +895,43 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
         for (int e = 0; e < FCPT; e++)
           if (e < np && ck[e] == vkey) kl.kidx[p++] = ci[e];
         __syncthreads();
+        LPS_FSTAMP(29);
         for (int i = tid; i < (int)ttot; i += FT) {
           const int ii = kl.kidx[i];
           if (count_below(kl.kidx, (int)ttot, ii) == (int)n_tie - 1) S.mi[25] = ii;
         }
       }
-      // any x of the cut's collision group (reloaded: x keys are not kept in registers)
+      // one candidate of the cut key (any: its x is reloaded by one thread)
 #pragma unroll
       for (int e = 0; e < FCPT; e++)
-        if (e < np && ck[e] == vkey) S.mi[26] = (int)cand_at(e * FT + tid).x;
+        if (e < np && ck[e] == vkey) S.mi[26] = e * FT + tid;
       __syncthreads();
       tie_lim = S.mi[25];
       LPS_FSTAMP(18);
       if (tid == 0) {
-        // the cut's whole division-collision group must lie inside the region
-        const float xv = key2f((uint32_t)S.mi[26]);
-        const float xl = collision_lo(xv, T);
-        float xh = xv;
-        for (int it = 0; it < 64; it++) {
+        // the cut's division-collision group [xl, xh] = {x : fl(x / T) == cut},
+        // which must lie inside the region
+        const float xv = key2f(cand_at(S.mi[26]).x);
+        const float zc = key2f(vkey);
+        float xl = xv, xh = xv;
+        bool ended = false;
+        for (int it = 0; it < 64 && !ended; it++) {
+          const uint32_t k = f2key(xl);
+          const float y = key2f(k - 1u);
+          if (k <= kNegInfKey + 1u || __fdiv_rn(y, T) != zc) ended = true;
+          else xl = y;
+        }
+        bool ended2 = false;
+        for (int it = 0; it < 64 && !ended2; it++) {
           const uint32_t k = f2key(xh);
-          if (k >= 0xFFFFFFFEu) break;
           const float y = key2f(k + 1u);
-          if (__fdiv_rn(y, T) != key2f(vkey)) break;
-          xh = y;
+          if (k >= 0xFFFFFFFEu || __fdiv_rn(y, T) != zc) ended2 = true;
+          else xh = y;
         }
         const int bl = wbin(xl, c), bh = wbin(xh, c);
-        S.mi[27] = (bl >= blo && bh <= bhi) ? 1 : 0;
+        S.mi[27] = (ended && ended2 && bl >= blo && bh <= bhi) ? 1 : 0;
+        S.mf[0] = xl;
+        S.mf[1] = xh;
       }
       // kept candidate mass per chunk and count (slot xg)
       uint32_t lc = 0;
@@ -887,6 +945,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
           lc++;
         }
       }
+      LPS_FSTAMP(12);
       lc = wsum(lc);
       if (lane == 0) S.xg[wv] = lc;
       __syncthreads();
@@ -938,6 +997,9 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
       // Kept mass of slot (v, e) with the formulas that built the chunk's kept
       // mass: exp2(x c - wm) * scale outside the cut region (as the chunk pass
       // summed it), the finaliser's exp(z - zmax) for region candidates.
+      // Region candidates are kept when z = fl(x / T) is above the cut, i.e.
+      // x > xh, or in the cut's collision group [xl, xh] with index <= tie_lim.
+      const float cxl = S.mf[0], cxh = S.mf[1];
       auto kept_m = [&](int v, int e) -> double {
         const float yv = Y.template val<true>(v * VEC + e, pa2);
         if (yv == -INFINITY || yv != yv) return 0.0;
@@ -946,14 +1008,11 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
           const int b = (int)floorf(__fmul_rn(w, (float)HS));
           if (b < blo) return 0.0;
           if (b <= bhi) {
-            const float z = __fdiv_rn(yv, T);
-            const uint32_t kz = f2key(z);
-            const int gi = lo2 + (v * FT + tid) * VEC + e;
-            if (!(kz > vkey || (kz == vkey && gi <= tie_lim))) return 0.0;
-            return (double)mass_fixed(mass_f(z, zmax)) / (double)kMassScale;
+            if (yv < cxl || (yv <= cxh && lo2 + (v * FT + tid) * VEC + e > tie_lim)) return 0.0;
+            return (double)mass_fixed(mass_f(__fdiv_rn(yv, T), zmax)) / (double)kMassScale;
           }
         }
-        return (double)exp2f(__fsub_rn(w, wmj)) * scj;
+        return (double)chunk_mass(w, wmj) * scj;
       };
       // Vocabulary order is (v, thread, e).  Groups are scanned in batches of NB;
       // each thread keeps its first group whose cumulative end passes the target
@@ -996,6 +1055,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
         }
         __syncthreads();
       }
+      LPS_FSTAMP(26);
       {
         const int f = wmin(myfirst), l = wmax(mylast);
         if (lane == 0) { S.xc[wv] = (uint32_t)f; S.xf[wv] = (uint32_t)l; }
@@ -1006,6 +1066,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
       const int gl = max(max((int)S.xf[0], (int)S.xf[1]), max((int)S.xf[2], (int)S.xf[3]));
       const bool found = gf != 0x7FFFFFFF;
       const int pick = found ? gf : gl;
+      LPS_FSTAMP(27);
       if (pick >= 0 && (pick % FT) == tid) {
         // walk the group: the first kept element whose cumulative end passes the
         // target, or (no group passed it: rounding at the top end) the last kept one
@@ -1089,10 +1150,10 @@ __device__ __forceinline__ int final_body(const FParams& F, FShared& S, const in
 // Split path, phase 1: grid of ceil(R / 8) * 8 * G workgroups.
 template <int DT, int VEC>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(FParams F) {
-  __shared__ CShared S;
+  __shared__ CSharedT<32> S;
   const ChunkId c = chunk_id(F.G);
   if (c.r >= F.k.R) return;
-  chunk_body<DT, VEC>(F, S, c.r, c.j);
+  chunk_body<DT, VEC, 32>(F, S, c.r, c.j);
 }
 
 // Split path, phase 2: one workgroup per row.  A row the fast path cannot
@@ -1101,24 +1162,35 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 // filter, samples it.
 template <int DT, int VEC>
 __global__ __launch_bounds__(FT) void final_kernel(FParams F) {
-  __shared__ FShared S;
+  __shared__ FSharedT<32> S;
   const int r = blockIdx.x;
-  const int reason = final_body<DT, VEC>(F, S, r, false);
+  const int reason = final_body<DT, VEC, 32>(F, S, r, false);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }
 
 // Fused path (grids that fit on the GPU at once): the chunk kernel whose last
 // workgroup of each row to finish, counted by an L2 atomic, finalises the row
 // while other rows are still in their chunk phase.
+#ifndef LPS_FUSED_WPE
+#define LPS_FUSED_WPE 3
+#endif
+#ifndef LPS_FUSED_NR16
+#define LPS_FUSED_NR16 32
+#endif
+// Logit registers per thread of the fused kernel: 16384-logit chunks for
+// 16-bit logits (read as 16 bytes = 8 logits per load), 8192 for fp32.
+template <int DT>
+constexpr int fused_nr() { return DT == LPS_DTYPE_F32 ? 32 : LPS_FUSED_NR16; }
 template <int DT, int VEC>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(3, 8))) void fused_kernel(FParams F) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WPE, 8))) void fused_kernel(FParams F) {
   __shared__ union {
-    CShared c;
-    FShared f;
+    CSharedT<fused_nr<DT>()> c;
+    FSharedT<fused_nr<DT>()> f;
   } SU;
-  const ChunkId c = chunk_id(F.G);
+  ChunkId c = chunk_id(F.G);
   if (c.r >= F.k.R) return;
-  const int mode = chunk_body<DT, VEC>(F, SU.c, c.r, c.j);
+  if (F.heavy_first) c.r = heavy_first_row(F.k, c.r);
+  const int mode = chunk_body<DT, VEC, fused_nr<DT>()>(F, SU.c, c.r, c.j);
   if (mode == MODE_DEFER) {
     if (c.j == 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1129,7 +1201,7 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(3, 8))) void
   if (threadIdx.x == 0) SU.c.mi[5] = l2_fetch_add(F.counters + (int64_t)c.r * 32, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
   __syncthreads();
   if (!SU.c.mi[5]) return;
-  const int reason = final_body<DT, VEC>(F, SU.f, c.r, true);
+  const int reason = final_body<DT, VEC, fused_nr<DT>()>(F, SU.f, c.r, true);
   if (reason > 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (reason << 8);
 }
 
