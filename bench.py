@@ -8,10 +8,14 @@ histories).  Inputs are resident in HBM before timing; launches rotate over
 >= 2 x 256 MB of distinct logits buffers so the MALL cannot serve the reads,
 and are replayed from a HIP graph so host overhead does not gap the GPU.
 
-Prints ONE JSON line (rank 0, N=1) with the roofline of the sampling kernel
+Prints ONE JSON line (rank 0, N=1) with the roofline of the sampling launch
 (algorithmic bytes per launch / average launch time, against 8 TB/s) and the
 CPU baseline (the oracle's op-for-op torch-CPU restatement of the reference
-sampler, row by row, timed on this host's cores).
+sampler, row by row, timed on this host's cores).  One ``lps_sample`` launch is
+the fast kernel(s) plus the filtered general-kernel launch for deferred rows;
+the launch time covers both (the filter launch is ~1-2 us when no row is
+deferred), so the roofline is that of the dominant fast kernel measured with
+the short filter launch included.
 """
 
 from __future__ import annotations
@@ -78,12 +82,22 @@ def build_args(w, dev, logits_dev, out, lib_mod):
     return a
 
 
-def hbm_traffic(config: str):
-    """HBM bytes per launch of the sampling kernel for a workload, as measured by
+def fast_path_kernel(w) -> str:
+    """The fast kernel(s) lps_sample picks for a workload (the host rule in
+    lps.hip: 16-byte-vector rows whose grid of 8192-logit chunk workgroups is at
+    most 2048 take the fused kernel, others the chunk + final pair)."""
+    es = 4 if str(w.logits.dtype) == "torch.float32" else 2
+    vec = w.V % (16 // es) == 0
+    grid = (w.B + 7) // 8 * 8 * ((w.V + 8191) // 8192)
+    return "fused_kernel" if vec and grid <= 2048 else "chunk_final_kernels"
+
+
+def hbm_traffic(kernel: str, config: str):
+    """HBM bytes per launch of the sampling kernels for a workload, as measured by
     rocprofv3 FETCH_SIZE + WRITE_SIZE passes and scaled by the same counters on a
-    plain copy of known size (profiles/fast_kernel_<config>_hbm_traffic.md,
+    plain copy of known size (profiles/<kernel>_<config>_hbm_traffic.md,
     line 'traffic_bytes_per_launch: N'); None when no such measurement exists."""
-    path = os.path.join(REPO, "profiles", f"fast_kernel_{config}_hbm_traffic.md")
+    path = os.path.join(REPO, "profiles", f"{kernel}_{config}_hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
@@ -265,7 +279,7 @@ def main():
                               "1024 ids/row, chosen + top-20 logprobs"}[args.config],
            "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
            "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes,
-           "kernel": "gen_row_kernel" if args.generic else "fast_kernel"}
+           "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w) + " + gen_row_kernel (deferred-row filter)"}
     line = {
         "metric": METRIC if args.config == "c2" else f"sampled rows/sec ({args.config})",
         "value": round(rows_s, 1),
@@ -282,7 +296,7 @@ def main():
         "config": cfg,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None if args.generic else hbm_traffic(args.config)},
+                     "traffic": None if args.generic else hbm_traffic(fast_path_kernel(w), args.config)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -251,7 +251,7 @@ __device__ void clear_hist(GenShared& S) {
 // kk-th largest key (1-based, counting multiplicity) of keyf over the row.
 // Returns the key; *n_above = number of elements with a strictly larger key.
 template <int DT, int VEC, typename KF>
-__device__ uint32_t select_kth(const void* row, int V, const PenCtx& pc, GenShared& S, uint32_t kk, KF keyf,
+__device__ __forceinline__ uint32_t select_kth(const void* row, int V, const PenCtx& pc, GenShared& S, uint32_t kk, KF keyf,
                                uint32_t* n_above) {
   uint32_t prefix = 0;
   uint32_t above = 0;
@@ -286,7 +286,7 @@ struct MassCut {
 
 // Largest key v with mass(active, key >= v) > limit (limit < total active mass).
 template <int DT, int VEC, typename KF, typename AF>
-__device__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShared& S, uint64_t limit, KF keyf,
+__device__ __forceinline__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShared& S, uint64_t limit, KF keyf,
                                AF massf) {
   uint32_t prefix = 0;
   uint64_t A = 0;
@@ -326,7 +326,7 @@ __device__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShar
 // The kernel.
 // ---------------------------------------------------------------------------
 template <int DT, int VEC>
-__device__ void gen_row(const KParams& P, const int r, GenShared& S) {
+__device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared& S) {
   const int tid = threadIdx.x;
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   const void* row = reinterpret_cast<const char*>(P.logits) +
