@@ -76,6 +76,9 @@ def build_args(w, dev, logits_dev, out, lib_mod):
         a.top_ids = out["ti"].data_ptr()
         a.n_top = w.n_top
     a.flags = out.get("flags", 0)
+    if out.get("allowed") is not None:
+        a.allowed = out["allowed"].data_ptr()
+        a.allowed_stride = out["allowed"].stride(0)
     if out.get("ws") is not None:
         a.workspace = out["ws"].data_ptr()
         a.workspace_bytes = out["ws"].numel()
@@ -160,6 +163,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
+    ap.add_argument("--allowed-frac", type=float, default=None,
+                    help="add a random legality mask with this fraction of legal ids per row")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -203,10 +208,16 @@ def main():
         "ti": torch.empty((B, max(w.n_top, 1)), dtype=torch.int64, device=dev),
     }
     io["flags"] = 1 if args.generic else 0
+    if args.allowed_frac is not None:
+        from lps import pack_allowed
+        gm = torch.Generator().manual_seed(11)
+        io["allowed"] = pack_allowed((torch.rand((B, w.V), generator=gm) < args.allowed_frac).to(dev))
     wsb = lib.lps_workspace_bytes(B, w.V, io["flags"])
     io["ws"] = torch.zeros((max(wsb, 1),), dtype=torch.uint8, device=dev) if wsb else None
     arglist = [build_args(w, dev, b, io, lib) for b in bufs]
     extra = (B * 4 + B * w.n_top * 12) if w.logprobs else 0
+    if io.get("allowed") is not None:
+        extra += B * ((w.V + 31) // 32) * 4  # the legality bits, read once
     abytes = alg_bytes(w, extra)
 
     def launch(i):
@@ -280,6 +291,8 @@ def main():
            "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
            "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes,
            "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w) + " + gen_row_kernel (deferred-row filter)"}
+    if args.allowed_frac is not None:
+        cfg["legality_mask"] = f"random, {args.allowed_frac:.0%} of ids legal per row, packed bits"
     line = {
         "metric": METRIC if args.config == "c2" else f"sampled rows/sec ({args.config})",
         "value": round(rows_s, 1),

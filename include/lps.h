@@ -151,6 +151,15 @@ typedef struct lps_sample_args {
    * that overlap in time must not share a workspace. */
   void* workspace;
   size_t workspace_bytes;
+
+  /* optional legality mask, the packed form of the reference's logit
+   * constraints (constraints.py:53-80, LogitConstraint.apply_to_logits sets
+   * illegal ids to -inf before sampling): id i is legal for row r when bit
+   * (i & 31) of allowed[r * allowed_stride + (i >> 5)] is set.  Illegal ids
+   * count as -inf logits in every step and every output (logprobs included).
+   * NULL = every id legal. */
+  const uint32_t* allowed;
+  int64_t allowed_stride;         /* 32-bit words per row, >= ceil(V / 32) */
 } lps_sample_args;
 
 typedef struct lps_spec_args {

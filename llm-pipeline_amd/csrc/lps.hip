@@ -158,6 +158,7 @@ KParams row_block(const KParams& P, int r0, int nr, int es) {
   B.kept_count = P.kept_count ? P.kept_count + r0 : nullptr;
   B.row_path = P.row_path ? P.row_path + r0 : nullptr;
   B.plans = P.plans ? P.plans + r0 : nullptr;
+  B.allowed = P.allowed ? P.allowed + (int64_t)r0 * P.allowed_stride : nullptr;
   return B;
 }
 
@@ -281,6 +282,7 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   if (!a->uniforms && !a->skip_draw) return LPS_EINVAL;
   if (a->history && (!a->history_len || a->history_stride < 0)) return LPS_EINVAL;
   if (a->query_tokens && (a->query_inner < 0 || a->query_inner > a->rows_inner)) return LPS_EINVAL;
+  if (a->allowed && a->allowed_stride < (int64_t)((a->vocab + 31) / 32)) return LPS_EINVAL;
   KParams P = neutral_params();
   P.logits = a->logits;
   P.V = a->vocab;
@@ -317,6 +319,8 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   P.plans = nullptr;
   P.only_status = nullptr;
   P.row_path = a->row_path;
+  P.allowed = a->allowed;
+  P.allowed_stride = a->allowed_stride;
   if (a->workspace && a->workspace_bytes < lps_workspace_bytes(a->num_rows, a->vocab, a->flags)) return LPS_EWORKSPACE;
   const bool vec = vec_ok(a->logits, a->dtype, a->vocab, a->rows_inner, a->stride_outer, a->stride_inner);
   hipError_t e = run_sample(P, a->dtype, vec, a->workspace, a->workspace_bytes, a->flags,

@@ -319,6 +319,33 @@ struct Chunk {
       }
     }
   }
+  // Slot s to -inf.
+  __device__ __forceinline__ void kill(int s) {
+    if constexpr (!PACKED) {
+      r[s] = __float_as_uint(-INFINITY);
+    } else {
+      const uint32_t sh = 16u * (uint32_t)(s & 1);
+      r[s >> 1] = (r[s >> 1] & ~(0xFFFFu << sh)) | (NEG16 << sh);
+    }
+  }
+  // Illegal ids of [lo, lo + n) to -inf, from the row's legality bits am (one
+  // byte read per vector, clamped inside the row; nullptr: every id legal).
+  __device__ __forceinline__ void mask(const uint8_t* am, int lo, int n) {
+    if (!am) return;
+    constexpr int NVS = VEC == 1 ? NR : NV;  // reads per thread
+    uint32_t b[NVS];
+#pragma unroll
+    for (int v = 0; v < NVS; v++) {
+      const int l0 = VEC == 1 ? v * FT + (int)threadIdx.x : (v * FT + (int)threadIdx.x) * VEC;
+      b[v] = (uint32_t)am[(lo + min(l0, n - 1)) >> 3] >> ((lo + min(l0, n - 1)) & 7);
+    }
+#pragma unroll
+    for (int v = 0; v < NVS; v++) {
+#pragma unroll
+      for (int e = 0; e < VEC; e++)
+        if (!((b[v] >> e) & 1u)) kill(v * VEC + e);
+    }
+  }
 };
 
 // History ids of the row, the first HPF * FT of them, read before the chunk so

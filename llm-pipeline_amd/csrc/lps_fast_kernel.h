@@ -22,8 +22,8 @@ namespace lps {
 
 // Block-wide penalised logit of one id (history scanned by all threads).
 template <int DT>
-__device__ float penalized_logit(const void* row, int id, const int32_t* h, int hlen, bool pen, float rep,
-                                 float pres, float freq, XShared& S) {
+__device__ float penalized_logit(const void* row, const uint8_t* am, int id, const int32_t* h, int hlen, bool pen,
+                                 float rep, float pres, float freq, XShared& S) {
   uint32_t c = 0;
   if (pen)
     for (int j = threadIdx.x; j < hlen; j += FT) c += h[j] == id ? 1u : 0u;
@@ -31,6 +31,7 @@ __device__ float penalized_logit(const void* row, int id, const int32_t* h, int 
   c = bcombine(wsum(c), S.xh, OpAdd{});
   __syncthreads();
   float x = load1<DT>(row, id);
+  if (!id_allowed(am, id)) x = -INFINITY;
   if (pen && c) x = penalize(x, (int)c, rep, pres, freq);
   return x;
 }
@@ -215,6 +216,8 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
   prefetch_history(P.history ? P.history + (int64_t)r * P.history_stride : nullptr, P.history_stride, hp);
   CK C;
   C.load(row, lo, n);
+  const uint8_t* am = row_allowed(P, r);
+  C.mask(am, lo, n);
 
   const RowCfg g = row_cfg(P, r);
   const float T = g.T, topp = g.topp, rep = g.rep, pres = g.pres, freq = g.freq;
@@ -983,6 +986,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       prefetch_history(hrow, P.history_stride, hp2);
       CK Y;
       Y.load(row, lo2, n2);
+      Y.mask(row_allowed(P, r), lo2, n2);
       const PenArgs pa2{S.x.hc, rep, pres, freq};
       if (pen) {  // (a row whose counts did not fit never reaches the finaliser)
         if constexpr (PK) {
@@ -1098,7 +1102,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       chosen_z = (float)S.md[7];
     }
     if (P.query_prob && qtok >= 0) {
-      const float xq = penalized_logit<DT>(row, (int)qtok, hrow, hlen, pen, rep, pres, freq, S);
+      const float xq = penalized_logit<DT>(row, row_allowed(P, r), (int)qtok, hrow, hlen, pen, rep, pres, freq, S);
       const float zq = __fdiv_rn(xq, T);
       if (mode == MODE_PURE) {
         qprob = zq != -INFINITY ? (float)((double)mass_f(zq, zmax) / Zf) : 0.0f;

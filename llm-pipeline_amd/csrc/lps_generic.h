@@ -65,7 +65,17 @@ struct KParams {
   RowPlan* plans;
   const int32_t* only_status;  // non-null: process only rows whose entry has LPS_ROW_DEFERRED (8) set
   int32_t* row_path;           // optional: 0 fast kernel, 1 general kernel
+  const uint32_t* allowed;     // optional legality bits, row r at allowed + r * allowed_stride
+  int64_t allowed_stride;      // 32-bit words
 };
+// Row r's legality bits (nullptr: every id legal).
+__device__ __forceinline__ const uint8_t* row_allowed(const KParams& P, int r) {
+  return P.allowed ? reinterpret_cast<const uint8_t*>(P.allowed + (int64_t)r * P.allowed_stride) : nullptr;
+}
+// Whether id i is legal under the row's legality bits.
+__device__ __forceinline__ bool id_allowed(const uint8_t* am, int64_t i) {
+  return !am || ((am[i >> 3] >> (i & 7)) & 1u);
+}
 // Workspace row status bit (beside the LPS_ROW_* bits): the fast kernels
 // deferred the row to the general kernel.
 constexpr int32_t LPS_ROW_DEFERRED = 8;
@@ -100,6 +110,7 @@ struct PenCtx {
   const uint32_t* bloom;
   const int32_t* hkey;
   const int32_t* hcnt;
+  const uint8_t* am;  // the row's legality bits, or nullptr
 
   __device__ __forceinline__ int lookup(int id) const {
     uint32_t s = hash_id(id);
@@ -111,8 +122,16 @@ struct PenCtx {
     }
     return 0;
   }
+  // Illegal ids to -inf, then the penalties, on the VEC logits of ids
+  // [i0, i0 + VEC) (i0 a multiple of VEC, VEC in {1, 4, 8}).
   template <int VEC>
   __device__ __forceinline__ void apply(int64_t i0, float (&x)[VEC]) const {
+    if (am) {
+      const uint32_t b = (uint32_t)am[i0 >> 3] >> (i0 & 7);
+#pragma unroll
+      for (int j = 0; j < VEC; j++)
+        if (!((b >> j) & 1u)) x[j] = -INFINITY;
+    }
     if (!active) return;
     uint32_t w = bloom[(i0 >> 5) & (BLOOM_WORDS - 1)] >> (i0 & 31);
     if (VEC < 32) w &= (1u << VEC) - 1u;
@@ -375,7 +394,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     used = gblock_sum_u32(used, S);
     if (used > LPS_MAX_HISTORY_DISTINCT) status |= LPS_ROW_HISTORY_OVERFLOW;
   }
-  PenCtx pc{pen, rep, pres, freq, S.bloom, S.hkey, S.hcnt};
+  PenCtx pc{pen, rep, pres, freq, S.bloom, S.hkey, S.hcnt, row_allowed(P, r)};
 
   // ---- pass 1: max and first argmax of the penalised logits ----
   uint64_t best = 0;
@@ -626,9 +645,8 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     if (P.chosen_logprob && tid == 0) {
       float lp = NAN;
       if (token >= 0 && need_full) {
-        float xt = load1<DT>(row, token);
-        float xa[1] = {xt};
-        if (pen) { int c = pc.lookup((int)token); if (c) xa[0] = penalize(xt, c, rep, pres, freq); }
+        float xa[1] = {load1<DT>(row, token)};
+        pc.apply<1>(token, xa);
         lp = (float)((double)__fsub_rn(zval(xa[0]), zmax) - lnZ);
       }
       P.chosen_logprob[r] = lp;

@@ -3,7 +3,8 @@ the llm-pipeline inference engine (``llm_pipeline.inference`` exports
 ``Sampler``, ``SamplingConfig`` and ``verify_drafts_batched``,
 ``src/llm_pipeline/inference/__init__.py:4,17,37-38``)."""
 
-from .batch import SampleOutput, SamplingParams, pad_histories, raise_on_status, sample_rows
+from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_allowed, pad_histories,
+                    raise_on_status, sample_rows)
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
 
@@ -13,6 +14,8 @@ __all__ = [
     "SamplingParams",
     "SampleOutput",
     "sample_rows",
+    "pack_allowed",
+    "allowed_from_constraint",
     "pad_histories",
     "raise_on_status",
     "verify_drafts_batched",

@@ -58,6 +58,7 @@ class SampleArgs(ctypes.Structure):
         ("row_path", _vp),
         ("flags", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("allowed", _vp), ("allowed_stride", _i64),
     ]
 
 

@@ -111,11 +111,37 @@ def pad_histories(histories: Iterable[Sequence[int]], device) -> tuple:
     return buf.to(device), lens.to(device)
 
 
+def pack_allowed(legal: torch.Tensor) -> torch.Tensor:
+    """Pack a boolean legality mask ``[B, V]`` (True = legal) into the ABI's
+    bit rows: ``int32 [B, ceil(V / 32)]`` whose bit ``i & 31`` of word
+    ``i >> 5`` is id ``i`` (the words are read as unsigned)."""
+    if legal.dim() != 2 or legal.dtype != torch.bool:
+        raise ValueError("legal must be a bool tensor [B, V]")
+    B, V = legal.shape
+    W = (V + 31) // 32
+    bits = torch.zeros((B, W * 32), dtype=torch.int64, device=legal.device)
+    bits[:, :V] = legal.to(torch.int64)
+    weights = torch.pow(2, torch.arange(32, device=legal.device, dtype=torch.int64))
+    words = (bits.view(B, W, 32) * weights).sum(-1)
+    words = torch.where(words >= 2 ** 31, words - 2 ** 32, words)  # two's complement for int32 storage
+    return words.to(torch.int32).contiguous()
+
+
+def allowed_from_constraint(constraint, generated_ids, tokenizer, vocab_size: int, device) -> torch.Tensor:
+    """Legality bits ``int32 [1, ceil(V / 32)]`` of a reference ``LogitConstraint``
+    (``constraints.py:53-80``): the constraint's own legality mask for the
+    decoded prefix, which already allows every id when none is legal."""
+    prefix_text = tokenizer.decode(list(generated_ids))
+    legal = constraint._compute_legality_mask(prefix_text, vocab_size, tokenizer)
+    return pack_allowed(legal.reshape(1, -1).to(device))
+
+
 def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional[torch.Tensor] = None, *,
                 histories: Optional[torch.Tensor] = None, history_lengths: Optional[torch.Tensor] = None,
                 logprobs: bool = False, top_logprobs: int = 0, entropy: bool = False,
                 query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
-                path: str = "auto", generator: Optional[torch.Generator] = None) -> SampleOutput:
+                path: str = "auto", generator: Optional[torch.Generator] = None,
+                allowed: Optional[torch.Tensor] = None) -> SampleOutput:
     """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
     synchronised and ``status`` is returned as a device tensor.
@@ -123,7 +149,12 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     ``path``: ``"auto"`` runs the multi-workgroup kernels (a row they cannot
     finish exactly is sampled by the general kernel launched after them;
     ``row_path`` reports which); ``"generic"`` runs only the general
-    one-workgroup-per-row kernel."""
+    one-workgroup-per-row kernel.
+
+    ``allowed``: the rows' legality masks, as a bool ``[B, V]`` tensor (True =
+    legal) or as packed bits ``int32 [B, W]`` (``pack_allowed``); illegal ids
+    count as -inf logits, as the reference's ``LogitConstraint`` masks them
+    (``constraints.py:53-80``)."""
     if path not in ("auto", "generic"):
         raise ValueError("path must be 'auto' or 'generic'")
     D.require_device(logits, "logits")
@@ -168,6 +199,16 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
         if history_lengths is None:
             history_lengths = torch.full((B,), histories.shape[1], dtype=torch.int32, device=dev)
         history_lengths = history_lengths.to(device=dev, dtype=torch.int32).contiguous()
+    if allowed is not None:
+        if allowed.dtype == torch.bool:
+            if tuple(allowed.shape) != (B, V):
+                raise ValueError(f"allowed must be bool [{B}, {V}]; got {tuple(allowed.shape)}")
+            allowed = pack_allowed(allowed.to(dev))
+        else:
+            allowed = allowed.to(device=dev, dtype=torch.int32)
+            if allowed.dim() != 2 or allowed.shape[0] != B or allowed.shape[1] < (V + 31) // 32:
+                raise ValueError(f"allowed bits must be int32 [{B}, >= {(V + 31) // 32}]")
+            allowed = allowed.contiguous()
     p = params
     a = _lib.SampleArgs()
     a.logits = D.ptr(logits)
@@ -209,6 +250,8 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     ws = workspace_for(dev, ws_bytes) if ws_bytes else None
     a.workspace = D.ptr(ws)
     a.workspace_bytes = ws.numel() if ws is not None else 0
+    a.allowed = D.ptr(allowed)
+    a.allowed_stride = allowed.stride(0) if allowed is not None else 0
     with torch.cuda.device(dev):
         rc = _lib.load().lps_sample(ctypes.byref(a), D.stream_of(dev))
     _lib.check(rc, "lps_sample")

@@ -64,7 +64,7 @@ class Sampler:
                      generated_tokens: Optional[List[int]] = None, *, uniforms: Optional[torch.Tensor] = None,
                      params: Optional[SamplingParams] = None, histories: Optional[torch.Tensor] = None,
                      history_lengths: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
-                     strict: bool = True) -> torch.Tensor:
+                     allowed: Optional[torch.Tensor] = None, strict: bool = True) -> torch.Tensor:
         """Sample next token ids ``int64 [B]`` from ``logits [B, V]``.
 
         As in the reference, ``generated_tokens`` is one history applied to
@@ -73,8 +73,11 @@ class Sampler:
         ``SamplingParams``) and ``histories`` (padded ``int32 [B, H]``)
         replace the shared values row by row.  ``uniforms`` (``[B]`` in
         [0, 1)) drive the inverse-CDF draw; when omitted they come from
-        ``torch.rand`` on the logits' device.  ``strict`` raises the
-        reference's errors (it synchronises once to read the row status)."""
+        ``torch.rand`` on the logits' device.  ``allowed`` (bool ``[B, V]`` or
+        packed ``int32`` bits) masks illegal ids to -inf, as a reference
+        ``LogitConstraint`` applied to the logits first would.  ``strict``
+        raises the reference's errors (it synchronises once to read the row
+        status)."""
         config = self._merge_config(config_override)
         D.require_device(logits, "logits")
         if logits.dim() != 2:
@@ -92,7 +95,7 @@ class Sampler:
             history_lengths = torch.full((B,), h.numel(), dtype=torch.int32, device=dev)
         out = sample_rows(logits, params, uniforms, histories=histories, history_lengths=history_lengths,
                           logprobs=bool(config.logprobs), top_logprobs=int(config.top_logprobs),
-                          generator=generator)
+                          generator=generator, allowed=allowed)
         self.last_output = out
         if strict:
             raise_on_status(out.status)

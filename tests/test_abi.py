@@ -105,6 +105,7 @@ def _args(**kw):
     (dict(uniforms=0), 1),
     (dict(history=0x5000), 1),
     (dict(stride_outer=-1), 1),
+    (dict(allowed=0x6000, allowed_stride=3), 1),      # V=100 needs 4 words per row
     (dict(num_rows=0), 0),
 ])
 def test_sample_argument_errors(lib, kw, code):
