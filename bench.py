@@ -154,6 +154,70 @@ def cpu_baseline(w, max_rows=None, repeats=3):
                       f"torch-CPU restatement of sampling.py:51-85 with torch.multinomial"}
 
 
+def engine_step(args):
+    """One decode step of the c2 batch (B=64, V=151936 bf16, mixed parameters,
+    512-id histories) through ``SamplerState``: one ``lps_sample`` launch that
+    also appends every token to its row's history on the GPU.  Against it, the
+    reference batcher's loop (``continuous_batching.py:394-404``): one
+    ``sample_token`` per row with its kwargs, each token read back with
+    ``.item()`` -- here run with this build's sampler and the rows' histories
+    passed as the reference would pass ``generated_tokens``."""
+    import torch
+    from lps import SamplerState, Sampler
+    from tests import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = W.c2()
+    B, V = w.B, w.V
+    H = int(w.histories.shape[1])
+    st = SamplerState(B, V, H + args.steps + args.warmup + 8, dev)
+    kws = []
+    for i in range(B):
+        kw = dict(temperature=float(w.temperature[i]), top_k=int(w.top_k[i]), top_p=float(w.top_p[i]),
+                  presence_penalty=float(w.pres[i]), frequency_penalty=float(w.freq[i]))
+        kws.append(kw)
+        st.add(kw, history=w.histories[i, : int(w.hist_len[i])].tolist())
+    x = w.logits.to(dev)
+    us = torch.rand((args.steps + args.warmup, B), device=dev)
+    for s in range(args.warmup):
+        st.sample(x, us[s])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for s in range(args.steps):
+        st.sample(x, us[args.warmup + s])
+    e1.record()
+    torch.cuda.synchronize()
+    wall_state = (time.perf_counter() - t0) / args.steps * 1e3
+    gpu_state = e0.elapsed_time(e1) / args.steps
+
+    sampler = Sampler()
+    hists = [w.histories[i, : int(w.hist_len[i])].tolist() for i in range(B)]
+    nref = min(args.steps, 20)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(nref):
+        for i in range(B):
+            t = sampler.sample_token(x[i:i + 1], kws[i], generated_tokens=hists[i], strict=False)
+            hists[i].append(int(t.item()))
+    torch.cuda.synchronize()
+    wall_rows = (time.perf_counter() - t0) / nref * 1e3
+    print(json.dumps({
+        "metric": "decode step of the c2 batch: device-resident SamplerState vs the per-row loop",
+        "value": round(B / (wall_state / 1e3), 1), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_state, 6), "higher_is_better": True,
+        "state_step_gpu_ms": round(gpu_state, 6),
+        "per_row_loop_ms_per_step": round(wall_rows, 3),
+        "per_row_loop_steps_timed": nref,
+        "speedup": round(wall_rows / wall_state, 1),
+        "data": "synthetic", "config": {"workload": "c2 rows with their parameters and 512-id histories, "
+                                                    "one token appended per row per step"},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,9 +231,15 @@ def main():
                     help="add a random legality mask with this fraction of legal ids per row")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--engine-step", action="store_true",
+                    help="time a decode step of the c2 batch through SamplerState (device-resident parameters "
+                         "and histories, one launch) against the reference batcher's per-row loop")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.engine_step:
+        engine_step(args)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sampler shards rows across "

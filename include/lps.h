@@ -64,7 +64,15 @@ enum {
 
 /* lps_sample_args.flags */
 enum {
-  LPS_FLAG_GENERIC = 1     /* use the general one-workgroup-per-row kernel only */
+  LPS_FLAG_GENERIC = 1,        /* use the general one-workgroup-per-row kernel only */
+  LPS_FLAG_APPEND_HISTORY = 2  /* also append each row's sampled token (when >= 0) to its history:
+                                * history[r, history_len[r]] = token, history_len[r] += 1, when
+                                * history_len[r] < history_stride (a full row is left as is).
+                                * The history arrays are then written, so the next step's
+                                * penalties see the token without a host round trip (the
+                                * reference appends on the host, continuous_batching.py:404,
+                                * and passes the list back, sampling.py:125).  Requires history
+                                * and history_len. */
 };
 
 /* Residual used by lps_spec_verify on the first rejected position. */

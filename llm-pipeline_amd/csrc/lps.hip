@@ -283,6 +283,7 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   if (a->history && (!a->history_len || a->history_stride < 0)) return LPS_EINVAL;
   if (a->query_tokens && (a->query_inner < 0 || a->query_inner > a->rows_inner)) return LPS_EINVAL;
   if (a->allowed && a->allowed_stride < (int64_t)((a->vocab + 31) / 32)) return LPS_EINVAL;
+  if ((a->flags & LPS_FLAG_APPEND_HISTORY) && (!a->history || !a->history_len)) return LPS_EINVAL;
   KParams P = neutral_params();
   P.logits = a->logits;
   P.V = a->vocab;
@@ -321,6 +322,7 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   P.row_path = a->row_path;
   P.allowed = a->allowed;
   P.allowed_stride = a->allowed_stride;
+  P.append_history = (a->flags & LPS_FLAG_APPEND_HISTORY) ? 1 : 0;
   if (a->workspace && a->workspace_bytes < lps_workspace_bytes(a->num_rows, a->vocab, a->flags)) return LPS_EWORKSPACE;
   const bool vec = vec_ok(a->logits, a->dtype, a->vocab, a->rows_inner, a->stride_outer, a->stride_inner);
   hipError_t e = run_sample(P, a->dtype, vec, a->workspace, a->workspace_bytes, a->flags,

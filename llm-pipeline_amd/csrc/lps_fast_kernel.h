@@ -1139,6 +1139,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
   }
   if (tid == 0) {
     P.tokens[r] = status ? -1 : token;
+    append_token(P, r, status ? -1 : token);
     F.status[r] = status;
     if (P.row_status) P.row_status[r] = status;
     if (P.query_prob) P.query_prob[r] = qprob;

@@ -67,7 +67,18 @@ struct KParams {
   int32_t* row_path;           // optional: 0 fast kernel, 1 general kernel
   const uint32_t* allowed;     // optional legality bits, row r at allowed + r * allowed_stride
   int64_t allowed_stride;      // 32-bit words
+  int append_history;          // write each sampled token into the row's history
 };
+// With append_history: row r's sampled token joins its history for the next
+// step (when the row has room, history_len[r] < history_stride).  One thread.
+__device__ __forceinline__ void append_token(const KParams& P, int r, int64_t token) {
+  if (!P.append_history || token < 0 || !P.history || !P.history_len) return;
+  int32_t* len = const_cast<int32_t*>(P.history_len) + r;
+  const int l = *len;
+  if (l < 0 || (int64_t)l >= P.history_stride) return;
+  const_cast<int32_t*>(P.history)[(int64_t)r * P.history_stride + l] = (int32_t)token;
+  *len = l + 1;
+}
 // Row r's legality bits (nullptr: every id legal).
 __device__ __forceinline__ const uint8_t* row_allowed(const KParams& P, int r) {
   return P.allowed ? reinterpret_cast<const uint8_t*>(P.allowed + (int64_t)r * P.allowed_stride) : nullptr;
@@ -711,6 +722,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   if (tid == 0) {
     const bool failed = (status & LPS_ROW_HISTORY_OVERFLOW) || (!greedy && status != 0);
     P.tokens[r] = failed ? -1 : token;
+    append_token(P, r, failed ? -1 : token);
     if (P.row_status) P.row_status[r] = status;
     if (P.query_prob) P.query_prob[r] = qprob;
     if (P.kept_cut) P.kept_cut[r] = key_lo <= kNegInfKey ? -INFINITY : key2f(key_lo);  // key 0: nothing cut

@@ -7,6 +7,7 @@ from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_
                     raise_on_status, sample_rows)
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
+from .state import SamplerState
 
 __all__ = [
     "Sampler",
@@ -16,6 +17,7 @@ __all__ = [
     "sample_rows",
     "pack_allowed",
     "allowed_from_constraint",
+    "SamplerState",
     "pad_histories",
     "raise_on_status",
     "verify_drafts_batched",

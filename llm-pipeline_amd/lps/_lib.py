@@ -31,6 +31,7 @@ LPS_MAX_TOP_LOGPROBS = 64
 LPS_MAX_HISTORY_DISTINCT = 1536
 
 LPS_FLAG_GENERIC = 1
+LPS_FLAG_APPEND_HISTORY = 2
 
 LPS_RESIDUAL_TARGET = 0
 LPS_RESIDUAL_LEVIATHAN = 1

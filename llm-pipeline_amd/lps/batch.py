@@ -141,7 +141,7 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
                 logprobs: bool = False, top_logprobs: int = 0, entropy: bool = False,
                 query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
                 path: str = "auto", generator: Optional[torch.Generator] = None,
-                allowed: Optional[torch.Tensor] = None) -> SampleOutput:
+                allowed: Optional[torch.Tensor] = None, append_history: bool = False) -> SampleOutput:
     """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
     synchronised and ``status`` is returned as a device tensor.
@@ -154,7 +154,14 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     ``allowed``: the rows' legality masks, as a bool ``[B, V]`` tensor (True =
     legal) or as packed bits ``int32 [B, W]`` (``pack_allowed``); illegal ids
     count as -inf logits, as the reference's ``LogitConstraint`` masks them
-    (``constraints.py:53-80``)."""
+    (``constraints.py:53-80``).
+
+    ``append_history``: the kernel also appends each row's sampled token to
+    its history row in place (``histories[r, history_lengths[r]]``, then
+    ``history_lengths[r] += 1``, when the row has room), so the next step's
+    penalties see it without a host round trip.  ``histories`` and
+    ``history_lengths`` must then be int32 device tensors used as they are
+    (row-contiguous histories, contiguous lengths)."""
     if path not in ("auto", "generic"):
         raise ValueError("path must be 'auto' or 'generic'")
     D.require_device(logits, "logits")
@@ -191,11 +198,20 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     if query_tokens is not None:
         query_tokens = query_tokens.to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
         out.query_prob = torch.empty((B,), dtype=torch.float32, device=dev)
+    if append_history:
+        if histories is None or history_lengths is None:
+            raise ValueError("append_history needs histories and history_lengths")
+        if (histories.dtype != torch.int32 or histories.device != dev or histories.dim() != 2
+                or histories.stride(1) != 1 or history_lengths.dtype != torch.int32
+                or history_lengths.device != dev or not history_lengths.is_contiguous()):
+            raise ValueError("append_history writes the histories in place: they must be int32 tensors on "
+                             "the logits' device (row-contiguous [B, H], contiguous lengths [B])")
     if histories is not None:
         histories = histories.to(device=dev, dtype=torch.int32)
         if histories.dim() != 2 or histories.shape[0] != B:
             raise ValueError("histories must be int32 [B, H]")
-        histories = histories.contiguous()
+        if histories.stride(1) != 1:
+            histories = histories.contiguous()
         if history_lengths is None:
             history_lengths = torch.full((B,), histories.shape[1], dtype=torch.int32, device=dev)
         history_lengths = history_lengths.to(device=dev, dtype=torch.int32).contiguous()
@@ -245,7 +261,7 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_ties = D.ptr(out.kept_ties)
     a.kept_count = D.ptr(out.kept_count)
     a.row_path = D.ptr(out.row_path)
-    a.flags = 0 if path == "auto" else _lib.LPS_FLAG_GENERIC
+    a.flags = (0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
     ws_bytes = _lib.load().lps_workspace_bytes(B, V, a.flags)
     ws = workspace_for(dev, ws_bytes) if ws_bytes else None
     a.workspace = D.ptr(ws)
