@@ -218,6 +218,139 @@ def engine_step(args):
     }), flush=True)
 
 
+SOFTMAX_WORKLOADS = {
+    # name: (rows, cols, dtype, causal, seq_len, description)
+    "logits": (64, 151936, "bfloat16", False, 1,
+               "LM-head softmax producer: the c2 logits, 64 x 151936 bf16, probabilities out in bf16"),
+    "attn": (32 * 2048, 2048, "bfloat16", True, 2048,
+             "causal attention probabilities: 32 heads x 2048 queries x 2048 keys bf16, row_offset 0"),
+}
+
+
+def softmax_bench(args):
+    """Row softmax (``lps_softmax``, the drop-in for the reference's
+    ``fused_softmax_triton``) over one workload: every launch reads one input
+    buffer and writes one output buffer, rotated over >= 2 x 256 MB, replayed
+    from a HIP graph.  Algorithmic bytes: the visible (unmasked) input read
+    once plus the whole output written once."""
+    import torch
+    from lps import _lib
+    from lps import _device as D
+    from lps import softmax as SM
+
+    rows, cols, dts, causal, seq_len, desc = SOFTMAX_WORKLOADS[args.softmax]
+    dtype = getattr(torch, dts)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    es = torch.tensor([], dtype=dtype).element_size()
+    nb_in = rows * cols * es
+    nbuf = max(2, math.ceil(2 * MALL_BYTES / nb_in))
+    g = torch.Generator().manual_seed(5)
+    x0 = (torch.randn((rows, cols), generator=g) * 3.0).to(dtype).to(dev)
+    xs = [x0] + [x0.roll(i, dims=1) for i in range(1, nbuf)]
+    outs = [torch.empty_like(x0) for _ in range(nbuf)]
+    wsb = lib.lps_softmax_workspace_bytes(rows, cols, D.dtype_code(x0))
+    ws = torch.zeros((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    arglist = []
+    for x, o in zip(xs, outs):
+        a = _lib.SoftmaxArgs()
+        a.x, a.out, a.dtype, a.rows, a.cols = x.data_ptr(), o.data_ptr(), D.dtype_code(x), rows, cols
+        a.x_stride = a.out_stride = cols
+        a.causal, a.seq_len, a.row_offset = int(causal), seq_len, 0
+        a.workspace, a.workspace_bytes = (ws.data_ptr(), ws.numel()) if wsb else (None, 0)
+        arglist.append(a)
+
+    def launch(i):
+        rc = lib.lps_softmax(ctypes.byref(arglist[i % nbuf]), torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lps_softmax failed: {rc}")
+
+    # self-check of the timed configuration: the first rows against torch in fp64
+    launch(0)
+    torch.cuda.synchronize()
+    chk = x0[:4].double().cpu()
+    if causal:
+        chk = chk.masked_fill(torch.arange(cols).unsqueeze(0) > torch.arange(4).unsqueeze(1), float("-inf"))
+    ref = torch.softmax(chk, dim=-1)
+    err = float(((outs[0][:4].double().cpu() - ref).abs() - 2 ** -8 * ref.abs()).max())
+    assert err <= 1e-6, f"softmax self-check failed ({err})"
+
+    per_graph = nbuf * max(1, 64 // nbuf)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            launch(i)
+    for _ in range(max(1, math.ceil(args.warmup / per_graph))):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, math.ceil(args.steps / per_graph))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    steps = reps * per_graph
+    ms_step = e0.elapsed_time(e1) / steps
+    assert all(int(t.count_nonzero()) == 0 for t in [ws]), "workspace not left zeroed"
+
+    visible = sum(min(cols, (r % seq_len) + 1) for r in range(rows)) if causal else rows * cols
+    abytes = visible * es + rows * cols * es
+    gbs = abytes / (ms_step / 1e3) / 1e9
+    plan = "softmax_wave_kernel" if cols <= (2048 if es == 4 else 4096) else (
+        "softmax_chunk_kernel (rows split over workgroups)" if wsb else "softmax_chunk_kernel")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        threads = max(1, min(share, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        n = rows if not causal else 2048
+        xc = x0[:n].cpu()
+
+        def ref_cpu():
+            xm = xc
+            if causal:
+                xm = xc.masked_fill(torch.arange(cols).unsqueeze(0) > torch.arange(n).unsqueeze(1), float("-inf"))
+            return torch.softmax(xm.float(), dim=-1).to(dtype)
+
+        ref_cpu()   # thread pool and allocator warm
+        ts = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            ref_cpu()
+            ts.append(time.perf_counter() - t0)
+        t = statistics.median(ts)
+        cpu_vis = visible if not causal else sum(min(cols, (r % seq_len) + 1) for r in range(n))
+        cpu_bytes = cpu_vis * es + n * cols * es
+        cpu = {"value": round(cpu_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{n} rows of the workload, torch-CPU restatement of triton_softmax.py:105-113 "
+                         f"(masked_fill, softmax in fp32, cast back), median of 10 after one warm-up call"}
+
+    print(json.dumps({
+        "metric": f"row softmax achieved HBM GB/s ({args.softmax})",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "rows_per_s": round(rows / (ms_step / 1e3), 1),
+        "config": {"workload": desc, "rows": rows, "cols": cols, "input_dtype": dts, "causal": causal,
+                   "buffers_rotated": nbuf, "hip_graph": True, "algorithmic_bytes_per_call": abytes,
+                   "kernel": plan},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": hbm_traffic("softmax", args.softmax)},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,7 +367,15 @@ def main():
     ap.add_argument("--engine-step", action="store_true",
                     help="time a decode step of the c2 batch through SamplerState (device-resident parameters "
                          "and histories, one launch) against the reference batcher's per-row loop")
+    ap.add_argument("--softmax", choices=sorted(SOFTMAX_WORKLOADS), default=None,
+                    help="time the row softmax (lps_softmax) on a workload instead of the sampler")
     args = ap.parse_args()
+    if args.softmax:
+        if args.gpus != 1:
+            print("bench.py runs on one GPU only", file=sys.stderr)
+            sys.exit(2)
+        softmax_bench(args)
+        return
     if args.copy_calibration:
         copy_calibration()
         return

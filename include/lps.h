@@ -227,6 +227,41 @@ int lps_verify_drafts(const void* target_probs, int32_t dtype, int64_t K, int64_
                       int64_t stride_v, const float* draft_probs, const int64_t* draft_tokens,
                       const float* rand_uniform, int8_t* accept, void* stream);
 
+/* Row softmax with an optional causal mask, the softmax producer of the
+ * reference's fused_softmax_triton (quantization/kernels/triton_softmax.py:65-102):
+ *   out[r, j] = softmax(masked)[j], masked[j] = -inf when causal and
+ *   j > (r % seq_len) + row_offset, else x[r, j];
+ * computed in fp32, written in `dtype` (round to nearest even).  Rows are
+ * contiguous; row r of x / out starts at element r * x_stride / r * out_stride.
+ * out may be x itself (in place).  row_lse, when given, gets log(sum(exp))
+ * of each row's masked values (natural log; -inf for an all -inf row).
+ *
+ * workspace: caller-owned scratch of lps_softmax_workspace_bytes() bytes,
+ * zero-filled before its first use and then reused as is (every launch leaves
+ * it zeroed).  It lets long rows (more than 16384 16-bit / 8192 fp32 columns)
+ * be split over several workgroups; NULL (or an in-place call) keeps one
+ * workgroup per row.  Calls that overlap in time must not share a workspace. */
+typedef struct lps_softmax_args {
+  const void* x;
+  void* out;
+  int32_t dtype;                  /* lps_dtype, x and out */
+  int32_t rows;
+  int32_t cols;
+  int64_t x_stride;               /* elements */
+  int64_t out_stride;             /* elements */
+  int32_t causal;                 /* 0 / 1 */
+  int32_t seq_len;                /* causal: rows per sequence (>= 1) */
+  int32_t row_offset;             /* causal: first row's position */
+  float* row_lse;                 /* float32 [rows] or NULL */
+  void* workspace;                /* or NULL */
+  size_t workspace_bytes;
+} lps_softmax_args;
+
+/* Bytes of workspace lps_softmax uses for rows x cols of dtype (0: none). */
+size_t lps_softmax_workspace_bytes(int rows, int cols, int dtype);
+
+int lps_softmax(const lps_softmax_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 
 #include "lps_fast_kernel.h"
 #include "lps_generic.h"
+#include "lps_softmax.h"
 #include "lps_spec.h"
 
 using namespace lps;
@@ -243,6 +244,57 @@ SpecWs spec_layout(void* base, int B, int k) {
   return w;
 }
 
+template <int DT, int VEC>
+hipError_t launch_softmax(const SoftmaxParams& S, hipStream_t s) {
+  if (S.cols >= 16384) hipLaunchKernelGGL((softmax_kernel<DT, VEC, 1024>), dim3(S.rows), dim3(1024), 0, s, S);
+  else hipLaunchKernelGGL((softmax_kernel<DT, VEC, 256>), dim3(S.rows), dim3(256), 0, s, S);
+  return hipGetLastError();
+}
+
+// Softmax kernel choice for rows whose starts are 16-byte aligned: one wave per
+// row (kind 0), G register-resident chunks per row (kind 1), or the three-pass
+// kernel (kind 2).  nv = 16-byte vectors per lane.
+struct SmPlan {
+  int kind, nv, G;
+};
+SmPlan softmax_plan(int dtype, int rows, int cols) {
+  const int vpl = dtype == LPS_DTYPE_F32 ? 4 : 8;
+  const int64_t vecs = ((int64_t)cols + vpl - 1) / vpl;  // 16-byte vectors per row
+  for (int nv = 1; nv <= 8; nv *= 2)
+    if (vecs <= 64 * nv) return {0, nv, 1};
+  if (vecs <= SM_NT * 4) return {1, 4, 1};
+  if (vecs <= SM_NT * 8) return {1, 8, 1};
+  auto chunks = [&](int nv) { return (int)((vecs + (int64_t)SM_NT * nv - 1) / ((int64_t)SM_NT * nv)); };
+  if (chunks(8) > SM_MAXG) return {2, 0, 1};
+  // 8 vectors per lane (16 KB of 16-bit / 32 KB of fp32 columns per chunk):
+  // measured fastest on 64 x 151936 bf16 (4 to 19 vectors swept); smaller
+  // chunks only for short grids, down to 4 (more chunks per row cost more in
+  // the record exchange than they add in parallelism)
+  const int nv = (int64_t)rows * chunks(8) < 256 && chunks(4) <= SM_MAXG ? 4 : 8;
+  return {1, nv, chunks(nv)};
+}
+size_t softmax_records_bytes(int rows, int G) {
+  return G > 1 ? (size_t)rows * G * sizeof(SmRecord) + ((size_t)rows * 4 + 255) / 256 * 256 : 0;
+}
+
+template <int DT>
+hipError_t launch_softmax_reg(const SoftmaxParams& S, const SmPlan& p, hipStream_t s) {
+  if (p.kind == 0) {
+    const dim3 grid((S.rows + SM_NT / 64 - 1) / (SM_NT / 64));
+    switch (p.nv) {
+      case 1: hipLaunchKernelGGL((softmax_wave_kernel<DT, 1>), grid, dim3(SM_NT), 0, s, S); break;
+      case 2: hipLaunchKernelGGL((softmax_wave_kernel<DT, 2>), grid, dim3(SM_NT), 0, s, S); break;
+      case 4: hipLaunchKernelGGL((softmax_wave_kernel<DT, 4>), grid, dim3(SM_NT), 0, s, S); break;
+      default: hipLaunchKernelGGL((softmax_wave_kernel<DT, 8>), grid, dim3(SM_NT), 0, s, S); break;
+    }
+  } else {
+    const dim3 grid((unsigned)(((int64_t)S.rows + 7) / 8 * S.G * 8));
+    if (p.nv == 4) hipLaunchKernelGGL((softmax_chunk_kernel<DT, 4>), grid, dim3(SM_NT), 0, s, S);
+    else hipLaunchKernelGGL((softmax_chunk_kernel<DT, 8>), grid, dim3(SM_NT), 0, s, S);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -422,6 +474,81 @@ int lps_verify_drafts(const void* target_probs, int32_t dtype, int64_t K, int64_
       break;
   }
   return hipGetLastError() == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
+
+size_t lps_softmax_workspace_bytes(int rows, int cols, int dtype) {
+  if (rows <= 0 || cols < 1 || !dtype_ok(dtype)) return 0;
+  const SmPlan p = softmax_plan(dtype, rows, cols);
+  return p.kind == 1 ? softmax_records_bytes(rows, p.G) : 0;
+}
+
+int lps_softmax(const lps_softmax_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  if (!dtype_ok(a->dtype)) return LPS_EUNSUPPORTED_DTYPE;
+  if (a->rows < 0 || a->cols < 1) return LPS_EINVAL;
+  if (a->rows == 0) return LPS_OK;
+  if (!a->x || !a->out) return LPS_EINVAL;
+  if (a->rows > 1 && (a->x_stride < a->cols || a->out_stride < a->cols)) return LPS_EINVAL;
+  if (a->causal && a->seq_len < 1) return LPS_EINVAL;
+  SoftmaxParams S{};
+  S.x = a->x;
+  S.out = a->out;
+  S.x_stride = a->x_stride;
+  S.out_stride = a->out_stride;
+  S.rows = a->rows;
+  S.cols = a->cols;
+  S.causal = a->causal ? 1 : 0;
+  S.seq_len = a->causal ? a->seq_len : 1;
+  S.row_offset = a->row_offset;
+  S.row_lse = a->row_lse;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  // register-resident kernels: every row of x and out starts 16-byte aligned
+  const int vpl = a->dtype == LPS_DTYPE_F32 ? 4 : 8;
+  auto aligned = [&](const void* p, int64_t stride) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (a->rows <= 1 || stride % vpl == 0);
+  };
+  if (aligned(a->x, a->x_stride) && aligned(a->out, a->out_stride)) {
+    SmPlan p = softmax_plan(a->dtype, a->rows, a->cols);
+    if (p.kind == 1 && p.G > 1) {
+      // split rows need the workspace, and distinct input and output (a
+      // workgroup that falls back re-reads its whole row)
+      const int es = a->dtype == LPS_DTYPE_F32 ? 4 : 2;
+      const char* x0 = static_cast<const char*>(a->x);
+      const char* o0 = static_cast<const char*>(a->out);
+      const int64_t xs = a->rows > 1 ? a->x_stride : a->cols, os = a->rows > 1 ? a->out_stride : a->cols;
+      const char* x1 = x0 + ((int64_t)(a->rows - 1) * xs + a->cols) * es;
+      const char* o1 = o0 + ((int64_t)(a->rows - 1) * os + a->cols) * es;
+      const bool overlap = x0 < o1 && o0 < x1;
+      const size_t need = softmax_records_bytes(a->rows, p.G);
+      if (overlap || !a->workspace || a->workspace_bytes < need) {
+        p.kind = 2;
+      } else {
+        S.G = p.G;
+        S.records = a->workspace;
+        S.done = reinterpret_cast<uint32_t*>(static_cast<char*>(a->workspace) + (size_t)a->rows * p.G * sizeof(SmRecord));
+      }
+    } else {
+      S.G = 1;
+    }
+    if (p.kind != 2) {
+      switch (a->dtype) {
+        case LPS_DTYPE_F32: e = launch_softmax_reg<LPS_DTYPE_F32>(S, p, s); break;
+        case LPS_DTYPE_BF16: e = launch_softmax_reg<LPS_DTYPE_BF16>(S, p, s); break;
+        default: e = launch_softmax_reg<LPS_DTYPE_F16>(S, p, s); break;
+      }
+      return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+    }
+  }
+  // three passes; 16-byte vectors when both rows start 16-byte aligned and cols fill whole vectors
+  const bool vec = vec_ok(a->x, a->dtype, a->cols, 1, a->rows > 1 ? a->x_stride : 0, 0) &&
+                   vec_ok(a->out, a->dtype, a->cols, 1, a->rows > 1 ? a->out_stride : 0, 0);
+  switch (a->dtype) {
+    case LPS_DTYPE_F32: e = vec ? launch_softmax<LPS_DTYPE_F32, 4>(S, s) : launch_softmax<LPS_DTYPE_F32, 1>(S, s); break;
+    case LPS_DTYPE_BF16: e = vec ? launch_softmax<LPS_DTYPE_BF16, 8>(S, s) : launch_softmax<LPS_DTYPE_BF16, 1>(S, s); break;
+    default: e = vec ? launch_softmax<LPS_DTYPE_F16, 8>(S, s) : launch_softmax<LPS_DTYPE_F16, 1>(S, s); break;
+  }
+  return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
 }
 
 }  // extern "C"

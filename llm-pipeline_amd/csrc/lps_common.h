@@ -24,12 +24,20 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
 
-template <int DT>
+// NTL: nontemporal (streamed once, not kept in the caches); false for data
+// that is read again soon (the row softmax's second and third passes).
+template <typename T, bool NTL>
+__device__ __forceinline__ T ldg(const T* p) {
+  if constexpr (NTL) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <int DT, bool NTL = true>
 __device__ __forceinline__ float load1(const void* row, int64_t i) {
   if constexpr (DT == LPS_DTYPE_F32) {
-    return __builtin_nontemporal_load(reinterpret_cast<const float*>(row) + i);
+    return ldg<float, NTL>(reinterpret_cast<const float*>(row) + i);
   } else {
-    uint32_t h = __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(row) + i);
+    uint32_t h = ldg<unsigned short, NTL>(reinterpret_cast<const unsigned short*>(row) + i);
     return DT == LPS_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
   }
 }
@@ -38,12 +46,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Loads VEC consecutive elements starting at element i0 (i0 % VEC == 0) with
 // one 16-byte load when VEC covers 16 bytes, else element loads.
-template <int DT, int VEC>
+template <int DT, int VEC, bool NTL = true>
 __device__ __forceinline__ void loadv(const void* row, int64_t i0, float (&x)[VEC]) {
   if constexpr ((DT == LPS_DTYPE_F32 && VEC == 4) || (DT != LPS_DTYPE_F32 && VEC == 8)) {
     const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(row) +
                                                      i0 * (DT == LPS_DTYPE_F32 ? 4 : 2));
-    u32x4 v = __builtin_nontemporal_load(p);
+    u32x4 v = ldg<u32x4, NTL>(p);
     if constexpr (DT == LPS_DTYPE_F32) {
       x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y);
       x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w);
@@ -62,7 +70,7 @@ __device__ __forceinline__ void loadv(const void* row, int64_t i0, float (&x)[VE
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < VEC; j++) x[j] = load1<DT>(row, i0 + j);
+    for (int j = 0; j < VEC; j++) x[j] = load1<DT, NTL>(row, i0 + j);
   }
 }
 

@@ -152,10 +152,6 @@ struct FSharedT : XShared {
 // ---------------------------------------------------------------------------
 // L2-level communication primitives.
 // ---------------------------------------------------------------------------
-// XCD id of the executing wave: hardware register HW_REG_XCC_ID (20), bits 0-3.
-__device__ __forceinline__ uint32_t xcc_id() {
-  return (uint32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)) & 0xFu;
-}
 // Counter reads: a compare-and-swap whose compare value a counter never holds,
 // so it always fails and returns the current value; it executes at the L2
 // (never in a possibly stale L1) and cannot be turned into a plain load.

@@ -29,6 +29,11 @@ __device__ __forceinline__ uint64_t rdlane_u64(uint64_t v, int l) {
   return ((uint64_t)rdlane_u32((uint32_t)(v >> 32), l) << 32) | rdlane_u32((uint32_t)v, l);
 }
 
+// XCD id of the executing wave: hardware register HW_REG_XCC_ID (20), bits 0-3.
+__device__ __forceinline__ uint32_t xcc_id() {
+  return (uint32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)) & 0xFu;
+}
+
 struct OpAdd {
   template <typename T> __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
 };

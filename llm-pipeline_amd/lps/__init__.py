@@ -7,6 +7,7 @@ from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_
                     raise_on_status, sample_rows)
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
+from .softmax import fused_softmax, fused_softmax_triton
 from .state import SamplerState
 
 __all__ = [
@@ -18,6 +19,8 @@ __all__ = [
     "pack_allowed",
     "allowed_from_constraint",
     "SamplerState",
+    "fused_softmax",
+    "fused_softmax_triton",
     "pad_histories",
     "raise_on_status",
     "verify_drafts_batched",

@@ -63,6 +63,16 @@ class SampleArgs(ctypes.Structure):
     ]
 
 
+class SoftmaxArgs(ctypes.Structure):
+    """Mirror of ``lps_softmax_args``."""
+
+    _fields_ = [
+        ("x", _vp), ("out", _vp), ("dtype", _i32), ("rows", _i32), ("cols", _i32),
+        ("x_stride", _i64), ("out_stride", _i64), ("causal", _i32), ("seq_len", _i32), ("row_offset", _i32),
+        ("row_lse", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class SpecArgs(ctypes.Structure):
     """Mirror of ``lps_spec_args``."""
 
@@ -86,6 +96,8 @@ SIGNATURES = {
     "lps_sample": (_i32, [ctypes.POINTER(SampleArgs), _vp]),
     "lps_spec_verify": (_i32, [ctypes.POINTER(SpecArgs), _vp]),
     "lps_verify_drafts": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "lps_softmax": (_i32, [ctypes.c_void_p, _vp]),
+    "lps_softmax_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
 }
 
 _lib = None

@@ -67,7 +67,8 @@ def _c_layout(struct, fields):
     return vals[0], vals[1:]
 
 
-@pytest.mark.parametrize("cname,pyname", [("lps_sample_args", "SampleArgs"), ("lps_spec_args", "SpecArgs")])
+@pytest.mark.parametrize("cname,pyname", [("lps_sample_args", "SampleArgs"), ("lps_spec_args", "SpecArgs"),
+                                         ("lps_softmax_args", "SoftmaxArgs")])
 def test_struct_layout_matches_c(cname, pyname):
     from lps import _lib
     py = getattr(_lib, pyname)
