@@ -351,6 +351,73 @@ def softmax_bench(args):
     }), flush=True)
 
 
+def spec_driver_bench(args):
+    """Batched two-model speculative decoding (``speculative_decode_batched``,
+    the batched form of ``speculative.py:68-178``) at c2's shape: 64 requests,
+    V = 151936 bf16, k = 4, T = 1.  The forwards cost nothing (each request's
+    target logits are a fixed random row, the draft's the same row plus noise,
+    at every position), so the time is the driver's own: k draft-sampling
+    launches, the gathers, one ``lps_spec_verify`` launch and one read-back per
+    round.  Reported: generated tokens/s and ms per round; the CPU baseline is
+    the oracle's restatement of the reference loop, one request, two rounds."""
+    import torch
+    from lps import speculative_decode_batched
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, V, k, T = 64, 151936, 4, 1.0
+    g = torch.Generator(device=dev).manual_seed(3)
+    tgt = (torch.randn((B, V), generator=g, device=dev) * 3.0).to(torch.bfloat16)
+    drf = (tgt.float() + torch.randn((B, V), generator=g, device=dev) * 0.7).to(torch.bfloat16)
+
+    class Fixed:
+        def __init__(self, tbl):
+            self.tbl = tbl
+
+        def __call__(self, x):
+            b, L = x.shape
+            return self.tbl[:b].unsqueeze(1).expand(b, L, V)
+
+    prompts = torch.randint(0, V, (B, 8), device=dev)
+    ug = torch.Generator(device=dev).manual_seed(5)
+    speculative_decode_batched(Fixed(tgt), Fixed(drf), prompts, 10, k, T, generator=ug)   # warm-up
+    torch.cuda.synchronize()
+    n_new = max(20, args.steps // 10)
+    t0 = time.perf_counter()
+    outs, stats = speculative_decode_batched(Fixed(tgt), Fixed(drf), prompts, n_new, k, T, generator=ug)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tokens = sum(int(o.numel()) for o in outs)
+    rounds = max(s.rounds for s in stats)
+    acc = sum(s.accepted for s in stats) / max(1, sum(s.rounds for s in stats))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import reference_semantics as O
+        tc, dc = tgt[:1].float().cpu(), drf[:1].float().cpu()
+        fc = lambda tbl: (lambda x: tbl.unsqueeze(1).expand(x.shape[0], x.shape[1], V))
+        gu = torch.Generator().manual_seed(1)
+        t1 = time.perf_counter()
+        out, r_cpu, _, _ = O.spec_decode_ref(fc(tc), fc(dc), prompts[:1].cpu(), 2 * (k + 1), k, T, None,
+                                             lambda r: (torch.rand(k, generator=gu), torch.rand(k, generator=gu),
+                                                        torch.rand(k + 1, generator=gu)))
+        tcpu = time.perf_counter() - t1
+        cpu = {"value": round(out.numel() / tcpu, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"one request, {r_cpu} rounds of the oracle's restatement of "
+                                          f"speculative.py:68-178 (fp32 CPU, same synthetic logits)"}
+    print(json.dumps({
+        "metric": "batched speculative decoding, generated tokens/s (driver and sampling only)",
+        "value": round(tokens / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": rounds, "warmup": 1,
+        "ms_per_step": round(dt / rounds * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "accepted_per_round": round(acc, 3),
+        "config": {"workload": "64 requests, V=151936 bf16, k=4, T=1; forwards are fixed random rows (target) "
+                               "and the same rows plus N(0, 0.7^2) noise (draft)",
+                   "rounds": rounds, "generated_tokens": tokens},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,7 +436,12 @@ def main():
                          "and histories, one launch) against the reference batcher's per-row loop")
     ap.add_argument("--softmax", choices=sorted(SOFTMAX_WORKLOADS), default=None,
                     help="time the row softmax (lps_softmax) on a workload instead of the sampler")
+    ap.add_argument("--spec-driver", action="store_true",
+                    help="time the batched speculative-decoding driver (zero-cost synthetic forwards)")
     args = ap.parse_args()
+    if args.spec_driver:
+        spec_driver_bench(args)
+        return
     if args.softmax:
         if args.gpus != 1:
             print("bench.py runs on one GPU only", file=sys.stderr)

@@ -195,6 +195,9 @@ typedef struct lps_spec_args {
   float* p_target;                /* float32 [B, k] or NULL */
   float* q_draft;                 /* float32 [B, k] or NULL */
   int32_t* row_status;            /* int32 [B*(2k+1)] or NULL */
+  /* caller-owned scratch of lps_spec_workspace_bytes() bytes, zero-filled
+   * before its first use and then reused as is (every launch leaves it ready
+   * for the next); calls that overlap in time must not share it */
   void* workspace;
   size_t workspace_bytes;
 } lps_spec_args;

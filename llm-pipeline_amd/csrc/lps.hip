@@ -220,6 +220,8 @@ KParams neutral_params() {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct SpecWs {
+  void* fast;         // the fast path's workspace (first, so its counters never move)
+  size_t fast_bytes;
   int64_t* draws_t;   // [B*(k+1)]
   int64_t* draws_d;   // [B*k]
   float* p_t;         // [B*(k+1)]
@@ -229,11 +231,13 @@ struct SpecWs {
   size_t bytes;
 };
 
-SpecWs spec_layout(void* base, int B, int k) {
+SpecWs spec_layout(void* base, int B, int k, int V) {
   SpecWs w{};
   const size_t Rt = (size_t)B * (k + 1), Rd = (size_t)B * k;
-  size_t off = 0;
   char* p = reinterpret_cast<char*>(base);
+  w.fast = base;
+  w.fast_bytes = fast_layout(nullptr, (int)Rt, V).bytes;
+  size_t off = align256(w.fast_bytes);
   w.draws_t = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rt * 8);
   w.draws_d = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rd * 8);
   w.p_t = reinterpret_cast<float*>(p + off); off = align256(off + Rt * 4);
@@ -318,9 +322,8 @@ size_t lps_workspace_bytes(int num_rows, int vocab, int flags) {
 }
 
 size_t lps_spec_workspace_bytes(int batch, int k, int vocab) {
-  (void)vocab;
-  if (batch <= 0 || k <= 0) return 0;
-  return spec_layout(nullptr, batch, k).bytes;
+  if (batch <= 0 || k <= 0 || vocab < 1 || vocab > kMaxVocab) return 0;
+  return spec_layout(nullptr, batch, k, vocab).bytes;
 }
 
 int lps_sample(const lps_sample_args* a, void* stream) {
@@ -392,9 +395,9 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
     return LPS_EINVAL;
   if (a->residual != LPS_RESIDUAL_TARGET && a->residual != LPS_RESIDUAL_LEVIATHAN) return LPS_EINVAL;
   const int B = a->batch, k = a->k, V = a->vocab;
-  const SpecWs need = spec_layout(nullptr, B, k);
+  const SpecWs need = spec_layout(nullptr, B, k, V);
   if (!a->workspace || a->workspace_bytes < need.bytes) return LPS_EWORKSPACE;
-  const SpecWs w = spec_layout(a->workspace, B, k);
+  const SpecWs w = spec_layout(a->workspace, B, k, V);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool lev = a->residual == LPS_RESIDUAL_LEVIATHAN && a->temperature > 0.0f;
 
@@ -415,8 +418,13 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   P.tokens = w.draws_t;
   P.row_status = a->row_status;
   P.plans = w.plans;
+  // The Leviathan residual reads the general kernel's per-row plans; otherwise
+  // both row sets take the fast kernels (rows they cannot finish exactly go
+  // to the general kernel after them), with the same results.
   bool vec = vec_ok(a->target_logits, a->dtype, V, k + 1, a->target_stride_b, a->target_stride_k);
-  if (dispatch_gen(a->dtype, vec, P, s) != hipSuccess) return LPS_ELAUNCH;
+  if ((lev ? dispatch_gen(a->dtype, vec, P, s) : run_sample(P, a->dtype, vec, w.fast, w.fast_bytes, 0, s)) !=
+      hipSuccess)
+    return LPS_ELAUNCH;
 
   // draft rows: probability of each draft token only
   KParams D = P;
@@ -433,7 +441,9 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   D.skip_draw = 1;
   D.plans = w.plans + (size_t)B * (k + 1);
   vec = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
-  if (dispatch_gen(a->dtype, vec, D, s) != hipSuccess) return LPS_ELAUNCH;
+  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, 0, s)) !=
+      hipSuccess)
+    return LPS_ELAUNCH;
 
   hipLaunchKernelGGL(spec_epilogue_kernel, dim3((B + 255) / 256), dim3(256), 0, s, B, k, a->temperature, w.p_t,
                      w.q_d, w.draws_t, a->draft_tokens, a->u_accept, a->n_accepted, a->tokens, a->accept,

@@ -8,6 +8,8 @@ from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
 from .softmax import fused_softmax, fused_softmax_triton
+from .spec_driver import (mtp_speculative_decode, mtp_speculative_decode_batched, speculative_decode,
+                          speculative_decode_batched)
 from .state import SamplerState
 
 __all__ = [
@@ -25,6 +27,10 @@ __all__ = [
     "raise_on_status",
     "verify_drafts_batched",
     "spec_verify",
+    "speculative_decode",
+    "speculative_decode_batched",
+    "mtp_speculative_decode",
+    "mtp_speculative_decode_batched",
     "SpecVerifyOutput",
     "SpecDecStats",
 ]

@@ -12,6 +12,7 @@
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -19,6 +20,22 @@ import torch
 
 from . import _device as D
 from . import _lib
+
+_WS_LOCK = threading.Lock()
+_WS = {}
+
+
+def _spec_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled scratch for ``lps_spec_verify``, cached per (device,
+    stream): every launch leaves it ready for the next, and launches on one
+    stream never overlap."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        t = _WS.get(key)
+        if t is None or t.numel() < nbytes:
+            t = torch.zeros((max(nbytes, 1 << 20),), dtype=torch.uint8, device=device)
+            _WS[key] = t
+        return t
 
 
 def verify_drafts_batched(target_probs: torch.Tensor, draft_probs: torch.Tensor, draft_tokens: torch.Tensor,
@@ -93,7 +110,7 @@ def spec_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_t
     ur = u_resample.to(device=dev, dtype=torch.float32).reshape(B, k1).contiguous()
     lib = _lib.load()
     ws_bytes = lib.lps_spec_workspace_bytes(B, k, V)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    ws = _spec_workspace(dev, ws_bytes)
     out = SpecVerifyOutput(
         torch.empty((B,), dtype=torch.int32, device=dev),
         torch.empty((B, k1), dtype=torch.int64, device=dev),
@@ -126,7 +143,7 @@ def spec_verify(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_t
     a.q_draft = D.ptr(out.q_draft)
     a.row_status = D.ptr(out.status)
     a.workspace = D.ptr(ws)
-    a.workspace_bytes = ws_bytes
+    a.workspace_bytes = ws.numel()
     with torch.cuda.device(dev):
         rc = lib.lps_spec_verify(ctypes.byref(a), D.stream_of(dev))
     _lib.check(rc, "lps_spec_verify")

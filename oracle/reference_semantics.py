@@ -11,7 +11,8 @@ DavidAkinpelu/llm-pipeline:
 * ``src/llm_pipeline/inference/sampling.py:51-238``   (Sampler.sample_token and
   its filters), ``:240-279`` (Mirostat v2);
 * ``src/llm_pipeline/inference/speculative.py:50-62, 119-174, 264-276``
-  (sampling primitives and the accept / reject / resample step);
+  (sampling primitives and the accept / reject / resample step), ``:68-178``
+  and ``:206-280`` (the two-model and MTP driver loops);
 * ``src/llm_pipeline/inference/speculative_kernel.py:24-58, 84-87``
   (``verify_drafts_batched`` and its torch reference);
 * ``src/llm_pipeline/inference/continuous_batching.py:394-401`` (heterogeneous
@@ -495,3 +496,118 @@ def mirostat_v2_ref(logits: torch.Tensor, temperature: float, tau: float, eta: f
         k = max(1, int(math.exp(prev)))
         x = apply_top_k(x, k)
     return draw_inverse_cdf(x.reshape(-1), u), prev, k
+
+
+# --------------------------------------------------------------------------- #
+# Speculative-decoding drivers (speculative.py:68-178, :206-280)
+# --------------------------------------------------------------------------- #
+
+
+def _plain(temperature: float) -> RowParams:
+    """The speculative path's plain distribution ``softmax(logits / T)``
+    (``speculative.py:50-57``): no top-k / top-p / penalties."""
+    return RowParams(temperature=temperature, top_k=0, top_p=1.0)
+
+
+def spec_decode_ref(target_forward, draft_forward, prompt_ids: torch.Tensor, max_new_tokens: int, k: int,
+                    temperature: float, eos_token_id: Optional[int], uniforms):
+    """``speculative.py:68-178`` for one request ``[1, T]`` with the build's
+    draws from caller uniforms.  Round ``r`` (0-based) takes
+    ``uniforms(r) -> (u_draft[k], u_accept[k], u_resample[k+1])``.
+
+    * Draft step ``s`` (``:102-111``): token from ``softmax(draft(seq)[-1] / T)``
+      by the inverse CDF at ``u_draft[s]`` (greedy: argmax).
+    * One target forward over ``seq + drafts`` (``:115-116``).
+    * The accept / reject / resample block (``:119-174``) is ``spec_verify_ref``
+      on target rows ``base-1 .. base-1+k``.
+    * Emitted: the accepted drafts, then the replacement or bonus token; an
+      accepted draft equal to ``eos`` ends the run right after it (``:136-142``),
+      as does a replacement / bonus equal to ``eos`` (``:159-163``, ``:170-172``).
+    * ``accepted`` grows by the accepted drafts of the round (``:140``, ``:158``,
+      ``:169``); the loop runs while fewer than ``max_new_tokens`` are emitted
+      (``:97``) and may overshoot it within a round, as the reference does.
+
+    Returns ``(generated [1, n], rounds, target_calls, accepted)``."""
+    seq = prompt_ids.clone()
+    plen = prompt_ids.shape[1]
+    rounds = target_calls = accepted = 0
+    while seq.shape[1] - plen < max_new_tokens:
+        u_draft, u_accept, u_resample = uniforms(rounds)
+        rounds += 1
+        draft_seq = seq
+        toks, rows = [], []
+        for s in range(k):
+            d = draft_forward(draft_seq)[0, -1, :]
+            rows.append(upcast(d))
+            tok = sample_row(d, _plain(temperature), (), float(u_draft[s])).token
+            toks.append(tok)
+            draft_seq = torch.cat([draft_seq, torch.tensor([[tok]], dtype=seq.dtype)], dim=1)
+        t = target_forward(draft_seq)
+        target_calls += 1
+        base = seq.shape[1]
+        t_rows = upcast(t[0, base - 1: base + k, :])
+        n_acc, out, _, _, _ = spec_verify_ref(t_rows.unsqueeze(0), torch.stack(rows).unsqueeze(0),
+                                              torch.tensor([toks]), torch.as_tensor(u_accept).reshape(1, k),
+                                              torch.as_tensor(u_resample).reshape(1, k + 1), temperature)
+        na = int(n_acc[0])
+        emit = [int(v) for v in out[0, : na + 1]]
+        stop = False
+        if eos_token_id is not None:
+            for j in range(na):
+                if emit[j] == eos_token_id:
+                    emit = emit[: j + 1]
+                    na = j + 1
+                    stop = True
+                    break
+            if not stop and emit[-1] == eos_token_id:
+                stop = True
+        seq = torch.cat([seq, torch.tensor([emit], dtype=seq.dtype)], dim=1)
+        accepted += na
+        if stop:
+            break
+    return seq[:, plen:], rounds, target_calls, accepted
+
+
+def mtp_decode_ref(main_forward_with_hidden, mtp_head, prompt_ids: torch.Tensor, max_new_tokens: int,
+                   temperature: float, eos_token_id: Optional[int], uniforms):
+    """``speculative.py:206-280`` for one request with the build's draws.
+    Round ``r`` takes ``uniforms(r) -> (u_next, u_draft, u_accept)``.
+
+    * ``x_next`` from the main model's last logits (``:249-251``).
+    * The MTP head's draft from ``(hidden[-1], x_next)`` (``:253-258``).
+    * ``x_next`` is always kept (``:259-261``); the run ends on ``eos`` or once
+      ``max_new_tokens`` are emitted (``:262-265``).
+    * A second main pass over ``seq + x_draft`` verifies the draft at position
+      -2 with the accept rule of ``spec_verify_ref`` (``:267-276``); no
+      replacement token on rejection.
+
+    Returns ``(generated [1, n], rounds, target_calls, accepted)``."""
+    seq = prompt_ids.clone()
+    plen = prompt_ids.shape[1]
+    rounds = target_calls = accepted = 0
+    while seq.shape[1] - plen < max_new_tokens:
+        u_next, u_draft, u_accept = uniforms(rounds)
+        rounds += 1
+        logits, hidden = main_forward_with_hidden(seq)
+        target_calls += 1
+        x_next = sample_row(logits[0, -1, :], _plain(temperature), (), float(u_next)).token
+        mtp_logits = mtp_head(hidden[:, -1:, :], torch.tensor([[x_next]], dtype=seq.dtype))
+        x_draft = sample_row(mtp_logits[0, 0, :], _plain(temperature), (), float(u_draft)).token
+        accepted += 1
+        seq = torch.cat([seq, torch.tensor([[x_next]], dtype=seq.dtype)], dim=1)
+        if eos_token_id is not None and x_next == eos_token_id:
+            break
+        if seq.shape[1] - plen >= max_new_tokens:
+            break
+        v_logits, _ = main_forward_with_hidden(torch.cat([seq, torch.tensor([[x_draft]], dtype=seq.dtype)], dim=1))
+        target_calls += 1
+        n_acc, _, _, _, _ = spec_verify_ref(upcast(v_logits[0, -2:, :]).unsqueeze(0),
+                                            upcast(mtp_logits[0, :1, :]).unsqueeze(0), torch.tensor([[x_draft]]),
+                                            torch.tensor([[float(u_accept)]]), torch.tensor([[0.5, 0.5]]),
+                                            temperature)
+        if int(n_acc[0]) == 1:
+            seq = torch.cat([seq, torch.tensor([[x_draft]], dtype=seq.dtype)], dim=1)
+            accepted += 1
+            if eos_token_id is not None and x_draft == eos_token_id:
+                break
+    return seq[:, plen:], rounds, target_calls, accepted
