@@ -418,6 +418,125 @@ def spec_driver_bench(args):
     }), flush=True)
 
 
+def lm_head_bench(args):
+    """LM-head projection with the statistics epilogue (``lps_lm_head``) at the
+    c2 decode shape of a Qwen3-8B head: 64 rows, H = 4096, V = 151936, bf16.
+    Timed from HIP graphs of back-to-back launches.  Algorithmic bytes: the
+    weight, the hidden rows, the logits and the block statistics, each once.
+    Beside it: ``torch.matmul`` (hipBLASLt) on the same operands, and the
+    softmax producer both ways (projection + statistics + one-pass softmax, vs
+    projection + the two-pass softmax)."""
+    import torch
+    from lps import _device as D
+    from lps import _lib, fused_softmax, lm_head
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, H, V = 64, 4096, 151936
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((M, H), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    G = (V + 127) // 128
+    out = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+    stats = torch.empty((M, G, 2), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    a = _lib.LmHeadArgs()
+    a.x, a.w, a.out, a.stats = x.data_ptr(), w.data_ptr(), out.data_ptr(), stats.data_ptr()
+    a.dtype = a.out_dtype = D.dtype_code(x)
+    a.rows, a.vocab, a.hidden = M, V, H
+    a.x_stride, a.w_stride, a.out_stride = H, H, V
+
+    def ours():
+        rc = lib.lps_lm_head(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lps_lm_head failed: {rc}")
+
+    # self-check on a few rows against fp32 torch
+    ours()
+    torch.cuda.synchronize()
+    ref = x[:4].float() @ w.float().T
+    assert float(((out[:4].float() - ref).abs() - 2 ** -8 * ref.abs()).max()) < 1e-3, "lm_head self-check failed"
+
+    def graph_of(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        return gr
+
+    logits = torch.empty_like(out)
+
+    def fused_pipeline():
+        lo, st = lm_head(x, w, return_stats=True)
+        fused_softmax(lo, row_stats=st)
+
+    def plain_pipeline():
+        torch.matmul(x, w.T, out=logits)
+        fused_softmax(logits)
+
+    # the candidates are replayed in turn, round after round (the GPU's state
+    # drifts over a long run of one kernel); medians over the rounds
+    reps = 10
+    rounds = max(5, min(40, args.steps // 50))
+    graphs = {"ours": graph_of(ours, reps), "blas": graph_of(lambda: torch.matmul(x, w.T, out=out), reps),
+              "fused": graph_of(fused_pipeline, reps), "plain": graph_of(plain_pipeline, reps)}
+    times = {k: [] for k in graphs}
+    for _ in range(rounds):
+        for k, gr in graphs.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times[k].append(e0.elapsed_time(e1) / reps)
+    t_ours, t_blas = statistics.median(times["ours"]), statistics.median(times["blas"])
+    t_fused, t_plain = statistics.median(times["fused"]), statistics.median(times["plain"])
+    abytes = V * H * 2 + M * H * 2 + M * V * 2 + M * G * 8
+    gbs = abytes / (t_ours / 1e3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        vs = 16384
+        xc, wc = x[:8].float().cpu(), w[:vs].float().cpu()
+        torch.matmul(xc, wc.T)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            torch.matmul(xc, wc.T)
+            ts.append(time.perf_counter() - t0)
+        t = statistics.median(ts)
+        cb = vs * H * 2 + 8 * H * 2 + 8 * vs * 2
+        cpu = {"value": round(cb / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"8 rows x {vs} vocabulary rows of the workload, torch-CPU fp32 matmul (the reference's "
+                         f"nn.Linear on the CPU), bf16-equivalent bytes, median of 5"}
+    print(json.dumps({
+        "metric": "LM-head projection + softmax statistics, achieved HBM GB/s (64 x 4096 -> 151936 bf16)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": reps * rounds, "warmup": 4,
+        "ms_per_step": round(t_ours, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 in, f32 accumulate", "data": "synthetic",
+        "torch_matmul_ms": round(t_blas, 5),
+        "softmax_producer_ms": {"lm_head+stats -> one-pass softmax": round(t_fused, 5),
+                                "torch.matmul -> two-pass softmax": round(t_plain, 5)},
+        "config": {"workload": "c2 decode rows through a Qwen3-8B-shaped head: x [64, 4096] bf16, "
+                               "w [151936, 4096] bf16 (random), logits bf16 + 128-column block statistics",
+                   "algorithmic_bytes_per_call": abytes, "kernel": "lmhead_kernel<bf16, bf16>"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": hbm_traffic("lmhead", "c2")},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -438,7 +557,12 @@ def main():
                     help="time the row softmax (lps_softmax) on a workload instead of the sampler")
     ap.add_argument("--spec-driver", action="store_true",
                     help="time the batched speculative-decoding driver (zero-cost synthetic forwards)")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the LM-head projection with the softmax statistics epilogue")
     args = ap.parse_args()
+    if args.lm_head:
+        lm_head_bench(args)
+        return
     if args.spec_driver:
         spec_driver_bench(args)
         return

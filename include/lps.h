@@ -258,7 +258,41 @@ typedef struct lps_softmax_args {
   float* row_lse;                 /* float32 [rows] or NULL */
   void* workspace;                /* or NULL */
   size_t workspace_bytes;
+  /* optional block statistics of x from its producer (lps_lm_head's stats):
+   * per row, ceil(cols / stats_cols) pairs { max, sum(exp(v - max)) } over
+   * consecutive blocks of stats_cols columns; rows stats_stride floats apart.
+   * With them the softmax is one streaming pass (not with causal). */
+  const float* row_stats;
+  int64_t stats_stride;
+  int32_t stats_cols;
 } lps_softmax_args;
+
+/* LM-head projection with the softmax statistics epilogue, the logits
+ * producer of the path (models/qwen3/custom_builder.py:415,
+ * models/qwen3_5/model.py:263: logits = lm_head(hidden), nn.Linear without
+ * bias):
+ *   out[m, n] = sum_k x[m, k] * w[n, k]   (fp32 accumulation, in out_dtype)
+ *   stats[m, b] = { max, sum(exp(v - max)) } over columns [128 b, 128 b + 128)
+ *                 of the stored (rounded) row, b < ceil(vocab / 128).
+ * x, w: bf16 or fp16 (same dtype), rows 16-byte aligned (strides multiples of
+ * 8 elements), hidden a multiple of 16.  stats may be NULL. */
+#define LPS_LMHEAD_BLOCK_COLS 128
+typedef struct lps_lm_head_args {
+  const void* x;                  /* [rows, hidden] */
+  const void* w;                  /* [vocab, hidden] */
+  void* out;                      /* [rows, vocab] in out_dtype */
+  float* stats;                   /* float32 [rows, ceil(vocab / 128), 2] or NULL */
+  int32_t dtype;                  /* lps_dtype of x and w: BF16 or F16 */
+  int32_t out_dtype;              /* lps_dtype of out */
+  int32_t rows;
+  int32_t vocab;
+  int32_t hidden;
+  int64_t x_stride;               /* elements */
+  int64_t w_stride;               /* elements */
+  int64_t out_stride;             /* elements */
+} lps_lm_head_args;
+
+int lps_lm_head(const lps_lm_head_args* args, void* stream);
 
 /* Bytes of workspace lps_softmax uses for rows x cols of dtype (0: none). */
 size_t lps_softmax_workspace_bytes(int rows, int cols, int dtype);

@@ -5,6 +5,7 @@
 
 #include "lps_fast_kernel.h"
 #include "lps_generic.h"
+#include "lps_lmhead.h"
 #include "lps_softmax.h"
 #include "lps_spec.h"
 
@@ -492,6 +493,47 @@ size_t lps_softmax_workspace_bytes(int rows, int cols, int dtype) {
   return p.kind == 1 ? softmax_records_bytes(rows, p.G) : 0;
 }
 
+int lps_lm_head(const lps_lm_head_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  if (a->dtype != LPS_DTYPE_BF16 && a->dtype != LPS_DTYPE_F16) return LPS_EUNSUPPORTED_DTYPE;
+  if (!dtype_ok(a->out_dtype)) return LPS_EUNSUPPORTED_DTYPE;
+  if (a->rows < 0 || a->vocab < 1 || a->hidden < 16 || a->hidden % 16) return LPS_EINVAL;
+  if (a->rows == 0) return LPS_OK;
+  if (!a->x || !a->w || !a->out) return LPS_EINVAL;
+  if (a->x_stride < a->hidden || a->w_stride < a->hidden || (a->rows > 1 && a->out_stride < a->vocab)) return LPS_EINVAL;
+  // 16-byte operand loads: x and w rows start 16-byte aligned
+  if (reinterpret_cast<uintptr_t>(a->x) % 16 || reinterpret_cast<uintptr_t>(a->w) % 16 || a->x_stride % 8 ||
+      a->w_stride % 8)
+    return LPS_EINVAL;
+  if ((a->rows + LMH_BM - 1) / LMH_BM > 65535) return LPS_EINVAL;   // grid y
+  LmHeadParams P{};
+  P.x = a->x;
+  P.w = a->w;
+  P.out = a->out;
+  P.stats = a->stats;
+  P.M = a->rows;
+  P.V = a->vocab;
+  P.H = a->hidden;
+  P.x_stride = a->x_stride;
+  P.w_stride = a->w_stride;
+  P.out_stride = a->rows > 1 ? a->out_stride : a->vocab;
+  P.G = (a->vocab + LMH_BN - 1) / LMH_BN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)P.G, (unsigned)((a->rows + LMH_BM - 1) / LMH_BM));
+#define LMH_LAUNCH(DT, ODT) hipLaunchKernelGGL((lmhead_kernel<DT, ODT, LMH_KC, LMH_NB>), grid, dim3(256), 0, s, P)
+  if (a->dtype == LPS_DTYPE_BF16) {
+    if (a->out_dtype == LPS_DTYPE_BF16) LMH_LAUNCH(LPS_DTYPE_BF16, LPS_DTYPE_BF16);
+    else if (a->out_dtype == LPS_DTYPE_F16) LMH_LAUNCH(LPS_DTYPE_BF16, LPS_DTYPE_F16);
+    else LMH_LAUNCH(LPS_DTYPE_BF16, LPS_DTYPE_F32);
+  } else {
+    if (a->out_dtype == LPS_DTYPE_BF16) LMH_LAUNCH(LPS_DTYPE_F16, LPS_DTYPE_BF16);
+    else if (a->out_dtype == LPS_DTYPE_F16) LMH_LAUNCH(LPS_DTYPE_F16, LPS_DTYPE_F16);
+    else LMH_LAUNCH(LPS_DTYPE_F16, LPS_DTYPE_F32);
+  }
+#undef LMH_LAUNCH
+  return hipGetLastError() == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
+
 int lps_softmax(const lps_softmax_args* a, void* stream) {
   if (!a) return LPS_EINVAL;
   if (!dtype_ok(a->dtype)) return LPS_EUNSUPPORTED_DTYPE;
@@ -518,6 +560,33 @@ int lps_softmax(const lps_softmax_args* a, void* stream) {
   auto aligned = [&](const void* p, int64_t stride) {
     return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (a->rows <= 1 || stride % vpl == 0);
   };
+  if (a->row_stats) {
+    // one streaming pass from the producer's block statistics
+    const int nstats = a->stats_cols > 0 ? (int)(((int64_t)a->cols + a->stats_cols - 1) / a->stats_cols) : 0;
+    if (a->causal || a->stats_cols < 1 || (a->rows > 1 && a->stats_stride < 2 * (int64_t)nstats)) return LPS_EINVAL;
+    if (aligned(a->x, a->x_stride) && aligned(a->out, a->out_stride)) {
+      const int64_t vecs = ((int64_t)a->cols + vpl - 1) / vpl;
+      const int nv = vecs > (int64_t)SM_NT * 2 ? 8 : 2;
+      S.G = (int)((vecs + (int64_t)SM_NT * nv - 1) / ((int64_t)SM_NT * nv));
+      S.row_stats = a->row_stats;
+      S.stats_stride = a->rows > 1 ? a->stats_stride : 2 * (int64_t)nstats;
+      S.nstats = nstats;
+      const dim3 grid((unsigned)(((int64_t)S.rows + 7) / 8 * S.G * 8));
+#define SMA_LAUNCH(DT)                                                                       \
+  do {                                                                                       \
+    if (nv == 8) hipLaunchKernelGGL((softmax_apply_kernel<DT, 8>), grid, dim3(SM_NT), 0, s, S); \
+    else hipLaunchKernelGGL((softmax_apply_kernel<DT, 2>), grid, dim3(SM_NT), 0, s, S);         \
+  } while (0)
+      switch (a->dtype) {
+        case LPS_DTYPE_F32: SMA_LAUNCH(LPS_DTYPE_F32); break;
+        case LPS_DTYPE_BF16: SMA_LAUNCH(LPS_DTYPE_BF16); break;
+        default: SMA_LAUNCH(LPS_DTYPE_F16); break;
+      }
+#undef SMA_LAUNCH
+      e = hipGetLastError();
+      return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+    }
+  }
   if (aligned(a->x, a->x_stride) && aligned(a->out, a->out_stride)) {
     SmPlan p = softmax_plan(a->dtype, a->rows, a->cols);
     if (p.kind == 1 && p.G > 1) {

@@ -49,6 +49,9 @@ struct SoftmaxParams {
   int G;                            // chunk kernel: workgroups per row
   void* records;                    // chunk kernel, G > 1: rows x G 8-byte records, zero between launches
   uint32_t* done;                   // chunk kernel, G > 1: rows counters, zero between launches
+  const float* row_stats;           // apply kernel: per row, nstats (max, sum) block pairs
+  int64_t stats_stride;             // floats between rows of row_stats
+  int nstats;
 };
 
 // Per-chunk record of the split softmax, 0 while absent (see pack_record);
@@ -458,6 +461,61 @@ __global__ __launch_bounds__(SM_NT) void softmax_chunk_kernel(SoftmaxParams S) {
   const int lim = causal_limit(S, r);
   if ((j + 1) * CH <= lim) chunk_row<DT, NV, true>(S, sh, row, orow, r, j, lim);   // lim <= cols
   else chunk_row<DT, NV, false>(S, sh, row, orow, r, j, lim);
+}
+
+// Single pass from block statistics (the LM-head epilogue's): every
+// workgroup of a row combines the row's nstats (max, sum) pairs in the same
+// order (thread t takes pairs t, t + 256, ...; then the block reduction), so
+// all of them hold the same (M, S); then its chunk is streamed as
+// exp2(x c - M c) / S.  Mapping as the chunk kernel's.
+template <int DT, int NV>
+__global__ __launch_bounds__(SM_NT) void softmax_apply_kernel(SoftmaxParams S) {
+  __shared__ SmShared sh;
+  constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
+  constexpr int VPL = DT == LPS_DTYPE_F32 ? 4 : 8;
+  constexpr int CH = SM_NT * NV * VPL;
+  const int G = S.G;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int r = (slot / G) * 8 + xcd, j = slot % G;
+  if (r >= S.rows) return;   // uniform over the workgroup
+  const int tid = threadIdx.x;
+  const void* row = reinterpret_cast<const char*>(S.x) + (int64_t)ES * r * S.x_stride;
+  void* orow = reinterpret_cast<char*>(S.out) + (int64_t)ES * r * S.out_stride;
+  const int n = S.cols;
+  // the chunk's loads first: they are in flight while the statistics combine
+  float v[NV][VPL];
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const int i0 = j * CH + (k * SM_NT + tid) * VPL;
+    if (i0 + VPL <= n) {
+      loadv<DT, VPL>(row, i0, v[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VPL; e++) v[k][e] = i0 + e < n ? load1<DT>(row, i0 + e) : -INFINITY;
+    }
+  }
+  const float* st = S.row_stats + (int64_t)r * S.stats_stride;
+  MS acc{-INFINITY, 0.0};
+  for (int b = tid; b < S.nstats; b += SM_NT) acc = ms_combine(acc, MS{st[2 * b], (double)st[2 * b + 1]});
+  const MS rs = block_reduce_ms(acc, sh);
+  if (S.row_lse && j == 0 && tid == 0) S.row_lse[r] = row_lse_value(rs);
+  const float Mc = __fmul_rn(rs.m, SM_LOG2E);
+  const float inv = rs.m == -INFINITY ? __builtin_nanf("") : (float)(1.0 / rs.s);
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const int i0 = j * CH + (k * SM_NT + tid) * VPL;
+    if (i0 >= n) continue;
+    float p[VPL];
+#pragma unroll
+    for (int e = 0; e < VPL; e++) p[e] = __fmul_rn(__builtin_amdgcn_exp2f(__builtin_fmaf(v[k][e], SM_LOG2E, -Mc)), inv);
+    if (i0 + VPL <= n) {
+      store16<DT>(orow, i0, p);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VPL; e++)
+        if (i0 + e < n) store1<DT>(orow, i0 + e, p[e]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -7,6 +7,7 @@ from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_
                     raise_on_status, sample_rows)
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
+from .lmhead import lm_head
 from .softmax import fused_softmax, fused_softmax_triton
 from .spec_driver import (mtp_speculative_decode, mtp_speculative_decode_batched, speculative_decode,
                           speculative_decode_batched)
@@ -27,6 +28,7 @@ __all__ = [
     "raise_on_status",
     "verify_drafts_batched",
     "spec_verify",
+    "lm_head",
     "speculative_decode",
     "speculative_decode_batched",
     "mtp_speculative_decode",

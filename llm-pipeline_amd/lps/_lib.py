@@ -63,6 +63,19 @@ class SampleArgs(ctypes.Structure):
     ]
 
 
+class LmHeadArgs(ctypes.Structure):
+    """Mirror of ``lps_lm_head_args``."""
+
+    _fields_ = [
+        ("x", _vp), ("w", _vp), ("out", _vp), ("stats", _vp), ("dtype", _i32), ("out_dtype", _i32),
+        ("rows", _i32), ("vocab", _i32), ("hidden", _i32), ("x_stride", _i64), ("w_stride", _i64),
+        ("out_stride", _i64),
+    ]
+
+
+LMHEAD_BLOCK_COLS = 128
+
+
 class SoftmaxArgs(ctypes.Structure):
     """Mirror of ``lps_softmax_args``."""
 
@@ -70,6 +83,7 @@ class SoftmaxArgs(ctypes.Structure):
         ("x", _vp), ("out", _vp), ("dtype", _i32), ("rows", _i32), ("cols", _i32),
         ("x_stride", _i64), ("out_stride", _i64), ("causal", _i32), ("seq_len", _i32), ("row_offset", _i32),
         ("row_lse", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("row_stats", _vp), ("stats_stride", _i64), ("stats_cols", _i32),
     ]
 
 
@@ -98,6 +112,7 @@ SIGNATURES = {
     "lps_verify_drafts": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "lps_softmax": (_i32, [ctypes.c_void_p, _vp]),
     "lps_softmax_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
+    "lps_lm_head": (_i32, [ctypes.c_void_p, _vp]),
 }
 
 _lib = None

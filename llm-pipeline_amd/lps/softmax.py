@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from typing import Tuple, Union
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -35,10 +35,14 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def fused_softmax(x: torch.Tensor, causal: bool = False, row_offset: int = 0,
-                  return_lse: bool = False) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+                  return_lse: bool = False, row_stats: Optional[torch.Tensor] = None,
+                  stats_cols: int = 128) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Softmax over the last axis of ``x [..., n_cols]`` (fp32 / bf16 / fp16 on
     a ROCm device).  ``return_lse`` also returns each row's log-sum-exp of the
-    masked values (fp32, shape ``x.shape[:-1]``; -inf for an all -inf row)."""
+    masked values (fp32, shape ``x.shape[:-1]``; -inf for an all -inf row).
+    ``row_stats [..., ceil(n_cols / stats_cols), 2]`` (float32 ``(max, sum(exp(v
+    - max)))`` per block of ``stats_cols`` columns, as ``lm_head(...,
+    return_stats=True)`` returns them) makes the softmax one streaming pass."""
     D.require_device(x, "x")
     if x.dim() < 1:
         raise ValueError("x must have at least one axis")
@@ -62,6 +66,17 @@ def fused_softmax(x: torch.Tensor, causal: bool = False, row_offset: int = 0,
     a.seq_len = shape[-2] if x.dim() >= 2 else 1
     a.row_offset = int(row_offset)
     a.row_lse = D.ptr(lse)
+    if row_stats is not None:
+        if causal:
+            raise ValueError("row_stats cannot be combined with causal")
+        nst = (n_cols + stats_cols - 1) // stats_cols
+        st = row_stats.reshape(-1, nst, 2)
+        if st.shape[0] != rows or st.dtype != torch.float32 or st.device != x.device:
+            raise ValueError(f"row_stats must be float32 [..., {nst}, 2] on the device of x")
+        st = st.contiguous()
+        a.row_stats = st.data_ptr()
+        a.stats_stride = 2 * nst
+        a.stats_cols = stats_cols
     if rows:
         lib = _lib.load()
         nb = lib.lps_softmax_workspace_bytes(rows, n_cols, a.dtype)

@@ -68,7 +68,7 @@ def _c_layout(struct, fields):
 
 
 @pytest.mark.parametrize("cname,pyname", [("lps_sample_args", "SampleArgs"), ("lps_spec_args", "SpecArgs"),
-                                         ("lps_softmax_args", "SoftmaxArgs")])
+                                         ("lps_softmax_args", "SoftmaxArgs"), ("lps_lm_head_args", "LmHeadArgs")])
 def test_struct_layout_matches_c(cname, pyname):
     from lps import _lib
     py = getattr(_lib, pyname)
@@ -180,3 +180,27 @@ def test_sampling_params_and_histories_host():
     assert q.presence_penalty.tolist() == [0.0, 0.0]
     h, n = pad_histories([[1, 2, 3], [], [7]], "cpu")
     assert h.shape == (3, 3) and n.tolist() == [3, 0, 1] and h[2, 0].item() == 7
+
+
+def test_lm_head_argument_errors(lib):
+    """Argument checks of lps_lm_head happen before any launch (no GPU)."""
+    from lps import _lib
+    a = _lib.LmHeadArgs()
+    a.dtype, a.out_dtype, a.rows, a.vocab, a.hidden = 0, 0, 4, 100, 64
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 2                # fp32 inputs are not supported
+    a.dtype = 1
+    a.hidden = 40
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 1                # hidden not a multiple of 16
+    a.hidden = 64
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 1                # null pointers
+    a.x, a.w, a.out = 0x1000, 0x2000, 0x3000
+    a.x_stride, a.w_stride, a.out_stride = 60, 64, 100
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 1                # x_stride < hidden
+    a.x_stride = 68
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 1                # stride not a multiple of 8
+    a.x = 0x1004
+    a.x_stride = 64
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 1                # misaligned rows
+    a.rows = 0
+    assert lib.lps_lm_head(ctypes.byref(a), None) == 0
+    assert lib.lps_lm_head(None, None) == 1
