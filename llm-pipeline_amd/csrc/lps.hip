@@ -69,7 +69,7 @@ FastWs fast_layout(void* base, int R, int V) {
   const int G = (V + FCH_MIN - 1) / FCH_MIN;  // the most chunks any dtype uses
   if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
   w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
-  w.h_stride = (int64_t)round_up((size_t)G * HB, 32);                // floats
+  w.h_stride = (int64_t)round_up((size_t)G * (HB + FB), 32);         // floats
   // candidates: G chunks of PUB slots, for either chunk variant
   constexpr int NR2 = fused_nr<LPS_DTYPE_BF16>();
   const int G2 = (V + FT * NR2 - 1) / (FT * NR2);

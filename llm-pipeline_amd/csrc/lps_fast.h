@@ -57,12 +57,20 @@ constexpr int FCAP = FT * FCPT;         // finaliser candidate capacity (4096)
 constexpr int KEPTCAP = 512;            // finaliser kept list
 constexpr int HB = 256;                 // histogram bins per chunk (1/8 log2 unit each)
 constexpr int HS = 8;                   // bins per log2 unit
+constexpr int FB = 256;                 // nucleus level-2 fine bins (one per thread)
+constexpr int FSUB_MAX = 5;             // fine bins per coarse bin: at most 2^5
+#ifndef LPS_FINE_MIN
+#define LPS_FINE_MIN 1024               // level 2 runs when the coarse region may hold more elements
+#endif
 #ifndef LPS_SELD
-#define LPS_SELD 12
+#define LPS_SELD 11
+#endif
+#ifndef LPS_SELDM
+#define LPS_SELDM 9
 #endif
 constexpr int SELD = LPS_SELD;          // count-select digit bits
 constexpr int SELB = 1 << SELD;         // count-select histogram bins
-constexpr int SELDM = 10;               // mass-select digit bits
+constexpr int SELDM = LPS_SELDM;        // mass-select digit bits
 constexpr int SELBM = 1 << SELDM;       // mass-select histogram bins
 constexpr int HPF = 4;                  // history ids prefetched per thread
 constexpr int MAXG = 64;                // chunks per row (V <= 524287)
@@ -84,19 +92,19 @@ struct ChunkSum2 {   // published at the end of phase 1
   uint32_t flags;    // CF_*
   uint64_t above;    // nucleus: fixed-point mass above the cut region (chunk reference)
   uint32_t nabove;   // nucleus: count above the cut region
-  int32_t blo, bhi;  // nucleus: the cut region (absolute bins), the same in every chunk
-  uint32_t pad;
+  int32_t blo, bhi;  // nucleus: the cut region (absolute bins of 2^-(3 + sub) log2 units), the same in every chunk
+  uint32_t sub;
 };
 
 struct FParams {
   KParams k;           // per-row parameters and outputs (shared with the general kernel)
   int G;               // chunks per row
   int heavy_first;     // fused kernel, R <= 128: dispatch rows without top-k first
-  uint32_t* counters;  // [R * 32]: fused handoff arrivals at [0], nucleus barrier arrivals at [2]; zero between launches
+  uint32_t* counters;  // [R * 32]: fused handoff arrivals at [0], nucleus barrier arrivals at [2] and [4]; zero between launches
   int32_t* status;     // [R]
   ChunkSum1* sum1;     // row r at sum1 + r * s_stride
   ChunkSum2* sum2;
-  float* hist;         // row r at hist + r * h_stride: G x HB masses (chunk reference)
+  float* hist;         // row r at hist + r * h_stride: G x HB masses (chunk reference), then G x FB fine masses
   uint2* cands;        // row r at cands + r * c_stride: G x PUB (x key, idx), PUB of the chunk variant
   int64_t s_stride, h_stride, c_stride;
 };
@@ -119,6 +127,7 @@ struct CSharedT : XShared {
   uint32_t hc[NR * 128];                  // history counts: 16-bit (fp32 chunks) or 8-bit (packed chunks)
   unsigned long long hm[HB];              // chunk mass histogram, fixed point
   unsigned long long gm[HB];              // nucleus region: merged row histogram, fixed point
+  unsigned long long fm[FB];              // nucleus region level 2: chunk fine histogram, fixed point
   double scale[MAXG];                     // nucleus region: chunk -> row reference
   int32_t btop[MAXG];
 };
@@ -141,6 +150,7 @@ struct FSharedT : XShared {
     } k;                                  // kept list
     uint32_t hc[NR * 128];                // rescan history counts
   } x;
+  int32_t cidx[FCAP];                     // vocabulary index of candidate slot e of thread t, at e * FT + t
   uint32_t pre[MAXG + 1];                 // candidate prefix over chunks
   double scale[MAXG];                     // chunk -> row reference
   float wm[MAXG];                         // chunk max * c (the chunk's mass reference)
@@ -439,18 +449,16 @@ __device__ __forceinline__ void mark_counts(Chunk<DT, VEC, NR>& C, int n, const 
 
 // Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end
 // of the division-collision group of x0, so that "z >= fl(x0 / T)" is
-// "x >= result" for every x.
+// "x >= result" for every x.  The group is searched at most 64 keys down, all
+// at once: lane l of the wave tests the step from l to l + 1 keys below x0,
+// and the group ends at the first failing lane.  x0 is wave-uniform and every
+// lane of the wave calls this.
 __device__ __forceinline__ float collision_lo(float x0, float T) {
   const float q = __fdiv_rn(x0, T);
-  float x = x0;
-  for (int i = 0; i < 64; i++) {
-    const uint32_t k = f2key(x);
-    if (k <= kNegInfKey + 1u) break;
-    const float y = key2f(k - 1u);
-    if (__fdiv_rn(y, T) != q) break;
-    x = y;
-  }
-  return x;
+  const uint32_t k0 = f2key(x0);
+  const uint32_t k = k0 - (threadIdx.x & 63u);
+  const uint64_t fail = wballot(!(k > kNegInfKey + 1u && __fdiv_rn(key2f(k - 1u), T) == q));
+  return key2f(k0 - (fail ? (uint32_t)__builtin_ctzll(fail) : 64u));
 }
 
 // ---------------------------------------------------------------------------
@@ -565,7 +573,12 @@ __device__ __forceinline__ MassSel sel_mass(const uint32_t (&ck)[FCPT], int np, 
         if (up == hi) {
           const uint32_t b = dw > 0 ? ((d >> sh) & ((1u << dw) - 1u)) : 0u;
           atomicAdd(&H.cnt[buf][b], 1u);
-          const uint64_t m = mass(e);
+          // the mass is recomputed at every level: hoisted out of the level
+          // loop, the 16 64-bit masses would hold 32 more registers for the
+          // whole select and cost the fused kernel a workgroup per CU
+          uint32_t kv = ck[e];
+          asm volatile("" : "+v"(kv));
+          const uint64_t m = mass(kv);
           if (m) atomicAdd(&H.mass[buf][b], (unsigned long long)m);
         }
       }

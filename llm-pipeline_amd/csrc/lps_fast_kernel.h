@@ -166,7 +166,7 @@ __device__ __forceinline__ ChunkId chunk_id(int G) {
 // pure: the longest finalisers) are dispatched first, so that their
 // finalisers overlap the chunk work of the rows dispatched after them.
 // Virtual row vr -> row; a bijection on [0, R), the same in every workgroup.
-__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr) {
+__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr, bool& is_heavy) {
   const int lane = threadIdx.x & 63;
   auto heavy = [&](int r) -> bool {
     if (r >= P.R) return false;
@@ -178,6 +178,7 @@ __device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr) {
   const uint64_t v1 = wballot(lane < P.R), v2 = wballot(lane + 64 < P.R);
   const int nh = __popcll(m1) + __popcll(m2);
   const bool hv = vr < nh;
+  is_heavy = hv;
   const uint64_t a = hv ? m1 : (v1 & ~m1), b = hv ? m2 : (v2 & ~m2);
   const int k = hv ? vr : vr - nh;
   const int pa = __popcll(a);
@@ -408,7 +409,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
   // ---- nucleus: histograms, one intra-XCD barrier, the common cut region ----
   uint64_t above = 0;
   uint32_t nabove = 0;
-  int blo = 0, bhi = -1;
+  int blo = 0, bhi = -1, rsub = 0;
   if (mode == MODE_NUCLEUS) {
     hist[(int64_t)j * HB + tid] = (float)((double)S.hm[tid] / (double)kMassScale);
     wait_stores();
@@ -493,9 +494,80 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
     } else if (rfin) {
       bhi = btg - tmin;
       blo = btg - tmax;
+      // ---- level 2: a coarse region holding many elements is split into 2^sub
+      // fine bins per bin; the fine bins are merged over the row after a second
+      // barrier, and the fine bins meeting the interval become the region ----
+      // The region's element count is bounded from its merged masses (an element
+      // of absolute bin btg - t has mass >= 2^-(t + 1) / 8 of the row maximum).
+      const bool inr = tid >= tmin && tid <= tmax;
+      const double cest = inr ? m * exp2((double)(tid + 1) * 0.125) : 0.0;
+      const double nest = bcombine(wsum(cest), S.xe, OpAdd{});
+      const int nreg = bhi - blo + 1;
+      int sub = 0;
+      if (nest > (double)LPS_FINE_MIN)
+        while (sub < FSUB_MAX && (nreg << (sub + 1)) <= FB) sub++;
+      int flo = blo << sub, fhi = ((bhi + 1) << sub) - 1;  // the region in fine bins (absolute)
+      const float wmc = __fmul_rn(xm, c);
+      auto fbin_of = [&](float v) -> int { return (int)floorf(__fmul_rn(__fmul_rn(v, c), (float)(HS << sub))); };
+      uint64_t afm = 0ull;  // exact mass of this chunk's fine bins above the fine region (thread tid: fine bin tid)
+      if (sub > 0) {
+        const int nf = nreg << sub;  // fine bins of the coarse region, <= FB
+        const int fb0 = flo;
+        S.fm[tid] = 0ull;  // FB == FT
+        if (tid == tmin) S.md[1] = ex;  // merged mass above the coarse region
+        __syncthreads();
+        with_pen<PK>(wpen, [&](auto PT) {
+          constexpr bool PEN = decltype(PT)::value;
+#pragma unroll
+          for (int s = 0; s < NE; s++) {
+            const float v = C.template val<PEN>(s, pa);
+            const bool fin = v != -INFINITY;
+            const float w = fin ? __fmul_rn(v, c) : 0.0f;
+            const int fi = (int)floorf(__fmul_rn(w, (float)(HS << sub))) - fb0;
+            if (fin && fi >= 0 && fi < nf) atomicAdd(&S.fm[fi], (unsigned long long)mass_fixed(chunk_mass(w, wmc)));
+          }
+        });
+        __syncthreads();
+        float* hfine = hist + (int64_t)G * HB;  // G x FB fine masses (chunk reference), after the G x HB bins
+        hfine[(int64_t)j * FB + tid] = (float)((double)S.fm[tid] / (double)kMassScale);
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) {
+          l2_fetch_add(ctr + 4, 1u);
+          int spins = 0;
+          while (ld_l2_u32(ctr + 4) < (uint32_t)G) {
+            if (++spins > (1 << 20)) { S.mi[9] = 1; break; }
+            __builtin_amdgcn_s_sleep(2);
+          }
+        }
+        __syncthreads();
+        // fine bin nf - 1 - tid (top first) of every chunk, rescaled to the row
+        // maximum, summed in fixed point in one register per bin
+        const int fi = nf - 1 - tid;
+        uint64_t mf = 0ull;
+        if (fi >= 0) {
+          for (int q = 0; q < G; q++) {
+            const float h = hfine[(int64_t)q * FB + fi];
+            const double sc = S.scale[q];
+            if (sc > 0.0 && h > 0.0f) mf += (unsigned long long)((double)h * sc * kGm);
+          }
+        }
+        const double m2 = (double)mf / kGm;
+        double mtot2;
+        const double ex2 = S.md[1] + bscan_excl<double>(m2, &mtot2, S.xd);
+        const bool meets2 = m2 > 0.0 && ex2 + m2 >= Pm - eps && ex2 <= Pm + eps;
+        const int f1 = (int)bcombine(wmin(meets2 ? (uint32_t)tid : (1u << 30)), S.xg, OpMin{});
+        const int f2 = (int)bcombine(wmax(meets2 ? (uint32_t)tid + 1u : 0u), S.xh, OpMax{}) - 1;
+        if (f2 >= 0) {  // else the coarse region stays (its fine bins all)
+          fhi = fb0 + (nf - 1 - f1);
+          flo = fb0 + (nf - 1 - f2);
+        }
+        if (S.mi[9] == 1) cflags |= CF_REGION;
+        if (tid < nf && fb0 + tid > fhi) afm = (uint64_t)S.fm[tid];
+      }
       // this chunk: mass and count above the region, candidates inside (slots xa xb xc)
-      const int hbt = btop - (bhi + 1);  // chunk histogram bins 0..hbt lie above the region
-      uint64_t am = (xm_finite && tid <= hbt) ? (uint64_t)S.hm[tid] : 0ull;
+      const int hbt = btop - (bhi + 1);  // chunk histogram bins 0..hbt lie above the coarse region
+      uint64_t am = ((xm_finite && tid <= hbt) ? (uint64_t)S.hm[tid] : 0ull) + afm;
       uint32_t na = 0, nc = 0;
       uint64_t inreg = 0;
       with_pen<PK>(wpen, [&](auto PT) {
@@ -504,9 +576,9 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
         for (int s = 0; s < NE; s++) {
           const float v = C.template val<PEN>(s, pa);
           if (v != -INFINITY) {
-            const int b = wbin(v, c);
-            na += b > bhi ? 1u : 0u;
-            const bool in = b >= blo && b <= bhi;
+            const int b = fbin_of(v);
+            na += b > fhi ? 1u : 0u;
+            const bool in = b >= flo && b <= fhi;
             nc += in ? 1u : 0u;
             if (NE <= 64) inreg |= in ? (1ull << (s & 63)) : 0ull;
           }
@@ -532,8 +604,8 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
               v = in ? C.template val<PEN>(s, pa) : 0.0f;
             } else {
               v = C.template val<PEN>(s, pa);
-              const int b = v != -INFINITY ? wbin(v, c) : (blo - 1);
-              in = b >= blo && b <= bhi;
+              const int b = v != -INFINITY ? fbin_of(v) : (flo - 1);
+              in = b >= flo && b <= fhi;
             }
             if (in) {
               if (p < (uint32_t)PUB) out[p] = make_uint2(f2key(v), (uint32_t)(lo + CK::local(s)));
@@ -544,6 +616,9 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
       }
       ncand = ctot > (uint32_t)PUB ? (uint32_t)PUB : ctot;
       if (ctot > (uint32_t)PUB) cflags |= CF_OVERFLOW;
+      blo = flo;  // the summary carries the region in fine bins, and sub
+      bhi = fhi;
+      rsub = sub;
     }
     LPS_STAMP(20);
   }
@@ -552,7 +627,7 @@ __device__ __forceinline__ int chunk_body(const FParams& F, CSharedT<NR>& S, con
   LPS_STAMP(6);
   if (tid == 0) {
     ChunkSum2 a;
-    a.ncand = ncand; a.flags = cflags; a.above = above; a.nabove = nabove; a.blo = blo; a.bhi = bhi; a.pad = 0;
+    a.ncand = ncand; a.flags = cflags; a.above = above; a.nabove = nabove; a.blo = blo; a.bhi = bhi; a.sub = (uint32_t)rsub;
     s2[j] = a;
   }
   return mode;
@@ -581,6 +656,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
   if (tid == 0) {  // the row's counters back to zero for the next launch
     F.counters[(int64_t)r * 32] = 0u;
     F.counters[(int64_t)r * 32 + 2] = 0u;
+    F.counters[(int64_t)r * 32 + 4] = 0u;
   }
   const RowCfg g = row_cfg(P, r);
   if (g.mode == MODE_DEFER) return 1;
@@ -629,8 +705,9 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
     }
     if (lane == 0) {
       S.pre[G] = NC;
-      S.mi[18] = b.blo;  // every chunk derived the same cut region
+      S.mi[18] = b.blo;  // every chunk derived the same cut region (fine bins of 2^-(3 + sub) log2 units)
       S.mi[19] = b.bhi;
+      S.mi[31] = (int)b.sub;
       S.mi[12] = (int)fl;
       S.mi[13] = (int)NC;
       S.mi[14] = (int)ninf_all;
@@ -643,7 +720,8 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
   }
   __syncthreads();
   const uint32_t fl = (uint32_t)S.mi[12];
-  const int blo = S.mi[18], bhi = S.mi[19];
+  const int blo = S.mi[18], bhi = S.mi[19], rsub = S.mi[31];
+  auto rbin = [&](float x) -> int { return (int)floorf(__fmul_rn(__fmul_rn(x, c), (float)(HS << rsub))); };
   if (fl & (CF_OVERFLOW | CF_HISTORY | CF_SPLIT | CF_REGION)) return (int)fl;
   const int NC = S.mi[13];
   const uint32_t ninf_all = (uint32_t)S.mi[14];
@@ -681,9 +759,12 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       if (q + step < G && (int)S.pre[q + step] <= i) q += step;
     return cands[(int64_t)q * PUB + (i - (int)S.pre[q])];
   };
-  // Candidates in registers: thread t holds candidate e * FT + t in slot e (z key, index).
+  // Candidates: thread t holds candidate e * FT + t in slot e, its z key in
+  // register ck[e] and its vocabulary index in S.cidx[e * FT + t] (LDS, read
+  // only by that thread: the index is needed for few candidates, and 16 more
+  // registers would cost the fused kernel a workgroup per CU).
   uint32_t ck[FCPT];
-  int32_t ci[FCPT];
+  auto ci = [&](int e) -> int32_t { return S.cidx[e * FT + tid]; };
   const int np = NC > tid ? min((NC - tid + FT - 1) / FT, FCPT) : 0;
   // The chunk of every slot's candidate by one binary search over pre[], its
   // steps interleaved over the slots (one LDS round trip per step), then all
@@ -713,7 +794,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       const bool pr = e < np;
       const float xv = key2f(pr ? cv[e].x : 0u);
       ck[e] = pr ? f2key(greedy ? xv : __fdiv_rn(xv, T)) : 0u;
-      ci[e] = pr ? (int32_t)cv[e].y : -1;
+      if (pr) S.cidx[e * FT + tid] = (int32_t)cv[e].y;
     }
   };
 
@@ -739,8 +820,9 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
 #pragma unroll
     for (int e = 0; e < FCPT; e++) {
       if (e < np && ck[e] >= zc) {
-        kl.skey[p] = ((uint64_t)ck[e] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)ci[e]);
-        kl.kidx[p] = ci[e];
+        const int32_t ix = ci(e);
+        kl.skey[p] = ((uint64_t)ck[e] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)ix);
+        kl.kidx[p] = ix;
         kl.km[p] = mass_fixed(mass_f(key2f(ck[e]), zmax));
         p++;
       }
@@ -872,7 +954,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       if (NC > FCAP) return 64;
       load_cands();
       LPS_FSTAMP(25);
-      auto cmass = [&](int e) -> uint64_t { return mass_fixed(mass_f(key2f(ck[e]), zmax)); };
+      auto cmass = [&](uint32_t key) -> uint64_t { return mass_fixed(mass_f(key2f(key), zmax)); };
       const uint64_t Af = (uint64_t)(Aabove * (double)kMassScale);
       const uint64_t Pf = (uint64_t)((double)topp * Zfull * (double)kMassScale);
       LPS_FSTAMP(16);
@@ -896,7 +978,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
         if (ttot > (uint32_t)KEPTCAP) return 32;
 #pragma unroll
         for (int e = 0; e < FCPT; e++)
-          if (e < np && ck[e] == vkey) kl.kidx[p++] = ci[e];
+          if (e < np && ck[e] == vkey) kl.kidx[p++] = ci(e);
         __syncthreads();
         LPS_FSTAMP(29);
         for (int i = tid; i < (int)ttot; i += FT) {
@@ -911,40 +993,39 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       __syncthreads();
       tie_lim = S.mi[25];
       LPS_FSTAMP(18);
-      if (tid == 0) {
+      if (wv == 0) {
         // the cut's division-collision group [xl, xh] = {x : fl(x / T) == cut},
-        // which must lie inside the region
+        // which must lie inside the region.  Lane l tests the step from l to
+        // l + 1 keys below (above) a candidate of the cut key; the group ends
+        // at the first failing lane, after at most 64 steps each way.
         const float xv = key2f(cand_at(S.mi[26]).x);
         const float zc = key2f(vkey);
-        float xl = xv, xh = xv;
-        bool ended = false;
-        for (int it = 0; it < 64 && !ended; it++) {
-          const uint32_t k = f2key(xl);
-          const float y = key2f(k - 1u);
-          if (k <= kNegInfKey + 1u || __fdiv_rn(y, T) != zc) ended = true;
-          else xl = y;
+        const uint32_t k0 = f2key(xv);
+        const uint32_t kd = k0 - (uint32_t)lane;
+        const uint64_t fd = wballot(!(kd > kNegInfKey + 1u && __fdiv_rn(key2f(kd - 1u), T) == zc));
+        const uint32_t ku = k0 + (uint32_t)lane;
+        const uint64_t fu = wballot(!(ku < 0xFFFFFFFEu && __fdiv_rn(key2f(ku + 1u), T) == zc));
+        if (lane == 0) {
+          const bool ended = fd != 0ull, ended2 = fu != 0ull;
+          const float xl = key2f(k0 - (ended ? (uint32_t)__builtin_ctzll(fd) : 64u));
+          const float xh = key2f(k0 + (ended2 ? (uint32_t)__builtin_ctzll(fu) : 64u));
+          const int bl = rbin(xl), bh = rbin(xh);
+          S.mi[27] = (ended && ended2 && bl >= blo && bh <= bhi) ? 1 : 0;
+          S.mf[0] = xl;
+          S.mf[1] = xh;
         }
-        bool ended2 = false;
-        for (int it = 0; it < 64 && !ended2; it++) {
-          const uint32_t k = f2key(xh);
-          const float y = key2f(k + 1u);
-          if (k >= 0xFFFFFFFEu || __fdiv_rn(y, T) != zc) ended2 = true;
-          else xh = y;
-        }
-        const int bl = wbin(xl, c), bh = wbin(xh, c);
-        S.mi[27] = (ended && ended2 && bl >= blo && bh <= bhi) ? 1 : 0;
-        S.mf[0] = xl;
-        S.mf[1] = xh;
       }
+      LPS_FSTAMP(14);
       // kept candidate mass per chunk and count (slot xg)
       uint32_t lc = 0;
 #pragma unroll
       for (int e = 0; e < FCPT; e++) {
-        const bool kept = e < np && (ck[e] > vkey || (ck[e] == vkey && ci[e] <= tie_lim));
+        const bool kept = e < np && (ck[e] > vkey || (ck[e] == vkey && ci(e) <= tie_lim));
         if (kept) {
-          const uint64_t m = cmass(e);
-          atomicAdd(&S.keptf[ci[e] / CH], (unsigned long long)m);
-          if ((int64_t)ci[e] == qtok) S.md[6] = (double)m / (double)kMassScale;
+          const int32_t ix = ci(e);
+          const uint64_t m = cmass(ck[e]);
+          atomicAdd(&S.keptf[ix / CH], (unsigned long long)m);
+          if ((int64_t)ix == qtok) S.md[6] = (double)m / (double)kMassScale;
           lc++;
         }
       }
@@ -1009,7 +1090,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
         if (yv == -INFINITY || yv != yv) return 0.0;
         const float w = __fmul_rn(yv, c);
         if (mode == MODE_NUCLEUS) {
-          const int b = (int)floorf(__fmul_rn(w, (float)HS));
+          const int b = (int)floorf(__fmul_rn(w, (float)(HS << rsub)));
           if (b < blo) return 0.0;
           if (b <= bhi) {
             if (yv < cxl || (yv <= cxh && lo2 + (v * FT + tid) * VEC + e > tie_lim)) return 0.0;
@@ -1107,7 +1188,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
       if (mode == MODE_PURE) {
         qprob = zq != -INFINITY ? (float)((double)mass_f(zq, zmax) / Zf) : 0.0f;
       } else {
-        const int bq = wbin(xq, c);
+        const int bq = rbin(xq);
         if (bq > bhi && zq != -INFINITY) qprob = (float)((double)mass_f(zq, zmax) / Zf);
         else if (qmass >= 0.0) qprob = (float)(qmass / Zf);
       }
@@ -1154,7 +1235,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
 
 // Split path, phase 1: grid of ceil(R / 8) * 8 * G workgroups.
 template <int DT, int VEC>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(FParams F) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(DT != LPS_DTYPE_F32 && VEC == 8 ? 5 : 4, 8))) void chunk_kernel(FParams F) {
   __shared__ CSharedT<32> S;
   const ChunkId c = chunk_id(F.G);
   if (c.r >= F.k.R) return;
@@ -1176,8 +1257,13 @@ __global__ __launch_bounds__(FT) void final_kernel(FParams F) {
 // Fused path (grids that fit on the GPU at once): the chunk kernel whose last
 // workgroup of each row to finish, counted by an L2 atomic, finalises the row
 // while other rows are still in their chunk phase.
+// Waves per SIMD the fused kernel is built for: four workgroups per CU for
+// 16-bit logits (<= 128 VGPRs, 37 KB LDS), three for fp32.
 #ifndef LPS_FUSED_WPE
-#define LPS_FUSED_WPE 3
+#define LPS_FUSED_WPE(DT) ((DT) == LPS_DTYPE_F32 ? 3 : 4)
+#endif
+#ifndef LPS_FUSED_PRIO
+#define LPS_FUSED_PRIO 0
 #endif
 #ifndef LPS_FUSED_NR16
 #define LPS_FUSED_NR16 32
@@ -1187,14 +1273,18 @@ __global__ __launch_bounds__(FT) void final_kernel(FParams F) {
 template <int DT>
 constexpr int fused_nr() { return DT == LPS_DTYPE_F32 ? 32 : LPS_FUSED_NR16; }
 template <int DT, int VEC>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WPE, 8))) void fused_kernel(FParams F) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WPE(DT), 8))) void fused_kernel(FParams F) {
   __shared__ union {
     CSharedT<fused_nr<DT>()> c;
     FSharedT<fused_nr<DT>()> f;
   } SU;
   ChunkId c = chunk_id(F.G);
   if (c.r >= F.k.R) return;
-  if (F.heavy_first) c.r = heavy_first_row(F.k, c.r);
+  bool heavy = false;
+  if (F.heavy_first) c.r = heavy_first_row(F.k, c.r, heavy);
+#if LPS_FUSED_PRIO
+  if (heavy) __builtin_amdgcn_s_setprio(2);
+#endif
   const int mode = chunk_body<DT, VEC, fused_nr<DT>()>(F, SU.c, c.r, c.j);
   if (mode == MODE_DEFER) {
     if (c.j == 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (1 << 8);
@@ -1206,6 +1296,9 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WP
   if (threadIdx.x == 0) SU.c.mi[5] = l2_fetch_add(F.counters + (int64_t)c.r * 32, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
   __syncthreads();
   if (!SU.c.mi[5]) return;
+#if LPS_FUSED_PRIO
+  __builtin_amdgcn_s_setprio(3);
+#endif
   const int reason = final_body<DT, VEC, fused_nr<DT>()>(F, SU.f, c.r, true);
   if (reason > 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (reason << 8);
 }
