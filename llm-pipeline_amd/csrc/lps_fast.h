@@ -60,7 +60,7 @@ constexpr int HS = 8;                   // bins per log2 unit
 constexpr int FB = 256;                 // nucleus level-2 fine bins (one per thread)
 constexpr int FSUB_MAX = 5;             // fine bins per coarse bin: at most 2^5
 #ifndef LPS_FINE_MIN
-#define LPS_FINE_MIN 1024               // level 2 runs when the coarse region may hold more elements
+#define LPS_FINE_MIN 2048               // level 2 runs when the coarse region may hold more elements
 #endif
 #ifndef LPS_SELD
 #define LPS_SELD 11

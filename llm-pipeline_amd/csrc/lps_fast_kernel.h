@@ -166,7 +166,7 @@ __device__ __forceinline__ ChunkId chunk_id(int G) {
 // pure: the longest finalisers) are dispatched first, so that their
 // finalisers overlap the chunk work of the rows dispatched after them.
 // Virtual row vr -> row; a bijection on [0, R), the same in every workgroup.
-__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr, bool& is_heavy) {
+__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr) {
   const int lane = threadIdx.x & 63;
   auto heavy = [&](int r) -> bool {
     if (r >= P.R) return false;
@@ -178,7 +178,6 @@ __device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr, b
   const uint64_t v1 = wballot(lane < P.R), v2 = wballot(lane + 64 < P.R);
   const int nh = __popcll(m1) + __popcll(m2);
   const bool hv = vr < nh;
-  is_heavy = hv;
   const uint64_t a = hv ? m1 : (v1 & ~m1), b = hv ? m2 : (v2 & ~m2);
   const int k = hv ? vr : vr - nh;
   const int pa = __popcll(a);
@@ -1099,6 +1098,27 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
         }
         return (double)chunk_mass(w, wmj) * scj;
       };
+      // kept_m with its per-element branches turned into selects and one
+      // wave-uniform branch around the region formula (every lane calls it):
+      // the same values, without divergent control flow per element.
+      auto kept_m_all = [&](int v, int e) -> double {
+        const float yv = Y.template val<true>(v * VEC + e, pa2);
+        const bool live = yv != -INFINITY && yv == yv;
+        const float yl = live ? yv : 0.0f;
+        const float w = __fmul_rn(yl, c);
+        double m = (double)chunk_mass(w, wmj) * scj;
+        if (mode == MODE_NUCLEUS) {
+          const int b = (int)floorf(__fmul_rn(w, (float)(HS << rsub)));
+          const bool inr = b >= blo && b <= bhi;
+          m = b < blo ? 0.0 : m;
+          if (wballot(live && inr)) {
+            const bool kept = !(yl < cxl || (yl <= cxh && lo2 + (v * FT + tid) * VEC + e > tie_lim));
+            const double mr = (double)mass_fixed(mass_f(__fdiv_rn(yl, T), zmax)) / (double)kMassScale;
+            m = inr ? (kept ? mr : 0.0) : m;
+          }
+        }
+        return live ? m : 0.0;
+      };
       // Vocabulary order is (v, thread, e).  Groups are scanned in batches of NB;
       // each thread keeps its first group whose cumulative end passes the target
       // (slots xv, then xc xf).
@@ -1112,7 +1132,7 @@ __device__ __forceinline__ int final_body(const FParams& F, FSharedT<NR>& S, con
         for (int b = 0; b < NB; b++) {
           double a = 0.0;
 #pragma unroll
-          for (int e = 0; e < VEC; e++) a += kept_m(vb + b, e);
+          for (int e = 0; e < VEC; e++) a += kept_m_all(vb + b, e);
           sv[b] = a;
           incv[b] = wscan_incl(a);
         }
@@ -1262,9 +1282,6 @@ __global__ __launch_bounds__(FT) void final_kernel(FParams F) {
 #ifndef LPS_FUSED_WPE
 #define LPS_FUSED_WPE(DT) ((DT) == LPS_DTYPE_F32 ? 3 : 4)
 #endif
-#ifndef LPS_FUSED_PRIO
-#define LPS_FUSED_PRIO 0
-#endif
 #ifndef LPS_FUSED_NR16
 #define LPS_FUSED_NR16 32
 #endif
@@ -1280,11 +1297,7 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WP
   } SU;
   ChunkId c = chunk_id(F.G);
   if (c.r >= F.k.R) return;
-  bool heavy = false;
-  if (F.heavy_first) c.r = heavy_first_row(F.k, c.r, heavy);
-#if LPS_FUSED_PRIO
-  if (heavy) __builtin_amdgcn_s_setprio(2);
-#endif
+  if (F.heavy_first) c.r = heavy_first_row(F.k, c.r);
   const int mode = chunk_body<DT, VEC, fused_nr<DT>()>(F, SU.c, c.r, c.j);
   if (mode == MODE_DEFER) {
     if (c.j == 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (1 << 8);
@@ -1296,9 +1309,6 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(LPS_FUSED_WP
   if (threadIdx.x == 0) SU.c.mi[5] = l2_fetch_add(F.counters + (int64_t)c.r * 32, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
   __syncthreads();
   if (!SU.c.mi[5]) return;
-#if LPS_FUSED_PRIO
-  __builtin_amdgcn_s_setprio(3);
-#endif
   const int reason = final_body<DT, VEC, fused_nr<DT>()>(F, SU.f, c.r, true);
   if (reason > 0 && threadIdx.x == 0) F.status[c.r] = LPS_ROW_DEFERRED | (reason << 8);
 }
