@@ -88,15 +88,18 @@ FastWs fast_layout(void* base, int R, int V) {
   return w;
 }
 
-// Grids of at most this many chunk workgroups take the fused kernel (three
-// workgroups per CU: row finalisers overlap other rows' chunk work).  Larger
-// grids take the split pair (five chunk workgroups per CU, then one finaliser
-// workgroup per row).
+// Grids of at most this many chunk workgroups take the fused kernel (four
+// workgroups per CU for 16-bit logits, three for fp32: row finalisers overlap
+// other rows' chunk work).  Larger grids take the split pair (five chunk
+// workgroups per CU, then one finaliser workgroup per row).
 #ifndef LPS_FUSED_MAX_WG
 #define LPS_FUSED_MAX_WG 2048
 #endif
-// Fused grids above one resident wave (three workgroups per CU) reorder rows
-// so that the longest finalisers start first.
+// Fused grids above this many workgroups reorder rows so that the longest
+// finalisers start first.  768 is one resident wave at three workgroups per
+// CU; at four (16-bit logits) a wave holds 1024, and grids between the two
+// are reordered too, which measured neutral (the reorder only moves rows
+// without top-k to the front).
 #ifndef LPS_HEAVY_FIRST_WG
 #define LPS_HEAVY_FIRST_WG 768
 #endif

@@ -130,6 +130,9 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   g.qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
                ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
                : -1;
+  // a query id outside the vocabulary has probability 0 (as verify_drafts_kernel
+  // treats it); no logit is read for it
+  if (g.qtok >= (int64_t)P.V) g.qtok = -1;
   if (g.topp != g.topp) g.topp = 1.0f;
   g.greedy = !(g.T > 0.0f);
   g.ntop = (P.n_top > 0 && P.top_logprobs) ? P.n_top : 0;
@@ -1285,8 +1288,8 @@ __global__ __launch_bounds__(FT) void final_kernel(FParams F) {
 #ifndef LPS_FUSED_NR16
 #define LPS_FUSED_NR16 32
 #endif
-// Logit registers per thread of the fused kernel: 16384-logit chunks for
-// 16-bit logits (read as 16 bytes = 8 logits per load), 8192 for fp32.
+// Logit registers per thread of the fused kernel: 32, i.e. 8192-logit chunks
+// for every dtype (16-bit logits are read 8 per 16-byte load and held as fp32).
 template <int DT>
 constexpr int fused_nr() { return DT == LPS_DTYPE_F32 ? 32 : LPS_FUSED_NR16; }
 template <int DT, int VEC>

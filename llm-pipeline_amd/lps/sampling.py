@@ -64,7 +64,7 @@ class Sampler:
                      generated_tokens: Optional[List[int]] = None, *, uniforms: Optional[torch.Tensor] = None,
                      params: Optional[SamplingParams] = None, histories: Optional[torch.Tensor] = None,
                      history_lengths: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
-                     allowed: Optional[torch.Tensor] = None, strict: bool = True) -> torch.Tensor:
+                     allowed: Optional[torch.Tensor] = None, strict: Optional[bool] = None) -> torch.Tensor:
         """Sample next token ids ``int64 [B]`` from ``logits [B, V]``.
 
         As in the reference, ``generated_tokens`` is one history applied to
@@ -75,9 +75,16 @@ class Sampler:
         [0, 1)) drive the inverse-CDF draw; when omitted they come from
         ``torch.rand`` on the logits' device.  ``allowed`` (bool ``[B, V]`` or
         packed ``int32`` bits) masks illegal ids to -inf, as a reference
-        ``LogitConstraint`` applied to the logits first would.  ``strict``
-        raises the reference's errors (it synchronises once to read the row
-        status)."""
+        ``LogitConstraint`` applied to the logits first would.
+
+        ``strict`` raises the reference's ``RuntimeError`` for rows
+        ``torch.multinomial`` would reject (NaN / +inf / all -inf); reading the
+        row status synchronises the stream once, as the engine's ``.item()``
+        after every call does anyway (``qwen3_engine.py:412-420``).  The
+        default (``None``) checks unless the stream is being captured into a
+        graph, where the call stays stream-ordered; ``False`` never checks
+        (tokens of rejected rows are -1 and ``last_output.status`` holds the
+        reason)."""
         config = self._merge_config(config_override)
         D.require_device(logits, "logits")
         if logits.dim() != 2:
@@ -97,6 +104,8 @@ class Sampler:
                           logprobs=bool(config.logprobs), top_logprobs=int(config.top_logprobs),
                           generator=generator, allowed=allowed)
         self.last_output = out
+        if strict is None:
+            strict = not torch.cuda.is_current_stream_capturing()
         if strict:
             raise_on_status(out.status)
         return out.tokens
@@ -129,6 +138,8 @@ class Sampler:
             previous_entropy = current
         previous_entropy -= config.mirostat_eta * (current - config.mirostat_tau)
         k = max(1, int(math.exp(previous_entropy))) if previous_entropy > 0 else 0
+        # the reference's _apply_top_k clamps k to the vocabulary (sampling.py:151)
+        k = min(k, logits.shape[-1])
         out = sample_rows(logits, SamplingParams.build(B, dev, temperature=T, top_k=k), uniforms)
         raise_on_status(out.status)
         return out.tokens, previous_entropy

@@ -94,7 +94,8 @@ def test_mask_split_kernels(dev):
     a = PY.run_workload(w, dev, allowed=m.to(dev))
     b = PY.run_workload(wm, dev)
     _same(a, b, "c2 B=128 split")
-    PY.check_rows(wm, a, rows=range(8))
+    rep = PY.check_rows(wm, a)
+    print(f"c2 B=128 masked: {rep}", flush=True)
 
 
 def test_mask_packed_bits_and_query(dev):

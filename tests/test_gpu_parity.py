@@ -34,12 +34,17 @@ def test_c2_mixed_params_bf16_full_size(dev):
     _print(f"c2: {rep}")
 
 
+@pytest.mark.parametrize("B", [16, 256])
 @pytest.mark.parametrize("flat", [False, True])
-def test_c3_nucleus_fp32(dev, flat):
-    w = W.c3(B=16, flat=flat)
+def test_c3_nucleus_fp32(dev, flat, B):
+    """c3 at B=16 and at its own size B=256 (the launch shape of the benchmark),
+    every row against the oracle's top-p rule (sampling.py:158-185)."""
+    w = W.c3(B=B, flat=flat)
     out = PY.run_workload(w, dev)
     rep = PY.check_rows(w, out)
-    _print(f"c3 flat={flat}: {rep} kept_counts={out.kept_count.cpu().tolist()[:6]}")
+    nfast = int((out.row_path.cpu() == 0).sum())
+    _print(f"c3 flat={flat} B={B}: {rep}; fast-path rows {nfast}/{B}; "
+           f"kept_counts={out.kept_count.cpu().tolist()[:6]}")
 
 
 def test_c5_logprobs_fp16_subset(dev):
@@ -207,15 +212,49 @@ def test_sampler_drop_in_matches_oracle(dev):
         assert int(tg[i]) == O.sample_row(x[i], O.RowParams(0.0, repetition_penalty=1.2), hist).token
 
 
+def _mirostat_kept(x_row, T, k):
+    z = (x_row.float() / T).reshape(1, -1)
+    return O.apply_top_k(z, k).reshape(-1) if k > 0 else z.reshape(-1)
+
+
 def test_mirostat_entropy(dev):
+    """sampling.py:240-279: the entropy update and the drawn token, against
+    mirostat_v2_ref (the token through its interval of the kept-set CDF)."""
     from lps import Sampler
     g = torch.Generator().manual_seed(15)
     x = torch.randn((1, 2000), generator=g) * 2
     s = Sampler()
-    tok, prev = s.sample_mirostat_v2(x.to(dev), {"temperature": 0.9}, None, uniforms=torch.tensor([0.3], device=dev))
-    ref_tok, ref_prev, k = O.mirostat_v2_ref(x[0], 0.9, 5.0, 0.1, None, 0.3)
-    assert abs(prev - ref_prev) < 1e-4
-    assert 0 <= int(tok) < 2000
+    for u in (0.3, 0.01, 0.97):
+        tok, prev = s.sample_mirostat_v2(x.to(dev), {"temperature": 0.9}, None, uniforms=torch.tensor([u], device=dev))
+        ref_tok, ref_prev, k = O.mirostat_v2_ref(x[0], 0.9, 5.0, 0.1, None, u)
+        assert abs(prev - ref_prev) < 1e-4
+        z = _mirostat_kept(x[0], 0.9, k)
+        kept = torch.isfinite(z).numpy()
+        assert PY.draw_ok(z, kept, u, int(tok)), (u, int(tok), ref_tok, k)
+
+
+def test_mirostat_long_low_entropy_loop(dev):
+    """A peaked row (entropy below tau) makes prev grow every step, so
+    k = int(exp(prev)) passes the vocabulary size; the reference's top-k
+    clamps it (sampling.py:151) and sampling goes on.  60 steps against the
+    oracle, token by token through the CDF interval."""
+    from lps import Sampler
+    g = torch.Generator().manual_seed(16)
+    V = 500
+    x = torch.randn((1, V), generator=g) * 6
+    s = Sampler()
+    prev = rprev = None
+    ks = []
+    for step in range(60):
+        u = float(torch.rand((), generator=g))
+        tok, prev = s.sample_mirostat_v2(x.to(dev), {"temperature": 1.0, "mirostat_eta": 0.5}, prev,
+                                         uniforms=torch.tensor([u], device=dev))
+        _, rprev, k = O.mirostat_v2_ref(x[0], 1.0, 5.0, 0.5, rprev, u)
+        assert abs(prev - rprev) < 1e-3 * max(1.0, abs(rprev)), (step, prev, rprev)
+        z = _mirostat_kept(x[0], 1.0, min(k, V))
+        assert PY.draw_ok(z, torch.isfinite(z).numpy(), u, int(tok)), (step, int(tok), k)
+        ks.append(k)
+    assert max(ks) > V
 
 
 # ------------------------------------------------------------ speculative --
@@ -294,9 +333,23 @@ def test_spec_verify_greedy_and_leviathan(dev):
     _check_spec(sw, out, residual="leviathan")
     tok = out.tokens.cpu()
     n = out.n_accepted.cpu()
+    n_ref, tok_ref, _, _, _ = O.spec_verify_ref(sw.target, sw.draft, sw.draft_tokens, sw.u_accept, sw.u_resample,
+                                                1.0, 0.9, "leviathan")
+    checked = 0
     for b in range(8):
         j = int(n[b])
         if j < 4:
             tp = O.spec_probs_row(sw.target[b, j], 1.0, 0.9).double()
             dp = O.spec_probs_row(sw.draft[b, j], 1.0, 0.9).double()
-            assert float(tp[int(tok[b, j])] - dp[int(tok[b, j])]) > -1e-6   # drawn where p > q
+            t = int(tok[b, j])
+            assert float(tp[t] - dp[t]) > -1e-6   # drawn where p > q
+            if j == int(n_ref[b]):
+                # the draw against the oracle's residual law norm(max(p - q, 0)),
+                # through its CDF interval in vocabulary order
+                r = torch.clamp(tp - dp, min=0.0)
+                cum = torch.cumsum(r, 0) / r.sum()
+                lo = float(cum[t - 1]) if t > 0 else 0.0
+                u = float(sw.u_resample[b, j])
+                assert lo - 1e-6 <= u < float(cum[t]) + 1e-6, (b, j, t, int(tok_ref[b, j]), u)
+                checked += 1
+    assert checked > 0

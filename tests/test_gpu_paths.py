@@ -37,10 +37,14 @@ def test_paths_c1(dev):
         assert nfast == 1
 
 
+@pytest.mark.parametrize("B", [16, 256])
 @pytest.mark.parametrize("flat", [False, True])
-def test_paths_c3(dev, flat):
-    w = W.c3(B=16, flat=flat)
-    _paths(w, dev)
+def test_paths_c3(dev, flat, B):
+    """c3 (and its flat variant) stays on the fast path: at B=256 this is the
+    launch shape the benchmark times."""
+    w = W.c3(B=B, flat=flat)
+    fast, gen, nfast = _paths(w, dev)
+    assert nfast == w.B
 
 
 def test_paths_c5(dev):

@@ -9,8 +9,28 @@ import pytest
 import torch
 
 from lps import SamplerState, SamplingParams, pad_histories, sample_rows
+from tests import parity as PY
+from tests import workloads as W
 
 pytestmark = pytest.mark.gpu
+
+
+def _oracle_step(x, kws, st, host, u, out):
+    """Every row of one batcher step against the oracle's sample_row on the
+    host-kept histories (continuous_batching.py:394-404: one
+    sample_token(logits[i:i+1], kwargs_i) per row, generated_tokens as the
+    history, sampling.py:125)."""
+    n = len(kws)
+    cfgs = [st.config_for(k) for k in kws]
+    col = lambda f, dt=torch.float32: torch.tensor([getattr(c, f) for c in cfgs], dtype=dt)
+    H = max(1, max(len(h) for h in host))
+    hist = torch.zeros((n, H), dtype=torch.int32)
+    for i, h in enumerate(host):
+        hist[i, :len(h)] = torch.tensor(h, dtype=torch.int32)
+    w = W.Workload("state", x.cpu(), col("temperature"), col("top_k", torch.int32), col("top_p"), col("min_p"),
+                   col("typical_p"), col("repetition_penalty"), col("presence_penalty"), col("frequency_penalty"),
+                   hist, torch.tensor([len(h) for h in host], dtype=torch.int32), u.cpu())
+    return PY.check_rows(w, out)
 
 
 def _kwargs(B, seed):
@@ -53,7 +73,9 @@ def test_state_steps_equal_host_loop(dev, path):
         x[:, :200] += 4.0                           # the history ids are likely picks
         x = x.to(dev)
         u = torch.rand((n,), generator=g).to(dev)
-        out = st.sample(x, u, path=path)
+        out = st.sample(x, u, path=path, kept_set=True)
+        rep = _oracle_step(x, kws, st, host, u, out)
+        print(f"step {s} ({path}): {rep}", flush=True)
         hist, hl = pad_histories(host, dev)
         ref = sample_rows(x, _params(st, kws, dev), u, histories=hist, history_lengths=hl, path=path)
         torch.cuda.synchronize(dev)

@@ -370,3 +370,92 @@ def test_top_p_reference_cum_invariants():
     assert np.all(np.diff(ref) >= 0)                        # descending order gives a non-decreasing prefix
     assert np.max(np.abs(ref - excl)) < 4000 * 2.0 ** -24   # fp32 accumulation of the fp64 truth
     assert np.max(np.abs(ref - excl)) > 0                   # and it is the fp32 one, not the truth
+
+
+def test_top_p_band_known_cases():
+    # four equal masses: exclusive prefixes 0, 1/4, 1/2, 3/4 in stable order
+    z = torch.zeros(4)
+    _, excl, n = O.top_p_truth(z, 0.5)
+    assert n == 3 and np.allclose(excl, [0.0, 0.25, 0.5, 0.75])
+    # counts 2 and 3 differ only at position 2, whose prefix is exactly top_p
+    assert O.top_p_band(z, 0.5, 3, 2, 2e-6)
+    assert O.top_p_band(z, 0.5 + 1e-6, 2, 3, 2e-6)
+    assert not O.top_p_band(z, 0.5 + 1e-5, 2, 3, 2e-6)
+    # counts 3 and 4 differ at position 3 (prefix 3/4, far from 0.5)
+    assert not O.top_p_band(z, 0.5, 3, 4, 2e-6)
+    # a span of two positions is in the band only if both are
+    assert not O.top_p_band(z, 0.5, 2, 4, 2e-6)
+    assert O.top_p_band(z, 0.5, 3, 3, 0.0)
+
+
+def test_top_p_reference_rounding_known_cases():
+    # three equal masses: fp32 softmax rounds 1/3 up to 0.33333334, so the
+    # reference's prefix at position 1 lies above the fp64 truth 1/3
+    z = torch.zeros(3)
+    ref = O.top_p_reference_cum(z)
+    _, excl, n_truth = O.top_p_truth(z, 1.0 / 3.0)
+    assert n_truth == 2
+    assert ref[1] > excl[1] and abs(ref[1] - excl[1]) < 1e-7
+    # with top_p = 1/3 the reference's fp32 compare drops position 1 (count 1);
+    # the difference is explained by its rounding, even with no slack
+    assert O.top_p_reference_rounding(z, 1.0 / 3.0, 2, 1, eps=0.0)
+    # at top_p = 0.3 position 1 is 0.033 away from top_p: not rounding
+    assert not O.top_p_reference_rounding(z, 0.3, 2, 1, eps=0.0)
+    # equal counts are always explained
+    assert O.top_p_reference_rounding(z, 0.3, 1, 1, eps=0.0)
+
+
+def _lev_case():
+    tgt = torch.tensor([[[1.0, 0.2, -0.5, 0.9], [0.0, 0.0, 0.0, 0.0]]])
+    drf = torch.tensor([[[0.1, 1.5, -0.2, 0.3]]])
+    return tgt, drf
+
+
+def test_leviathan_residual_brute_force():
+    """speculative.py:150-157 computes the textbook residual max(p - q, 0) (and
+    then resamples the target instead); the oracle's "leviathan" branch draws
+    from the normalised residual by inverse CDF in vocabulary order."""
+    tgt, drf = _lev_case()
+    p = torch.softmax(tgt[0, 0].double(), -1)
+    q = torch.softmax(drf[0, 0].double(), -1)
+    t = int(torch.argmax(q - p))                       # q > p there: a likely reject
+    r = [max(float(p[i] - q[i]), 0.0) for i in range(4)]
+    for u in np.linspace(0.0, 0.999, 41):
+        # brute force: walk the ids, accumulating the residual
+        acc, want = 0.0, None
+        for i in range(4):
+            acc += r[i] / sum(r)
+            if want is None and u < acc:
+                want = i
+        n, tok, bits, _, _ = O.spec_verify_ref(tgt, drf, torch.tensor([[t]]), torch.tensor([[0.9999]]),
+                                               torch.tensor([[float(u), 0.5]]), 1.0, 1.0, "leviathan")
+        assert int(n[0]) == 0 and int(bits[0, 0]) == 0
+        assert int(tok[0, 0]) == want, (u, int(tok[0, 0]), want)
+        assert r[int(tok[0, 0])] > 0.0
+
+
+def test_leviathan_first_token_law_is_target():
+    """Speculative sampling with the residual max(p - q, 0) emits its first
+    token with the target law p exactly (Leviathan et al. 2023, Theorem 1).
+    The oracle's accept rule and residual branch, integrated over the draft
+    token and both uniforms on a fine grid, must give p."""
+    tgt, drf = _lev_case()
+    p = torch.softmax(tgt[0, 0], -1).double().numpy()
+    q = torch.softmax(drf[0, 0], -1).double().numpy()
+    grid = (np.arange(400) + 0.5) / 400
+    law = np.zeros(4)
+    for t in range(4):
+        n_acc = 0
+        for ua in grid:
+            n, tok, bits, _, _ = O.spec_verify_ref(tgt, drf, torch.tensor([[t]]), torch.tensor([[float(ua)]]),
+                                                   torch.tensor([[0.5, 0.5]]), 1.0, 1.0, "leviathan")
+            n_acc += int(n[0])
+        acc = n_acc / grid.size
+        law[t] += q[t] * acc
+        res = np.zeros(4)
+        for ur in grid:
+            _, tok, _, _, _ = O.spec_verify_ref(tgt, drf, torch.tensor([[t]]), torch.tensor([[1.0]]),
+                                                torch.tensor([[float(ur), 0.5]]), 1.0, 1.0, "leviathan")
+            res[int(tok[0, 0])] += 1.0 / grid.size
+        law += q[t] * (1.0 - acc) * res
+    assert np.abs(law - p).max() < 6e-3, (law, p)
