@@ -117,8 +117,11 @@ typedef struct lps_sample_args {
   int64_t history_stride;
   const int32_t* history_len;
 
-  /* uniforms in [0, 1), float32 [R]: the inverse-CDF draw of sampling rows.
-   * Required when any row samples (temperature > 0). */
+  /* uniforms in [0, 1), float32 [R]: the inverse-CDF draw of sampling rows,
+   * over the kept ids in sorted order (scaled logit descending, ties lower
+   * index first): the token is the first id whose cumulative kept mass
+   * exceeds u times the total.  Required when any row samples
+   * (temperature > 0). */
   const float* uniforms;
 
   /* optional query tokens: query_prob[r] = probability of the query token

@@ -3,7 +3,7 @@
 // mutable state.
 #include <hip/hip_runtime.h>
 
-#include "lps_fast_kernel.h"
+#include "lps_rowgroup.h"
 #include "lps_generic.h"
 #include "lps_lmhead.h"
 #include "lps_softmax.h"
@@ -44,97 +44,90 @@ bool dtype_ok(int d) { return d == LPS_DTYPE_F32 || d == LPS_DTYPE_BF16 || d == 
 
 size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
-// Fast-path workspace: per-row counters, row status, chunk summaries,
-// histograms and candidates, every row's region a whole number of 128-byte
-// lines.
-struct FastWs {
+// Row-group workspace: per-row counters (a fixed region at offset 0, so a
+// workspace reused for any (rows, vocab) keeps them apart from the data; they
+// are zero between launches: every launch leaves them zero), row status, chunk
+// summaries, histogram exchange and candidates.
+struct RgWs {
   uint32_t* counters;
   int32_t* status;
-  ChunkSum1* sum1;
-  ChunkSum2* sum2;
+  rg::RgSum* sums;
   float* hist;
   uint2* cands;
-  int64_t s_stride, h_stride, c_stride;
   size_t bytes;
 };
 
-// Rows per fast launch; larger batches are split.  The counter region has this
-// fixed size at offset 0, so a workspace reused for any (rows, vocab) keeps its
-// counters apart from the data regions (the counters must stay zero between
-// launches; every launch leaves them zero).
-constexpr int FAST_MAX_ROWS = 8192;
+// Rows per row-group launch; larger batches are split into launches.
+constexpr int RG_MAX_ROWS = 1024;
 
-FastWs fast_layout(void* base, int R, int V) {
-  FastWs w{};
-  const int G = (V + FCH_MIN - 1) / FCH_MIN;  // the most chunks any dtype uses
-  if (R > FAST_MAX_ROWS) R = FAST_MAX_ROWS;
-  w.s_stride = (int64_t)round_up((size_t)G, 4);                      // 4 x 32 B = one 128 B line
-  w.h_stride = (int64_t)round_up((size_t)G * (HB + FB), 32);         // floats
-  // candidates: G chunks of PUB slots, for either chunk variant
-  constexpr int NR2 = fused_nr<LPS_DTYPE_BF16>();
-  const int G2 = (V + FT * NR2 - 1) / (FT * NR2);
-  const int64_t c32 = (int64_t)G * Chunk<LPS_DTYPE_F32, 1, 32>::PUB;
-  const int64_t c2 = (int64_t)G2 * Chunk<LPS_DTYPE_BF16, 1, NR2>::PUB;
-  w.c_stride = c32 > c2 ? c32 : c2;                                  // uint2, multiple of 16
+// Launch shape of the row-group kernel for a batch: logits per thread (NE) of
+// the instantiated variants, chunks per row (G <= MAXG), vectors per chunk.
+struct RgPlan {
+  int vpe, ne, G, cv, nvec, capw;
+  bool ok;
+};
+RgPlan rg_plan(int dtype, bool vec, int R, int V) {
+  RgPlan p{};
+  p.vpe = !vec ? 1 : (dtype == LPS_DTYPE_F32 ? 4 : 8);
+  p.nvec = V / p.vpe;
+  auto chunks = [&](int ne) { return (p.nvec + rg::NT * (ne / p.vpe) - 1) / (rg::NT * (ne / p.vpe)); };
+  // fp32 rows of small batches: 24 logits per thread, so a row spreads over
+  // more workgroups (latency); rows read element by element: 40; otherwise 80
+  p.ne = p.vpe == 1 ? 40 : ((p.vpe == 4 && R <= 16 && chunks(24) <= rg::MAXG) ? 24 : 80);
+  p.G = chunks(p.ne);
+  p.ok = p.G >= 1 && p.G <= rg::MAXG && V >= 1;
+  p.cv = p.ok ? (p.nvec + p.G - 1) / p.G : 1;
+  p.capw = p.ok ? (rg::CAPR / p.G) / rg::NW * rg::NW : 0;
+  return p;
+}
+// The most chunks any dtype's plan uses for (R, V): sizes the workspace.
+int rg_max_chunks(int R, int V) {
+  int g = 1;
+  for (int d = 0; d < 2; d++)
+    for (int v = 0; v < 2; v++) {
+      const RgPlan p = rg_plan(d == 0 ? LPS_DTYPE_F32 : LPS_DTYPE_BF16, v == 1, R, V);
+      if (p.ok && p.G > g) g = p.G;
+    }
+  return g;
+}
+
+RgWs rg_layout(void* base, int R, int V) {
+  RgWs w{};
+  if (R > RG_MAX_ROWS) R = RG_MAX_ROWS;
+  const int G = rg_max_chunks(R, V);
   size_t off = 0;
   char* p = reinterpret_cast<char*>(base);
-  w.counters = reinterpret_cast<uint32_t*>(p + off); off = (size_t)FAST_MAX_ROWS * 128;
+  w.counters = reinterpret_cast<uint32_t*>(p + off); off = (size_t)RG_MAX_ROWS * 128;
   w.status = reinterpret_cast<int32_t*>(p + off); off = round_up(off + (size_t)R * 4, 256);
-  w.sum1 = reinterpret_cast<ChunkSum1*>(p + off); off = round_up(off + (size_t)R * w.s_stride * sizeof(ChunkSum1), 256);
-  w.sum2 = reinterpret_cast<ChunkSum2*>(p + off); off = round_up(off + (size_t)R * w.s_stride * sizeof(ChunkSum2), 256);
-  w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * w.h_stride * 4, 256);
-  w.cands = reinterpret_cast<uint2*>(p + off); off = round_up(off + (size_t)R * w.c_stride * 8, 256);
+  w.sums = reinterpret_cast<rg::RgSum*>(p + off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
+  w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
+  w.cands = reinterpret_cast<uint2*>(p + off); off = round_up(off + (size_t)R * rg::CAPR * 8, 256);
   w.bytes = off;
   return w;
 }
 
-// Grids of at most this many chunk workgroups take the fused kernel (four
-// workgroups per CU for 16-bit logits, three for fp32: row finalisers overlap
-// other rows' chunk work).  Larger grids take the split pair (five chunk
-// workgroups per CU, then one finaliser workgroup per row).
-#ifndef LPS_FUSED_MAX_WG
-#define LPS_FUSED_MAX_WG 2048
-#endif
-// Fused grids above this many workgroups reorder rows so that the longest
-// finalisers start first.  768 is one resident wave at three workgroups per
-// CU; at four (16-bit logits) a wave holds 1024, and grids between the two
-// are reordered too, which measured neutral (the reorder only moves rows
-// without top-k to the front).
-#ifndef LPS_HEAVY_FIRST_WG
-#define LPS_HEAVY_FIRST_WG 768
-#endif
-
-template <int DT, int VEC>
-hipError_t launch_fast(FParams F, int rows_pad, bool fused, hipStream_t s) {
-  hipError_t e;
-  if (VEC > 1 && fused) {
-    if constexpr (VEC > 1) hipLaunchKernelGGL((fused_kernel<DT, VEC>), dim3((unsigned)(rows_pad * F.G)), dim3(FT), 0, s, F);
-    e = hipGetLastError();
-  } else {
-    const unsigned grid = (unsigned)(rows_pad * F.G);
-    hipLaunchKernelGGL((chunk_kernel<DT, VEC>), dim3(grid), dim3(FT), 0, s, F);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((final_kernel<DT, VEC>), dim3((unsigned)F.k.R), dim3(FT), 0, s, F);
-    e = hipGetLastError();
-  }
+template <int DT, int VPE, int NE>
+hipError_t launch_rg(const rg::RgParams& F, hipStream_t s) {
+  const unsigned grid = (unsigned)((F.k.R + 7) / 8 * 8 * F.G);
+  hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // rows the finaliser deferred: the general algorithm, one 1024-thread
+  // rows the row-group kernel deferred: the general algorithm, one 1024-thread
   // workgroup per row (the others return at once)
   KParams G = F.k;
   G.only_status = F.status;
   G.plans = nullptr;
-  return launch_gen<DT, VEC>(G, s);
+  return launch_gen<DT, VPE == 1 ? 1 : (DT == LPS_DTYPE_F32 ? 4 : 8)>(G, s);
 }
 
-hipError_t dispatch_fast(int dtype, bool vec, const FParams& F, int rows_pad, bool fused, hipStream_t s) {
-  switch (dtype) {
-    case LPS_DTYPE_F32:
-      return vec ? launch_fast<LPS_DTYPE_F32, 4>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_F32, 1>(F, rows_pad, false, s);
-    case LPS_DTYPE_BF16:
-      return vec ? launch_fast<LPS_DTYPE_BF16, 8>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_BF16, 1>(F, rows_pad, false, s);
-    default:
-      return vec ? launch_fast<LPS_DTYPE_F16, 8>(F, rows_pad, fused, s) : launch_fast<LPS_DTYPE_F16, 1>(F, rows_pad, false, s);
+template <int DT>
+hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, hipStream_t s) {
+  if (p.vpe == 1) return launch_rg<DT, 1, 40>(F, s);
+  if constexpr (DT == LPS_DTYPE_F32) {
+    if (p.ne == 24) return launch_rg<DT, 4, 24>(F, s);
+    return launch_rg<DT, 4, 80>(F, s);
+  } else {
+    return launch_rg<DT, 8, 80>(F, s);
   }
 }
 
@@ -167,44 +160,48 @@ KParams row_block(const KParams& P, int r0, int nr, int es) {
   return B;
 }
 
-// Runs the fast kernels (rows they cannot finish exactly go to the general
-// kernel launched after them), or only the general kernel when asked or
-// without workspace.
-hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws_bytes, int flags, hipStream_t s) {
-  const FastWs need = fast_layout(nullptr, P.R, P.V);
+// Runs the row-group kernel (rows it cannot finish exactly go to the general
+// kernel launched after it), or only the general kernel when asked or without
+// workspace.
+// plan_rows: the batch size the launch shape is planned for (the whole batch,
+// also for its blocks when it is split, so that every block fits the
+// workspace sized for it); 0 = P.R.
+hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws_bytes, int flags, hipStream_t s,
+                      int plan_rows = 0) {
+  if (plan_rows <= 0) plan_rows = P.R;
+  const RgWs need = rg_layout(nullptr, plan_rows, P.V);
   if ((flags & LPS_FLAG_GENERIC) || !ws || ws_bytes < need.bytes) return dispatch_gen(dtype, vec, P, s);
-  if (P.R > FAST_MAX_ROWS) {
-    const int blk = FAST_MAX_ROWS / P.rows_inner * P.rows_inner;
+  if (P.R > RG_MAX_ROWS) {
+    const int blk = RG_MAX_ROWS / P.rows_inner * P.rows_inner;
+    if (blk < 1) return dispatch_gen(dtype, vec, P, s);
     const int es = dtype == LPS_DTYPE_F32 ? 4 : 2;
     for (int r0 = 0; r0 < P.R; r0 += blk) {
       const int nr = P.R - r0 < blk ? P.R - r0 : blk;
-      hipError_t e = run_sample(row_block(P, r0, nr, es), dtype, vec, ws, ws_bytes, flags, s);
+      hipError_t e = run_sample(row_block(P, r0, nr, es), dtype, vec, ws, ws_bytes, flags, s, plan_rows);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
   }
-  const FastWs w = fast_layout(ws, P.R, P.V);
-  FParams F{};
+  const RgPlan p = rg_plan(dtype, vec, plan_rows, P.V);
+  if (!p.ok) return dispatch_gen(dtype, vec, P, s);
+  const RgWs w = rg_layout(ws, plan_rows, P.V);
+  rg::RgParams F{};
   F.k = P;
-  const int rows_pad = (P.R + 7) / 8 * 8;
-  // chunk size of the kernel variant: FT * (logit registers per thread); the
-  // split kernel's 16-bit rows read in 16-byte vectors take 16384 when packed
-  // two per register
-  const int chf = FT * (dtype == LPS_DTYPE_F32 ? fused_nr<LPS_DTYPE_F32>() : fused_nr<LPS_DTYPE_BF16>());
-  const bool fused = vec && (int64_t)rows_pad * ((P.V + chf - 1) / chf) <= LPS_FUSED_MAX_WG;
-  const int ch = fused ? chf : (LPS_PACK16 && dtype != LPS_DTYPE_F32 && vec) ? 2 * FCH_MIN : FCH_MIN;
-  F.G = (P.V + ch - 1) / ch;
-  F.heavy_first = fused && P.R <= 128 && (int64_t)rows_pad * F.G > LPS_HEAVY_FIRST_WG ? 1 : 0;
+  F.G = p.G;
+  F.cv = p.cv;
+  F.nvec = p.nvec;
+  F.heavy_first = 0;
   F.counters = w.counters;
   F.status = w.status;
-  F.sum1 = w.sum1;
-  F.sum2 = w.sum2;
+  F.sums = w.sums;
   F.hist = w.hist;
   F.cands = w.cands;
-  F.s_stride = w.s_stride;
-  F.h_stride = w.h_stride;
-  F.c_stride = w.c_stride;
-  return dispatch_fast(dtype, vec, F, rows_pad, fused, s);
+  F.capw = p.capw;
+  switch (dtype) {
+    case LPS_DTYPE_F32: return dispatch_rg_dt<LPS_DTYPE_F32>(F, p, s);
+    case LPS_DTYPE_BF16: return dispatch_rg_dt<LPS_DTYPE_BF16>(F, p, s);
+    default: return dispatch_rg_dt<LPS_DTYPE_F16>(F, p, s);
+  }
 }
 
 KParams neutral_params() {
@@ -240,7 +237,7 @@ SpecWs spec_layout(void* base, int B, int k, int V) {
   const size_t Rt = (size_t)B * (k + 1), Rd = (size_t)B * k;
   char* p = reinterpret_cast<char*>(base);
   w.fast = base;
-  w.fast_bytes = fast_layout(nullptr, (int)Rt, V).bytes;
+  w.fast_bytes = rg_layout(nullptr, (int)Rt, V).bytes;
   size_t off = align256(w.fast_bytes);
   w.draws_t = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rt * 8);
   w.draws_d = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rd * 8);
@@ -307,6 +304,15 @@ hipError_t launch_softmax_reg(const SoftmaxParams& S, const SmPlan& p, hipStream
 
 extern "C" {
 
+#ifdef LPS_RG_STAMPS
+// Timing builds only: copies the phase stamps of the last launches (8192 x 32
+// uint64 on the host).
+int lps_debug_stamps(uint64_t* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(rg::rg_stamps), sizeof(uint64_t) * 8192 * 32, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+#endif
+
 int lps_version(void) { return LPS_ABI_VERSION; }
 
 const char* lps_status_string(int code) {
@@ -322,7 +328,7 @@ const char* lps_status_string(int code) {
 
 size_t lps_workspace_bytes(int num_rows, int vocab, int flags) {
   if (num_rows <= 0 || vocab < 1 || vocab > kMaxVocab || (flags & LPS_FLAG_GENERIC)) return 0;
-  return fast_layout(nullptr, num_rows, vocab).bytes;
+  return rg_layout(nullptr, num_rows, vocab).bytes;
 }
 
 size_t lps_spec_workspace_bytes(int batch, int k, int vocab) {
@@ -445,7 +451,8 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   D.skip_draw = 1;
   D.plans = w.plans + (size_t)B * (k + 1);
   vec = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
-  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, 0, s)) !=
+  // (planned for the target rows' count, for which the workspace is sized)
+  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, 0, s, P.R)) !=
       hipSuccess)
     return LPS_ELAUNCH;
 

@@ -13,8 +13,8 @@
 // (:139-156), top-p "keep sorted position j iff j == 0 or cum[j-1] <= p" with
 // ties ordered lower index first (:158-185), min-p (:187-205), typical-p
 // (:207-238, including its NaN fallback to the argmax when the row holds
-// -inf), then an inverse-CDF draw in vocabulary order from the caller's
-// uniform.
+// -inf), then an inverse-CDF draw from the caller's uniform over the kept ids
+// in sorted order (z descending, ties lower index first).
 #pragma once
 
 #include "lps_common.h"
@@ -550,7 +550,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     }
   }
 
-  // ---- kept mass (vocabulary order, tie ranks) and the query probability ----
+  // ---- kept mass (tie ranks in vocabulary order) and the query probability ----
   uint64_t Zf = 0;
   uint32_t kept_n = greedy ? 1u : 0u;
   if (!greedy && status == 0) {
@@ -594,58 +594,59 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     qprob = qkr ? (float)((double)qmr / (double)Zf) : 0.0f;
   }
 
-  // ---- inverse-CDF draw in vocabulary order ----
+  // ---- inverse-CDF draw in sorted order: z descending, ties lower index first ----
   if (!greedy && status == 0 && !P.skip_draw) {
     float u = P.uniforms ? P.uniforms[r] : 0.5f;
     if (!(u >= 0.0f)) u = 0.0f;
     if (u >= 1.0f) u = 0.99999994f;
     uint64_t target = (uint64_t)((double)u * (double)Zf);
     if (target >= Zf) target = Zf - 1;
-    uint64_t run = 0;
-    uint32_t tie_run = 0;
+    // the key holding the target: the largest v with mass(kept, key > v) <= target
+    // (elements of key_lo past the kept ties weigh after every kept one)
+    const MassCut dc = select_mass<DT, VEC>(row, V, pc, S, target, zkey, [&](float x, uint32_t* k, uint64_t* m) {
+      const float z = zval(x);
+      *k = f2key(z);
+      if (*k < key_lo) return false;
+      *m = mass_fixed(mass_f(z, zmax));
+      return true;
+    });
+    // every element of that key has the same mass: the tie holding the target,
+    // counted in vocabulary order
+    const uint64_t e1 = dc.c_eq ? dc.m_eq / dc.c_eq : 0;
+    uint32_t jt = e1 ? (uint32_t)((target - dc.above) / e1) : 0u;
+    if (jt >= dc.c_eq && dc.c_eq) jt = dc.c_eq - 1;
+    const uint32_t vkey = dc.key;
+    uint32_t run = 0;
     if (tid == 0) S.misc[1] = -1;
     __syncthreads();
     for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
-      float x[VEC];
       uint32_t k[VEC];
-      uint64_t m[VEC];
       uint32_t nt_loc = 0;
-      uint64_t msum = 0;
       if (i0 < V) {
+        float x[VEC];
         loadv<DT, VEC>(row, i0, x);
         pc.apply<VEC>(i0, x);
 #pragma unroll
-        for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == key_lo ? 1u : 0u; }
+        for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == vkey ? 1u : 0u; }
       }
-      uint32_t ttot = 0, tex = 0;
-      if (n_tie != kNoTie) tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
-      if (i0 < V) {
-        uint32_t rk = tie_run + tex;
+      uint32_t ttot;
+      const uint32_t tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
+      if (i0 < V && run + tex <= jt && jt < run + tex + nt_loc) {
+        uint32_t rk = run + tex;
 #pragma unroll
         for (int j = 0; j < VEC; j++) {
-          bool kept = k[j] > key_lo || (k[j] == key_lo && (n_tie == kNoTie || rk < n_tie));
-          if (k[j] == key_lo) rk++;
-          m[j] = kept ? mass_fixed(mass_f(zval(x[j]), zmax)) : 0;
-          msum += m[j];
-        }
-      }
-      uint64_t btot;
-      const uint64_t bex = gblock_excl_scan<uint64_t>(msum, &btot, S.red64);
-      if (i0 < V && run + bex <= target && target < run + bex + msum) {
-        uint64_t a = run + bex;
-#pragma unroll
-        for (int j = 0; j < VEC; j++) {
-          if (m[j] && a <= target && target < a + m[j]) S.misc[1] = (int)(i0 + j);
-          a += m[j];
+          if (k[j] == vkey) {
+            if (rk == jt) S.misc[1] = (int)(i0 + j);
+            rk++;
+          }
         }
       }
       __syncthreads();
       const int found = S.misc[1];
       __syncthreads();
       if (found >= 0) { token = found; break; }
-      run += btot;
-      tie_run += ttot;
+      run += ttot;
     }
   } else if (!greedy) {
     token = -1;

@@ -22,6 +22,9 @@ FLAGS = [
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Wall", "-Werror=return-type", "-Werror=uninitialized",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # a private array moved to LDS is addressed by the flat work-item id, which
+    # makes every wave read the dispatch packet (host memory) first
+    "-mllvm", "-disable-promote-alloca-to-lds",
 ]
 
 

@@ -26,7 +26,8 @@ given (``rows``: the int64 request indices still active, on the host), else
 from ``torch.rand`` on the prompts' device (``generator`` optional).  Two-model
 rounds take ``3k + 1`` uniforms per row (``k`` draft draws, ``k`` accept tests,
 ``k + 1`` replacement / bonus draws); MTP rounds take 3 (next token, draft,
-accept test).  Draws are inverse CDFs in vocabulary order, as ``lps_sample``
+accept test).  Draws are inverse CDFs in sorted order (scaled logit descending,
+ties lower index first), as ``lps_sample``
 defines them; the reference's ``torch.multinomial`` / ``torch.rand`` draw from
 the same distributions.
 """

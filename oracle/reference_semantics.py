@@ -29,7 +29,8 @@ Parity rules adopted (the reference leaves these open):
 
 Build extensions (absent from the reference, defined here by closed form):
 presence / frequency penalties (OpenAI definition), per-row histories,
-caller-supplied uniforms with an inverse-CDF draw in vocabulary order, the
+caller-supplied uniforms with an inverse-CDF draw in sorted order (scaled logit
+descending, ties lower index first: the order of the reference's top-p sort), the
 probability of a query token under the kept distribution, full-vocab logprobs
 and top-N logprobs.
 
@@ -227,21 +228,30 @@ def filter_row(z_row: torch.Tensor, p: RowParams) -> torch.Tensor:
     return z.reshape(-1)
 
 
+def sorted_order(z: np.ndarray) -> np.ndarray:
+    """Ids in the draw order: scaled logit descending, ties lower index first
+    (the stable descending sort of ``sampling.py:165``; -inf last)."""
+    return np.lexsort((np.arange(z.size), -z))
+
+
 def draw_inverse_cdf(filtered: torch.Tensor, u: float) -> int:
     """Build definition of the draw from caller uniform ``u in [0, 1)``: the
-    kept distribution ``p_i ~ exp(z_i - max z)`` in fp64, and the first index
-    in vocabulary order whose inclusive cumulative mass exceeds ``u * Z``.  The
-    reference's ``torch.multinomial`` draws from the same distribution
-    (``sampling.py:84-85``)."""
+    kept distribution ``p_i ~ exp(z_i - max z)`` in fp64, walked in sorted
+    order (``sorted_order``), and the first id whose inclusive cumulative mass
+    exceeds ``u * Z``.  The reference's ``torch.multinomial`` draws from the
+    same distribution (``sampling.py:84-85``); any fixed order gives that law,
+    and the sorted one is the order in which top-p already ranks the ids."""
     zf = filtered.double().numpy()
     m = np.max(zf)
-    e = np.where(np.isfinite(zf), np.exp(zf - m), 0.0)
+    order = sorted_order(zf)
+    zs = zf[order]
+    e = np.where(np.isfinite(zs), np.exp(zs - m), 0.0)
     cum = np.cumsum(e)
     tgt = u * cum[-1]
     j = int(np.searchsorted(cum, tgt, side="right"))
     if j >= len(e):                      # u * Z rounded up to Z: last kept id
         j = int(np.nonzero(e > 0)[0][-1])
-    return j
+    return int(order[j])
 
 
 def sample_row(x_row: torch.Tensor, p: RowParams, history: Sequence[int] = (), u: float = 0.5) -> RowResult:

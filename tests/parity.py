@@ -8,8 +8,9 @@ Bars:
   (fp32 softmax + fp32 cumsum) it is bit-exact except where the reference's
   own rounding at a position exceeds that position's distance to top_p
   (counted and reported as reference-rounding rows);
-* draws: the GPU token's interval of the fp64 kept-set CDF contains the
-  uniform, up to ``DRAW_EPS`` (inverse CDF over the same kept set);
+* draws: the GPU token's interval of the fp64 kept-set CDF in sorted order
+  (z descending, ties lower index first) contains the uniform, up to
+  ``DRAW_EPS`` (inverse CDF over the same kept set);
 * logprobs / probabilities: |gpu - ref| <= LP_RTOL * |ref| + LP_ATOL.
 """
 
@@ -47,14 +48,18 @@ def row_params(w, i) -> O.RowParams:
 
 
 def draw_ok(z: torch.Tensor, kept: np.ndarray, u: float, tok: int, eps: float = DRAW_EPS) -> bool:
+    """The uniform lies in the token's interval of the fp64 kept-set CDF in
+    sorted order (z descending, ties lower index first), up to ``eps``."""
     if tok < 0 or tok >= kept.size or not kept[tok]:
         return False
     zz = z.double().numpy()
     m = zz[kept].max()
     e = np.where(kept, np.exp(np.where(kept, zz, m) - m), 0.0)
-    cum = np.cumsum(e) / e.sum()
-    lo = cum[tok - 1] if tok > 0 else 0.0
-    hi = cum[tok]
+    Z = e.sum()
+    zt = zz[tok]
+    before = (zz > zt) | ((zz == zt) & (np.arange(zz.size) < tok))
+    lo = e[before & kept].sum() / Z
+    hi = lo + e[tok] / Z
     return lo - eps <= u < hi + eps
 
 

@@ -302,9 +302,18 @@ def _check_spec(sw, out, residual="target"):
         if sw.temperature <= 0:
             assert int(tok[b, j]) == int(torch.argmax(sw.target[b, j]))
         elif residual == "target" and int(n[b]) == int(n_ref[b]):
-            z = O.apply_top_p((sw.target[b, j] / sw.temperature).reshape(1, -1), sw.top_p).reshape(-1)
+            zj = sw.target[b, j] / sw.temperature
+            z = O.apply_top_p(zj.reshape(1, -1), sw.top_p).reshape(-1)
             kept = torch.isfinite(z).numpy()
-            assert PY.draw_ok(sw.target[b, j] / sw.temperature, kept, float(sw.u_resample[b, j]), int(tok[b, j]))
+            u, t = float(sw.u_resample[b, j]), int(tok[b, j])
+            if not PY.draw_ok(zj, kept, u, t):
+                # a top-p boundary row: the kernel keeps the fp64-exact set, which may
+                # differ from the fp32 restatement within the band (parity rule 4)
+                order, _, n_truth = O.top_p_truth(zj, sw.top_p)
+                kt = np.zeros(kept.size, dtype=bool)
+                kt[order[:n_truth]] = True
+                assert O.top_p_band(zj, sw.top_p, int(kept.sum()), n_truth, PY.TOP_P_EPS), (b, j)
+                assert PY.draw_ok(zj, kt, u, t), (b, j, t)
     return amb
 
 
@@ -353,3 +362,25 @@ def test_spec_verify_greedy_and_leviathan(dev):
                 assert lo - 1e-6 <= u < float(cum[t]) + 1e-6, (b, j, t, int(tok_ref[b, j]), u)
                 checked += 1
     assert checked > 0
+
+
+def test_query_token_outside_vocab_has_zero_probability(dev):
+    """A query (draft) id >= V on nucleus, pure and top-k rows: probability 0,
+    no logit read past the row (the accept rule then rejects, as
+    verify_drafts_kernel does for such ids)."""
+    from lps import SamplingParams, sample_rows
+    g = torch.Generator().manual_seed(31)
+    B, V = 6, 20000
+    x = (torch.randn((B, V), generator=g) * 2).to(dev)
+    T = torch.tensor([1.0, 0.8, 1.0, 0.7, 1.0, 0.9])
+    k = torch.tensor([0, 0, 0, 0, 40, 40], dtype=torch.int32)
+    p = torch.tensor([0.9, 0.95, 1.0, 1.0, 0.9, 1.0])
+    q = torch.tensor([V, V + 7, V, 2**40, V, V + 1], dtype=torch.int64)
+    params = SamplingParams.build(B, dev, temperature=T.to(dev), top_k=k.to(dev), top_p=p.to(dev))
+    u = torch.rand(B, generator=g).to(dev)
+    a = sample_rows(x, params, u, query_tokens=q.to(dev))
+    ok = sample_rows(x, params, u, query_tokens=torch.zeros(B, dtype=torch.int64, device=dev))
+    torch.cuda.synchronize(dev)
+    assert (a.query_prob.cpu() == 0).all()
+    assert torch.equal(a.tokens, ok.tokens)
+    assert (a.status.cpu() == 0).all()

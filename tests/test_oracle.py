@@ -172,14 +172,23 @@ def test_typical_p_closed_form_and_nan_fallback():
 
 
 def test_inverse_cdf_draw_brute_force():
-    z = torch.tensor([0.0, float("-inf"), 1.0, 0.5, float("-inf"), -0.3])
-    e = np.array([math.exp(v - 1.0) if math.isfinite(v) else 0.0 for v in z.tolist()])
-    cum = np.cumsum(e) / e.sum()
+    # ids walked by z descending, ties lower index first: 2, 3, 6, 0, 5 (-inf last)
+    z = torch.tensor([0.0, float("-inf"), 1.0, 0.5, float("-inf"), -0.3, 0.5])
+    vals = z.tolist()
+    order = sorted(range(len(vals)), key=lambda i: (-vals[i], i))
+    assert order[:5] == [2, 3, 6, 0, 5]
+    e = [math.exp(vals[i] - 1.0) if math.isfinite(vals[i]) else 0.0 for i in order]
+    tot = sum(e)
     for u in np.linspace(0, 0.999999, 97):
         j = O.draw_inverse_cdf(z, float(u))
-        want = int(np.argmax(cum > u))
-        assert j == want and math.isfinite(z[j].item())
-    assert O.draw_inverse_cdf(z, 0.0) == 0
+        acc, want = 0.0, None
+        for pos, i in enumerate(order):
+            acc += e[pos] / tot
+            if want is None and u < acc:
+                want = i
+        assert j == want and math.isfinite(z[j].item()), (u, j, want)
+    assert O.draw_inverse_cdf(z, 0.0) == 2          # the largest z first
+    assert O.draw_inverse_cdf(z, 0.99999) == 5       # the smallest finite z last
 
 
 def test_inverse_cdf_draw_chi_square():
