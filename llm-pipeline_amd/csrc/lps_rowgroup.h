@@ -19,10 +19,11 @@
 //            published as a candidate.
 //   NUCLEUS  (and PURE, top_p = 1): an exact mass histogram of the chunk in
 //            LDS: e = exp2(fma(x, c, -ref)), ref = ceil(max * c), binned by
-//            e's exponent and top 7 mantissa bits (8192 bins, 128 per
-//            octave), accumulating count << 48 | the low 16 mantissa bits, so
-//            each bin's mass is exact (and the chunk's total mass Z with it).
-//            The top 32 octaves are published; after one barrier among the
+//            e's exponent and top 7 mantissa bits (the top 32 octaves, 128
+//            bins each), accumulating count << 48 | the low 16 mantissa bits,
+//            so each bin's mass is exact; smaller masses are summed in
+//            registers, and the chunk's total mass Z is exact to fp64.
+//            The bins are published; after one barrier among the
 //            row's workgroups every workgroup merges them (rescaled to the
 //            row's reference) and locates two regions: the bins holding the
 //            top-p cut (cumulative mass p * Z from the top) and the bins
@@ -74,10 +75,12 @@ __device__ uint64_t rg_stamps[8192 * 32];
 
 constexpr int NT = 512;            // threads per workgroup (8 waves: up to 256 VGPRs each)
 constexpr int NW = NT / 64;        // waves per workgroup
-constexpr int HB = 8192;           // mass histogram bins: 64 octaves x 128 sub-bins
+constexpr int HB = 4096;           // mass histogram bins: the top 32 octaves x 128 sub-bins
 constexpr int HOCT = 128;          // bins per octave
 constexpr int HB_NAN = HB - 1;     // bin of NaN masses (no real mass reaches it)
-constexpr int HPUB = 4096;         // published bins: the top 32 octaves
+constexpr int HPUB = HB;           // published bins
+constexpr uint32_t BELOW = 0xFFFFu;  // "bin" of masses under the histogram (summed apart)
+constexpr int HE0 = 96;            // float exponent of bin 0: masses from 2^-31
 constexpr int MAXG = 16;           // chunks per row
 constexpr int CAPR = 4096;         // candidates per row (the finaliser holds 4 per thread)
 constexpr int FPT = CAPR / NT;     // finaliser candidates per thread
@@ -95,7 +98,6 @@ enum {
   RF_HISTORY = 2,     // a history count does not fit 8 bits
   RF_SPLIT = 4,       // the row's workgroups ran on more than one XCD
   RF_REGION = 8,      // no usable cut / draw region, or the barrier timed out
-  RF_RANGE = 16,      // a region lies outside this chunk's histogram range
 };
 
 // Per-chunk summary, one 64-byte record (published for the finaliser).
@@ -155,16 +157,15 @@ struct RgX {  // cross-wave exchange slots, each reused only after a barrier
   double md[16];
   uint64_t mq[8];
   float mf[8];
-  int32_t nc[MAXG];                  // finaliser: candidates per chunk
-  int32_t cpre[MAXG];                // finaliser: exclusive prefix of nc
-  int32_t wpre[MAXG * NW];           // finaliser: exclusive prefix of the wave counts in a chunk
+  int32_t wpre[MAXG * NW];           // finaliser: candidates of each wave segment
+  int32_t opre[MAXG * NW];           // finaliser: prefix of the segments' overflow entries
   float rf[MAXG];                    // the row's chunk references
   float rm[MAXG];                    // the row's chunk maxima (NaN chunk: +inf)
 };
 template <int NE>
 struct RgChunkS : RgX {
   uint32_t hc[NT * NE / 4];            // 8-bit history counts of the chunk's ids
-  unsigned long long hist[HB];          // count << 48 | sum of low 16 mantissa bits
+  unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
 };
 struct RgFinalS : RgX {
   uint32_t cnt[SELB];                   // select histograms: counts
@@ -295,12 +296,13 @@ __device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ float emass(float x, float c, float ref) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(x, c, -ref));
 }
-// Histogram bin of a mass: its exponent and top 7 mantissa bits, 64 octaves
-// below 2 (bin 8064 holds [1, 1 + 1/128)); smaller masses (and 0) in bin 0,
+// Histogram bin of a mass: its exponent and top 7 mantissa bits, 32 octaves
+// below 2 (bin 3968 holds [1, 1 + 1/128)); smaller masses (and 0) BELOW,
 // NaN / inf in bin HB_NAN.
 __device__ __forceinline__ uint32_t ebin(float e) {
-  uint32_t b = __float_as_uint(e) >> 16;
-  b = (b > 8192u ? b : 8192u) - 8192u;
+  const uint32_t q = __float_as_uint(e) >> 16;
+  if (q < (uint32_t)(HE0 << 7)) return BELOW;
+  const uint32_t b = q - (uint32_t)(HE0 << 7);
   return b < (uint32_t)HB_NAN ? b : (uint32_t)HB_NAN;
 }
 // Exact mass of a bin from its accumulator (count << 48 | sum of the low 16
@@ -308,7 +310,7 @@ __device__ __forceinline__ uint32_t ebin(float e) {
 __device__ __forceinline__ double bin_mass(uint32_t b, unsigned long long acc) {
   const double cnt = (double)(acc >> 48);
   const double low = (double)(acc & 0xFFFFFFFFFFFFull);
-  const int E = (int)(b >> 7) + 64;
+  const int E = (int)(b >> 7) + HE0;
   const double m = cnt * (8388608.0 + (double)(b & 127u) * 65536.0) + low;
   return ldexp(m, E - 150);
 }
@@ -322,11 +324,11 @@ __device__ __forceinline__ uint64_t zmass_fix(float z, float R) {
 __device__ __forceinline__ double bin_mass_u(int b, unsigned long long acc) {
   const uint32_t cnt = (uint32_t)(acc >> 48), low = (uint32_t)acc;
   const double m = __builtin_fma((double)(cnt * (128u + (uint32_t)(b & 127))), 65536.0, (double)low);
-  return ldexp(m, (b >> 7) + 64 - 150);
+  return ldexp(m, (b >> 7) + HE0 - 150);
 }
 // The smallest mass of bin b.
 __device__ __forceinline__ double bin_base(int b) {
-  return ldexp(8388608.0 + (double)(b & 127) * 65536.0, (b >> 7) + 64 - 150);
+  return ldexp(8388608.0 + (double)(b & 127) * 65536.0, (b >> 7) + HE0 - 150);
 }
 
 // ---------------------------------------------------------------------------

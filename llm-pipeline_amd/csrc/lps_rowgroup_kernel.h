@@ -140,13 +140,19 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     // ---- exact mass histogram of the chunk ----
     uint32_t bins[NE / 2 + 1];
 #pragma unroll
-    for (int i = 0; i < NE / 2 + 1; i++) bins[i] = 0u;
+    for (int i = 0; i < NE / 2 + 1; i++) bins[i] = 0u;  // (read only when the chunk max is finite)
+    // masses under the histogram (each < 2^-31, at most NE of them: an fp32
+    // sum is within 2^-40 of the chunk's largest mass)
+    float zlow = 0.0f;
     if (Mfin) {
 #pragma unroll
       for (int s = 0; s < NE; s++) {
         const float e = emass(C.x[s], c, ref);
         const uint32_t b = ebin(e);
-        atomicAdd(&S.hist[b], (1ull << 48) | (unsigned long long)(__float_as_uint(e) & 0xFFFFu));
+        // masses under the histogram go to a per-lane spare slot (no branch, no conflicts)
+        atomicAdd(&S.hist[b != BELOW ? b : (uint32_t)(HB + lane)],
+                  (1ull << 48) | (unsigned long long)(__float_as_uint(e) & 0xFFFFu));
+        zlow += b == BELOW ? e : 0.0f;
         bins[s >> 1] |= b << (16 * (s & 1));
       }
     }
@@ -166,9 +172,9 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
         double m = bin_mass_u(b, a);
         if (b == HB_NAN) { nanc = (uint32_t)(a >> 48); m = 0.0; }
         zs += m;
-        if (NT * i >= HB - HPUB) hout[b - (HB - HPUB)] = (float)m;
+        hout[b] = (float)m;
       }
-      zs = wreduce(zs, OpAdd{});
+      zs = wreduce(zs + (double)zlow, OpAdd{});
       nanc = wreduce(nanc, OpAdd{});
       if (lane == 0) { S.d[wv] = zs; S.u[wv] = nanc; }
       __syncthreads();
@@ -311,9 +317,6 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const int dl = Mfin && rfin ? (int)(R - ref) : 0;
     auto own = [&](int b) { return b >= (1 << 30) ? b : b + HOCT * dl; };
     const int l1 = own(sm.reg[0]), h1 = own(sm.reg[1]), l2 = own(sm.reg[2]), h2 = own(sm.reg[3]);
-    // a region reaching this chunk's lowest bin cannot be told apart from the
-    // masses below the histogram's range
-    if (Mfin && (l1 <= 0 || l2 <= 0) && (S.hist[0] >> 48) != 0ull) flags |= RF_RANGE;
     double ab1 = 0.0, ab2 = 0.0;
     uint32_t nab = 0;
 #pragma unroll
@@ -410,6 +413,16 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   const float T = g.T;
   const float c = __fdiv_rn(kLog2e, greedy ? 1.0f : T);
 
+  // ---- candidates, first pass: entry k0 of wave segment s0, loaded before the
+  // counts are known (in flight with the summaries); the rest after them ----
+  const int capw = F.capw;
+  const int nseg = G * NW;
+  const int lgK = 31 - __builtin_clz(NT / nseg);  // entries per segment in the first pass
+  const int s0 = tid >> lgK, k0 = tid & ((1 << lgK) - 1);
+  auto seg_slot = [&](int sg, int k) -> int { return (sg / NW) * capw + (sg % NW) * (capw / NW) + k; };
+  uint2 cv0 = make_uint2(0u, 0u);
+  if (s0 < nseg) cv0 = ld_pub(cands + seg_slot(s0, k0));
+
   // ---- F1: the chunk summaries (wave 0) ----
   if (wv == 0) {
     RgSum a{};
@@ -427,22 +440,30 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const double A2 = wsum(af ? a.ab2 * sc : 0.0);
     const uint32_t nab = wsum(lane < G ? a.nab1 : 0u);
     const uint32_t nanb = wmax(lane < G ? a.nanbin : 0u);
-    // candidates per chunk and their prefixes (the waves' segments in order)
-    uint32_t nch = 0, over = 0;
+    // segment counts; overflow beyond the first pass, prefixed over segments
+    uint32_t ntot = 0, nover = 0, over = 0;
     if (lane < G) {
 #pragma unroll
       for (int q = 0; q < NW; q++) {
         const uint32_t n = a.wc[q];
         over |= n == WC_OVER ? 1u : 0u;
-        S.wpre[lane * NW + q] = (int)nch;
-        nch += n == WC_OVER ? 0u : n;
+        const uint32_t nn = n == WC_OVER ? 0u : n;
+        S.wpre[lane * NW + q] = (int)nn;
+        ntot += nn;
+        nover += nn > (1u << lgK) ? nn - (1u << lgK) : 0u;
       }
     }
     if (wreduce(over, OpOr{})) fl |= RF_OVERFLOW;
-    const uint32_t cinc = wscan_incl(nch);
+    const uint32_t ncand = wsum(ntot);
+    const uint32_t oinc = wscan_incl(nover);
     if (lane < G) {
-      S.nc[lane] = (int)nch;
-      S.cpre[lane] = (int)(cinc - nch);
+      uint32_t o = oinc - nover;
+#pragma unroll
+      for (int q = 0; q < NW; q++) {
+        const uint32_t nn = (uint32_t)S.wpre[lane * NW + q];
+        S.opre[lane * NW + q] = (int)o;
+        o += nn > (1u << lgK) ? nn - (1u << lgK) : 0u;
+      }
       S.rf[lane] = af ? a.ref : -INFINITY;
       S.rm[lane] = a.mkey == 0xFFFFFFFFu ? INFINITY : key2f(a.mkey);
     }
@@ -453,10 +474,11 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       S.mi[19] = (int)nab;
       S.mi[20] = (int)nanb;
       S.mi[21] = a.reg[0]; S.mi[22] = a.reg[1]; S.mi[23] = a.reg[2]; S.mi[24] = a.reg[3];
+      S.mi[25] = (int)ncand;
       S.md[0] = Z; S.md[1] = A1; S.md[2] = A2;
       S.mf[0] = R;
     }
-    if (lane == 63) S.mi[25] = (int)cinc;  // candidates of the row
+    if (lane == 63) S.mi[26] = (int)oinc;  // overflow entries of the row
   }
   __syncthreads();
   RG_STAMP(25);
@@ -483,36 +505,39 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0.99999994f;
 
-  // ---- candidates: the row's candidate i (chunk, then wave order) at e * NT + t ----
-  const int capw = F.capw;
+  // ---- candidates in register slots e * NT + t: e = 0 the first pass, e >= 1
+  // the overflow entries (o = (e - 1) * NT + t of the row's overflow list) ----
   uint32_t ck[FPT];
   uint64_t cm[FPT];
   uint32_t cf[FPT];  // region flags (nucleus)
   const int NC = __builtin_amdgcn_readfirstlane(S.mi[25]);
-  auto present = [&](int e) -> bool { return e * NT + tid < NC; };
-  // slot of candidate i: its chunk and wave segment from the prefixes
-  auto slot_of = [&](int i) -> int {
-    int w = 0;
-    for (int k = 1; k < G; k++) w += i >= S.cpre[k] ? 1 : 0;
-    const int rem = i - S.cpre[w];
-    int q = 0;
-#pragma unroll
-    for (int k = 1; k < NW; k++) q += rem >= S.wpre[w * NW + k] ? 1 : 0;
-    return w * capw + q * (capw / NW) + rem - S.wpre[w * NW + q];
+  const int NO = __builtin_amdgcn_readfirstlane(S.mi[26]);
+  if (NO > (FPT - 1) * NT) return 13;
+  const bool p0 = s0 < nseg && k0 < S.wpre[min(s0, nseg - 1)];
+  auto present = [&](int e) -> bool { return e == 0 ? p0 : (e - 1) * NT + tid < NO; };
+  // slot of overflow entry o: the last segment whose overflow prefix is <= o
+  auto over_slot = [&](int o) -> int {
+    int lo = 0, hi = nseg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (S.opre[mid] <= o) lo = mid; else hi = mid - 1;
+    }
+    return seg_slot(lo, (1 << lgK) + o - S.opre[lo]);
   };
   {
     uint2 cv[FPT];
+    cv[0] = cv0;
 #pragma unroll
-    for (int e = 0; e < FPT; e++) {
+    for (int e = 1; e < FPT; e++) {
       cv[e] = make_uint2(0u, 0u);
-      if (e * NT < NC && present(e)) cv[e] = ld_pub(cands + slot_of(e * NT + tid));
+      if ((e - 1) * NT < NO && present(e)) cv[e] = ld_pub(cands + over_slot((e - 1) * NT + tid));
     }
 #pragma unroll
     for (int e = 0; e < FPT; e++) {
       ck[e] = 0u;
       cf[e] = 0u;
       cm[e] = 0ull;
-      if (e * NT >= NC) continue;
+      if (e > 0 && (e - 1) * NT >= NO) continue;
       const int sl = e * NT + tid;
       const bool pr = present(e);
       const float xv = __uint_as_float(cv[e].x);
@@ -684,18 +709,21 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     uint64_t Zkept = Zfx;
     // whether every id whose z equals fl(x / T) lies inside row bins [lo, hi]
     // under the binning of each chunk that can hold it (one wave)
+    // (one wave; lane w checks chunk w)
     auto group_inside = [&](float x, int lo, int hi) -> bool {
       const Group gr = collision_group(x, T);
-      bool ok = gr.ok != 0;
-      for (int w = 0; w < G; w++) {
-        const float rw = S.rf[w];
-        if (rw == -INFINITY || gr.lo > S.rm[w]) continue;  // no id of this chunk reaches the group
-        const int sh = HOCT * (int)(Rref - rw);
-        const int bl = (int)ebin(emass(gr.lo, c, rw)) - sh;
-        const int bh = (int)min(ebin(emass(fminf(gr.hi, S.rm[w]), c, rw)), (uint32_t)HB_NAN - 1u) - sh;
-        ok = ok && bl >= lo && bh <= hi;
+      bool bad = false;
+      if (lane < G) {
+        const float rw = S.rf[lane], mw = S.rm[lane];
+        if (rw != -INFINITY && !(gr.lo > mw)) {  // some id of this chunk may reach the group
+          const int sh = HOCT * (int)(Rref - rw);
+          const uint32_t el = ebin(emass(gr.lo, c, rw)), eh = ebin(emass(fminf(gr.hi, mw), c, rw));
+          const int bl = (el == BELOW ? -(1 << 20) : (int)el) - sh;
+          const int bh = (eh == BELOW ? -(1 << 20) : (int)min(eh, (uint32_t)HB_NAN - 1u)) - sh;
+          bad = !(bl >= lo && bh <= hi);
+        }
       }
-      return ok;
+      return gr.ok != 0 && __builtin_amdgcn_ballot_w64(bad) == 0ull;
     };
     // the kk-th lowest index among the candidates of key v selected by sel
     auto kth_index = [&](auto sel, uint32_t v, uint32_t kk) -> int {
@@ -727,6 +755,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       }
       if (tid == 0) S.mi[13] = -1;
       __syncthreads();
+      RG_STAMP(16);
       {  // rank sort: keys are distinct within a list (the index is part of the key);
          // 2^lg adjacent lanes share an entry, each comparing one slice of its list
         const int lg = NL <= 64 ? 3 : NL <= 128 ? 2 : NL <= 256 ? 1 : 0;
@@ -751,6 +780,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
         if (ie < NL && part == 0) S.kord[b + rank] = ie;
       }
       __syncthreads();
+      RG_STAMP(17);
       {  // inclusive prefix of the masses in sorted order (list 2's from kcum[N1 - 1])
         const uint64_t mv = tid < NL ? (uint64_t)S.kmass[S.kord[tid]] : 0ull;
         uint64_t tot;
@@ -759,37 +789,45 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
         __syncthreads();
       }
       RG_STAMP(27);
+      // every thread finds the cut and the draw by binary search over the
+      // prefixes; the two collision-group checks run on two waves at once
+      auto zkey_at = [&](int pos) -> uint32_t { return (uint32_t)(S.kkey[S.kord[pos]] >> 32); };
       uint64_t ckey = 0;  // the last kept id's sort key
+      int qc = -1, pd = -1;
       if (nuc) {
         // sorted position p of the row is kept iff its exclusive prefix <= limit
         const uint64_t A1 = (uint64_t)(S.md[1] * kFix);
         const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zfx : 0.0;
         uint64_t limit = (uint64_t)pl;
         if (limit >= Zfx) limit = Zfx - 1;
-        uint32_t nk = (tid < N1 && A1 + (tid > 0 ? S.kcum[tid - 1] : 0ull) <= limit) ? 1u : 0u;
-        nk = bred(nk, S.u2, OpAdd{});
+        int lo = 0, hi = N1;  // the first dropped position
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (A1 + (mid > 0 ? S.kcum[mid - 1] : 0ull) <= limit) lo = mid + 1; else hi = mid;
+        }
         // the cut must fall inside the list: something kept, something dropped
-        if (nk == 0u || A1 + S.kcum[N1 - 1] <= limit) return 6;
-        const int q = (int)nk - 1;
-        ckey = S.kkey[S.kord[q]];
+        if (lo == 0 || A1 + S.kcum[N1 - 1] <= limit) return 6;
+        qc = lo - 1;
+        ckey = S.kkey[S.kord[qc]];
         vkey = (uint32_t)(ckey >> 32);
-        uint32_t et = 0;  // ids at the cut's z: all (low half), kept (high half)
-        if (tid < N1 && (uint32_t)(S.kkey[S.kord[tid]] >> 32) == vkey) et = tid <= q ? 0x10001u : 1u;
-        et = bred(et, S.u3, OpAdd{});
-        const uint32_t ea = et & 0xFFFFu, ek = et >> 16;
+        // the ids at the cut's z are contiguous around qc
+        int f0 = 0, f1 = qc;  // the first position with z key <= vkey
+        while (f0 < f1) {
+          const int mid = (f0 + f1) >> 1;
+          if (zkey_at(mid) <= vkey) f1 = mid; else f0 = mid + 1;
+        }
+        int l0 = qc + 1, l1 = N1;  // the first position with z key < vkey
+        while (l0 < l1) {
+          const int mid = (l0 + l1) >> 1;
+          if (zkey_at(mid) < vkey) l1 = mid; else l0 = mid + 1;
+        }
+        const uint32_t ea = (uint32_t)(l0 - f0), ek = (uint32_t)(qc + 1 - f0);
         n_tie = ek == ea ? kNoTie : ek;
         if (n_tie != kNoTie) tie_lim = (int)(0xFFFFFFFFu - (uint32_t)ckey);
-        Zkept = A1 + S.kcum[q];
-        kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)nk);
+        Zkept = A1 + S.kcum[qc];
+        kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)lo);
         ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
         cut = key2f(vkey);
-        // the cut's collision group must lie inside region 1 in every chunk
-        if (wv == 0) {
-          const bool ok = group_inside(S.cx[S.lslot[S.kord[q]]], lo1, hi1);
-          if (lane == 0) S.mi[12] = ok ? 1 : 0;
-        }
-        __syncthreads();
-        if (!S.mi[12]) return 8;
       } else {
         kept_n = -1;  // filled below when asked
       }
@@ -798,22 +836,28 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
         uint64_t target = (uint64_t)((double)u * (double)Zkept);
         if (target >= Zkept) target = Zkept - 1;
         const uint64_t b2 = N1 > 0 ? S.kcum[N1 - 1] : 0ull;
-        if (tid < N2) {
-          const uint64_t hi_ = A2 + (S.kcum[N1 + tid] - b2);
-          const uint64_t lo_ = A2 + (tid > 0 ? S.kcum[N1 + tid - 1] - b2 : 0ull);
-          if (lo_ <= target && target < hi_) S.mi[13] = tid;
+        int lo = 0, hi = N2;  // the first position whose inclusive prefix passes the target
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (A2 + (S.kcum[N1 + mid] - b2) <= target) lo = mid + 1; else hi = mid;
         }
-        __syncthreads();
-        const int pd = S.mi[13];
-        if (pd < 0) return 9;
+        if (lo == N2 || target < A2) return 9;
+        pd = lo;
+      }
+      if (wv == 0 && nuc) {  // the cut's collision group lies inside region 1 in every chunk
+        const bool ok = group_inside(S.cx[S.lslot[S.kord[qc]]], lo1, hi1);
+        if (lane == 0) S.mi[12] = ok ? 1 : 0;
+      }
+      if (wv == 1 && want2) {  // the drawn id's group inside region 2
+        const bool ok = group_inside(S.cx[S.lslot[S.kord[N1 + pd]]], lo2, hi2);
+        if (lane == 0) S.mi[14] = ok ? 1 : 0;
+      }
+      __syncthreads();
+      if (nuc && !S.mi[12]) return 8;
+      if (want2) {
+        if (!S.mi[14]) return 11;
         const uint64_t dkey = S.kkey[S.kord[N1 + pd]];
         token = (int64_t)(0xFFFFFFFFu - (uint32_t)dkey);
-        if (wv == 0) {
-          const bool ok = group_inside(S.cx[S.lslot[S.kord[N1 + pd]]], lo2, hi2);
-          if (lane == 0) S.mi[14] = ok ? 1 : 0;
-        }
-        __syncthreads();
-        if (!S.mi[14]) return 11;
         chosen_z = key2f((uint32_t)(dkey >> 32));
         // the drawn id must be kept
         if (nuc && dkey < ckey) return 12;
