@@ -12,10 +12,14 @@ Prints ONE JSON line (rank 0, N=1) with the roofline of the sampling launch
 (algorithmic bytes per launch / average launch time, against 8 TB/s) and the
 CPU baseline (the oracle's op-for-op torch-CPU restatement of the reference
 sampler, row by row, timed on this host's cores).  One ``lps_sample`` launch is
-the fast kernel(s) plus the filtered general-kernel launch for deferred rows;
+the row-group kernel plus the filtered general-kernel launch for deferred rows;
 the launch time covers both (the filter launch is ~1-2 us when no row is
-deferred), so the roofline is that of the dominant fast kernel measured with
-the short filter launch included.
+deferred), so the roofline is that of the dominant row-group kernel measured
+with the short filter launch included.  Exactly ``--steps`` launches are
+timed: whole replays of a captured graph, then one graph of the remainder.
+
+``--config c4`` times ``lps_spec_verify`` (speculative-decoding verification,
+32 requests, k = 4, fp32) the same way.
 """
 
 from __future__ import annotations
@@ -86,13 +90,59 @@ def build_args(w, dev, logits_dev, out, lib_mod):
 
 
 def fast_path_kernel(w) -> str:
-    """The fast kernel(s) lps_sample picks for a workload (the host rule in
-    lps.hip: 16-byte-vector rows whose grid of 8192-logit chunk workgroups is at
-    most 2048 take the fused kernel, others the chunk + final pair)."""
-    es = 4 if str(w.logits.dtype) == "torch.float32" else 2
-    vec = w.V % (16 // es) == 0
-    grid = (w.B + 7) // 8 * 8 * ((w.V + 8191) // 8192)
-    return "fused_kernel" if vec and grid <= 2048 else "chunk_final_kernels"
+    """The kernel lps_sample runs for every row it can finish exactly: the
+    row-group kernel (chunks of a row on one XCD, the last to arrive
+    finalising the row)."""
+    return "rowgroup_kernel"
+
+
+def timed_replays(launch, K, Wm, nbuf, use_graph=True):
+    """Exactly K timed launches (after Wm untimed ones), bracketed by HIP events
+    on the launching stream: whole replays of a graph of ``per_graph``
+    launches, then one graph of the remainder.  Returns ms per launch."""
+    import torch
+    if not use_graph:
+        for i in range(Wm):
+            launch(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(K):
+            launch(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / K
+    per_graph = min(K, nbuf * max(1, 64 // nbuf))
+    full, rem = divmod(K, per_graph)
+
+    def capture(n):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(n):
+                launch(i)
+        return gr
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g_full = capture(per_graph)
+    g_rem = capture(rem) if rem else None
+    for _ in range(max(1, math.ceil(Wm / per_graph))):
+        g_full.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(full):
+        g_full.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / K
 
 
 def hbm_traffic(kernel: str, config: str):
@@ -125,7 +175,7 @@ def copy_calibration(nbytes: int = 256 << 20, reps: int = 4):
     print(json.dumps({"copy_calibration_bytes": nbytes, "copies": reps}), flush=True)
 
 
-def cpu_baseline(w, max_rows=None, repeats=3):
+def cpu_baseline(w, max_rows=None, repeats=3, dev=None):
     """Reference-as-written sampler (oracle restatement), one call per row with
     that row's parameters and history (continuous_batching.py:394-401)."""
     import torch
@@ -149,9 +199,18 @@ def cpu_baseline(w, max_rows=None, repeats=3):
         one_pass()
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    return {"value": round(len(rows) / t, 2), "unit": "rows/s", "cores": threads, "kind": "port",
-            "sample": f"{len(rows)} rows of the {w.name} batch x {repeats} repeats (median), fp32-upcast logits, "
-                      f"torch-CPU restatement of sampling.py:51-85 with torch.multinomial"}
+    out = {"value": round(len(rows) / t, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+           "sample": f"{len(rows)} rows of the {w.name} batch x {repeats} repeats (median), fp32-upcast logits, "
+                     f"torch-CPU restatement of sampling.py:51-85 with torch.multinomial"}
+    if dev is not None:
+        # the same rows through the GPU path, checked against the restatement:
+        # exact tokens, and the rows whose top-p cut or draw sits in the fp32
+        # band where the reference's rounding and the exact cut may differ
+        res = PY.run_workload(w, dev)
+        rep = PY.check_rows(w, res, rows=rows, lp=bool(w.logprobs))
+        out["parity"] = {"rows_checked": rep.rows, "exact_tokens": rep.exact_tokens,
+                         "band_keep_rows": rep.band_keep, "band_draw_rows": rep.band_draw}
+    return out
 
 
 def engine_step(args):
@@ -537,12 +596,111 @@ def lm_head_bench(args):
     }), flush=True)
 
 
+def spec_bench(args):
+    """c4: speculative-decoding verification (``lps_spec_verify``, the drop-in
+    for ``speculative.py:119-174``): 32 requests, k = 4, target logits
+    [32, 5, 151936] and draft logits [32, 4, 151936] fp32, T 0.8, top_p 0.95.
+    A step is one launch: both distributions' top-p filters and softmaxes, the
+    accept tests, and the replacement or bonus draw of every request.
+    Algorithmic bytes: both logits tensors once, the drafts and uniforms, and
+    the outputs."""
+    import torch
+    from lps import _device as D
+    from lps import _lib
+    from tests import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sw = W.c4()
+    B, k1, V = sw.target.shape
+    k = k1 - 1
+    tgt0, drf0 = sw.target.to(dev), sw.draft.to(dev)
+    nb = (tgt0.numel() + drf0.numel()) * 4
+    nbuf = max(2, math.ceil(2 * MALL_BYTES / nb))
+    tgts = [tgt0] + [tgt0.clone() for _ in range(nbuf - 1)]
+    drfs = [drf0] + [drf0.clone() for _ in range(nbuf - 1)]
+    tok = sw.draft_tokens.to(dev, torch.int64).contiguous()
+    ua = sw.u_accept.to(dev, torch.float32).contiguous()
+    ur = sw.u_resample.to(dev, torch.float32).contiguous()
+    lib = _lib.load()
+    ws = torch.zeros((max(lib.lps_spec_workspace_bytes(B, k, V), 1),), dtype=torch.uint8, device=dev)
+    n_acc = torch.empty((B,), dtype=torch.int32, device=dev)
+    toks = torch.empty((B, k1), dtype=torch.int64, device=dev)
+    acc = torch.empty((B, k), dtype=torch.int8, device=dev)
+    pt = torch.empty((B, k), dtype=torch.float32, device=dev)
+    qd = torch.empty((B, k), dtype=torch.float32, device=dev)
+    st = torch.empty((B * (2 * k + 1),), dtype=torch.int32, device=dev)
+    arglist = []
+    for t, d in zip(tgts, drfs):
+        a = _lib.SpecArgs()
+        a.target_logits, a.target_stride_b, a.target_stride_k = t.data_ptr(), t.stride(0), t.stride(1)
+        a.draft_logits, a.draft_stride_b, a.draft_stride_k = d.data_ptr(), d.stride(0), d.stride(1)
+        a.dtype, a.batch, a.k, a.vocab = D.dtype_code(t), B, k, V
+        a.temperature, a.top_p = float(sw.temperature), float(sw.top_p)
+        a.residual = _lib.LPS_RESIDUAL_TARGET
+        a.draft_tokens, a.u_accept, a.u_resample = tok.data_ptr(), ua.data_ptr(), ur.data_ptr()
+        a.n_accepted, a.tokens, a.accept = n_acc.data_ptr(), toks.data_ptr(), acc.data_ptr()
+        a.p_target, a.q_draft, a.row_status = pt.data_ptr(), qd.data_ptr(), st.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        arglist.append(a)
+
+    def launch(i):
+        rc = lib.lps_spec_verify(ctypes.byref(arglist[i % nbuf]), torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"lps_spec_verify failed: {rc}")
+
+    launch(0)
+    torch.cuda.synchronize()
+    assert int(st.ne(0).sum()) == 0, "row status errors"
+    ms_step = timed_replays(launch, args.steps, args.warmup, nbuf, not args.no_graph)
+    abytes = nb + B * k * (8 + 4) + B * k1 * 4 + B * 4 + B * k1 * 8 + B * k * (1 + 4 + 4) + B * (2 * k + 1) * 4
+    gbs = abytes / (ms_step / 1e3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import reference_semantics as O
+        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        threads = max(1, min(share, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        nr = 8
+        args_ref = (sw.target[:nr], sw.draft[:nr], sw.draft_tokens[:nr], sw.u_accept[:nr], sw.u_resample[:nr],
+                    sw.temperature, sw.top_p)
+        n_ref = O.spec_verify_ref(*args_ref)[0]
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.spec_verify_ref(*args_ref)
+            ts.append(time.perf_counter() - t0)
+        t = statistics.median(ts)
+        # agreement of the timed launch with the restatement on the sampled requests
+        # (an accept test within 1e-5 of its uniform may go either way)
+        same = int((n_acc[:nr].cpu() == n_ref).sum())
+        cpu = {"value": round(nr / t, 2), "unit": "requests/s", "cores": threads, "kind": "port",
+               "sample": f"{nr} of the 32 requests x 3 repeats (median): the oracle's torch-CPU restatement of "
+                         f"speculative.py:119-174 (top-p, softmax, accept tests, resample) on the same logits",
+               "parity": {"requests_checked": nr, "n_accepted_equal": same}}
+    print(json.dumps({
+        "metric": "speculative verification, requests/sec (c4: B=32, k=4, V=151936 fp32)",
+        "value": round(B / (ms_step / 1e3), 1), "unit": "requests/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c4: target [32, 5, 151936] fp32, draft = target[:, :4] + N(0, 0.5^2), draft tokens "
+                               "sampled from the draft, T 0.8, top_p 0.95, reference residual",
+                   "logits_buffers_rotated": nbuf, "hip_graph": not args.no_graph,
+                   "algorithmic_bytes_per_call": abytes, "kernel": "rowgroup_kernel (target and draft rows) + "
+                                                                  "spec verify kernels"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": hbm_traffic("spec_verify", "c4")},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c3", "c3f", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c3", "c3f", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
@@ -582,6 +740,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sampler shards rows across "
               f"GPUs with no exchange, which this single-GPU build does not launch.", file=sys.stderr)
         sys.exit(2)
+    if args.config == "c4":
+        spec_bench(args)
+        return
 
     import torch
     from lps import _lib
@@ -632,60 +793,30 @@ def main():
         if rc != 0:
             raise RuntimeError(f"lps_sample failed: {rc}")
 
-    # correctness self-check of the timed configuration (first rows vs oracle)
+    # the timed configuration must run clean (every row status 0); the rows the
+    # row-group kernel deferred to the general kernel are counted
     launch(0)
     torch.cuda.synchronize()
     assert int(io["status"].ne(0).sum()) == 0, "row status errors"
+    rp = torch.full((B,), -1, dtype=torch.int32, device=dev)
+    a_chk = build_args(w, dev, bufs[0], io, lib)
+    a_chk.row_path = rp.data_ptr()
+    rc = lib.lps_sample(ctypes.byref(a_chk), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0 and int(io["status"].ne(0).sum()) == 0, "row status errors"
+    deferred = int(rp.ne(0).sum())
 
     K, Wm = args.steps, args.warmup
     use_graph = not args.no_graph
-    if use_graph:
-        per_graph = nbuf * max(1, 64 // nbuf)
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(2):
-                launch(i)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            for i in range(per_graph):
-                launch(i)
-        reps_w = max(1, math.ceil(Wm / per_graph))
-        reps = max(1, math.ceil(K / per_graph))
-        for _ in range(reps_w):
-            g.replay()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        steps = reps * per_graph
-    else:
-        for i in range(Wm):
-            launch(i)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(K):
-            launch(i)
-        e1.record()
-        torch.cuda.synchronize()
-        steps = K
-    ms = e0.elapsed_time(e1)
-    ms_step = ms / steps
+    ms_step = timed_replays(launch, K, Wm, nbuf, use_graph)
+    steps = K
     rows_s = B / (ms_step / 1e3)
     gbs = abytes / (ms_step / 1e3) / 1e9
     assert int(io["status"].ne(0).sum()) == 0
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(w, max_rows=64 if B > 64 else None)
+        cpu = cpu_baseline(w, max_rows=64 if B > 64 else None, dev=dev)
 
     cfg = {"workload": {"c1": "c1: B=1, V=151936 fp32, rep 1.1 over 64 ids, T 0.7, top_k 50, top_p 0.9",
                         "c1g": "c1 greedy: B=1, V=151936 fp32, rep 1.1, T=0",
@@ -697,7 +828,8 @@ def main():
                               "1024 ids/row, chosen + top-20 logprobs"}[args.config],
            "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
            "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes,
-           "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w) + " + gen_row_kernel (deferred-row filter)"}
+           "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w) + " + gen_row_kernel (deferred-row filter)",
+           "deferred_rows": int(deferred)}
     if args.allowed_frac is not None:
         cfg["legality_mask"] = f"random, {args.allowed_frac:.0%} of ids legal per row, packed bits"
     line = {
