@@ -4,8 +4,10 @@
  * Plain C: pointers, sizes and enums only, no torch or HIP types.  The stream
  * argument is a hipStream_t passed as void* (NULL = the null stream).  Every
  * pointer in an args struct is a device pointer unless stated otherwise.  All
- * entry points are stream-ordered, never synchronise, keep no global mutable
- * state and are safe to call from several host threads at once.
+ * entry points are stream-ordered and never synchronise.  All but
+ * lps_sample_noalloc keep no global mutable state and are safe to call from
+ * several host threads at once; lps_sample_noalloc shares one workspace per
+ * GPU between its calls (see its declaration).
  *
  * The entry points replace the logits->token path of DavidAkinpelu/llm-pipeline:
  *
@@ -42,7 +44,9 @@ enum {
   LPS_EINVAL = 1,              /* bad shape, stride, pointer or parameter     */
   LPS_EUNSUPPORTED_DTYPE = 2,  /* logits dtype not one of lps_dtype            */
   LPS_ELAUNCH = 3,             /* the HIP launch failed                         */
-  LPS_EWORKSPACE = 4           /* workspace missing or smaller than required   */
+  LPS_EWORKSPACE = 4,          /* workspace missing or smaller than required   */
+  LPS_ENOALLOC_CAPACITY = 5    /* lps_sample_noalloc: the batch needs more workspace than
+                                * LPS_NOALLOC_WORKSPACE_BYTES                    */
 };
 
 /* Logits element types. */
@@ -219,6 +223,25 @@ size_t lps_spec_workspace_bytes(int batch, int k, int vocab);
 
 /* Sampler.sample_token (sampling.py:51-85), batched with per-row parameters. */
 int lps_sample(const lps_sample_args* args, void* stream);
+
+/* lps_sample without a caller workspace and without any allocation.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  args->workspace / workspace_bytes are ignored; the
+ * kernels use the library's own workspace, a device array of
+ * LPS_NOALLOC_WORKSPACE_BYTES per GPU that each GPU the library runs on holds
+ * until the process ends.  The call itself allocates nothing (no hipMalloc,
+ * no allocating library routine); the first call on a device looks the
+ * array's address up once and clears its counters with a small kernel on
+ * `stream`.  Batches whose lps_workspace_bytes(num_rows, vocab, flags)
+ * exceeds LPS_NOALLOC_WORKSPACE_BYTES return LPS_ENOALLOC_CAPACITY (for
+ * V = 151936: up to 99 rows per call).  Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (other streams, other host
+ * threads) race and must be ordered by the caller.  Results equal
+ * lps_sample's on the same inputs. */
+#define LPS_NOALLOC_WORKSPACE_BYTES ((size_t)16 << 20)
+int lps_sample_noalloc(const lps_sample_args* args, void* stream);
 
 /* speculative.py:119-174, batched: accept / reject, then the replacement or
  * bonus token. */

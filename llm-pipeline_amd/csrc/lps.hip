@@ -3,6 +3,8 @@
 // mutable state.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "lps_rowgroup.h"
 #include "lps_generic.h"
 #include "lps_lmhead.h"
@@ -91,13 +93,16 @@ int rg_max_chunks(int R, int V) {
   return g;
 }
 
+// Bytes of the per-row counter region at the workspace's start.
+size_t rg_counter_bytes() { return (size_t)RG_MAX_ROWS * 128; }
+
 RgWs rg_layout(void* base, int R, int V) {
   RgWs w{};
   if (R > RG_MAX_ROWS) R = RG_MAX_ROWS;
   const int G = rg_max_chunks(R, V);
   size_t off = 0;
   char* p = reinterpret_cast<char*>(base);
-  w.counters = reinterpret_cast<uint32_t*>(p + off); off = (size_t)RG_MAX_ROWS * 128;
+  w.counters = reinterpret_cast<uint32_t*>(p + off); off = rg_counter_bytes();
   w.status = reinterpret_cast<int32_t*>(p + off); off = round_up(off + (size_t)R * 4, 256);
   w.sums = reinterpret_cast<rg::RgSum*>(p + off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
   w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
@@ -322,6 +327,7 @@ const char* lps_status_string(int code) {
     case LPS_EUNSUPPORTED_DTYPE: return "unsupported logits dtype";
     case LPS_ELAUNCH: return "kernel launch failed";
     case LPS_EWORKSPACE: return "workspace missing or too small";
+    case LPS_ENOALLOC_CAPACITY: return "batch needs more workspace than lps_sample_noalloc holds (LPS_NOALLOC_WORKSPACE_BYTES)";
     default: return "unknown status";
   }
 }
@@ -336,7 +342,13 @@ size_t lps_spec_workspace_bytes(int batch, int k, int vocab) {
   return spec_layout(nullptr, batch, k, vocab).bytes;
 }
 
-int lps_sample(const lps_sample_args* a, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// lps_sample's launches with the workspace ws (the caller's, or the
+// no-allocation variant's static one).
+int sample_impl(const lps_sample_args* a, void* ws, size_t ws_bytes, void* stream) {
   if (!a) return LPS_EINVAL;
   if (!dtype_ok(a->dtype)) return LPS_EUNSUPPORTED_DTYPE;
   if (a->num_rows < 0 || a->vocab < 1 || a->vocab > kMaxVocab || a->rows_inner < 1) return LPS_EINVAL;
@@ -388,11 +400,83 @@ int lps_sample(const lps_sample_args* a, void* stream) {
   P.allowed = a->allowed;
   P.allowed_stride = a->allowed_stride;
   P.append_history = (a->flags & LPS_FLAG_APPEND_HISTORY) ? 1 : 0;
-  if (a->workspace && a->workspace_bytes < lps_workspace_bytes(a->num_rows, a->vocab, a->flags)) return LPS_EWORKSPACE;
+  if (ws && ws_bytes < lps_workspace_bytes(a->num_rows, a->vocab, a->flags)) return LPS_EWORKSPACE;
   const bool vec = vec_ok(a->logits, a->dtype, a->vocab, a->rows_inner, a->stride_outer, a->stride_inner);
-  hipError_t e = run_sample(P, a->dtype, vec, a->workspace, a->workspace_bytes, a->flags,
-                            reinterpret_cast<hipStream_t>(stream));
+  hipError_t e = run_sample(P, a->dtype, vec, ws, ws_bytes, a->flags, reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
+
+// ---------------------------------------------------------------------------
+// The no-allocation variant's workspace: one array per GPU, for the lifetime
+// of the process.  Host code never passes the array's name to a kernel or a
+// copy (on the host it is only a stand-in); it uses the device address that
+// hipGetSymbolAddress returns for the current device.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[LPS_NOALLOC_WORKSPACE_BYTES];
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipErrorNotInitialized;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// Zeroes n 32-bit words (a kernel rather than hipMemsetAsync, so that a
+// first call made under graph capture records no memset node).
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The current device's scratch address (set up on the device's first call:
+// the address lookup, then the row counters cleared on `s`, the one region
+// the kernels need zero at launch; every launch leaves it zero again).
+void* scratch_for_current_device(hipStream_t s, int* rc) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = LPS_ELAUNCH;
+    return nullptr;
+  }
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&] {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) {
+      const int words = (int)(rg_counter_bytes() / 4);
+      hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, s, static_cast<uint32_t*>(p),
+                         words);
+      e = hipGetLastError();
+    }
+    slot.ptr = e == hipSuccess ? p : nullptr;
+    slot.err = e;
+  });
+  if (slot.err != hipSuccess || !slot.ptr) {
+    *rc = LPS_ELAUNCH;
+    return nullptr;
+  }
+  *rc = LPS_OK;
+  return slot.ptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lps_sample(const lps_sample_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  return sample_impl(a, a->workspace, a->workspace_bytes, stream);
+}
+
+int lps_sample_noalloc(const lps_sample_args* a, void* stream) {
+  if (!a) return LPS_EINVAL;
+  const size_t need = lps_workspace_bytes(a->num_rows, a->vocab, a->flags);
+  if (need > (size_t)LPS_NOALLOC_WORKSPACE_BYTES) return LPS_ENOALLOC_CAPACITY;
+  if (need == 0) return sample_impl(a, nullptr, 0, stream);  // the general kernel (or nothing) needs no workspace
+  int rc = LPS_OK;
+  void* ws = scratch_for_current_device(reinterpret_cast<hipStream_t>(stream), &rc);
+  if (!ws) return rc;
+  return sample_impl(a, ws, LPS_NOALLOC_WORKSPACE_BYTES, stream);
 }
 
 int lps_spec_verify(const lps_spec_args* a, void* stream) {

@@ -18,6 +18,10 @@ LPS_EINVAL = 1
 LPS_EUNSUPPORTED_DTYPE = 2
 LPS_ELAUNCH = 3
 LPS_EWORKSPACE = 4
+LPS_ENOALLOC_CAPACITY = 5
+
+# lps_sample_noalloc's per-GPU workspace (include/lps.h)
+LPS_NOALLOC_WORKSPACE_BYTES = 16 << 20
 
 LPS_DTYPE_F32 = 0
 LPS_DTYPE_BF16 = 1
@@ -108,6 +112,7 @@ SIGNATURES = {
     "lps_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "lps_spec_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "lps_sample": (_i32, [ctypes.POINTER(SampleArgs), _vp]),
+    "lps_sample_noalloc": (_i32, [ctypes.POINTER(SampleArgs), _vp]),
     "lps_spec_verify": (_i32, [ctypes.POINTER(SpecArgs), _vp]),
     "lps_verify_drafts": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "lps_softmax": (_i32, [ctypes.c_void_p, _vp]),
@@ -147,6 +152,6 @@ def check(rc: int, what: str) -> None:
     msg = f"{what}: {load().lps_status_string(rc).decode()}"
     if rc == LPS_EUNSUPPORTED_DTYPE:
         raise TypeError(msg)
-    if rc in (LPS_EINVAL, LPS_EWORKSPACE):
+    if rc in (LPS_EINVAL, LPS_EWORKSPACE, LPS_ENOALLOC_CAPACITY):
         raise ValueError(msg)
     raise RuntimeError(msg)

@@ -141,7 +141,8 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
                 logprobs: bool = False, top_logprobs: int = 0, entropy: bool = False,
                 query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
                 path: str = "auto", generator: Optional[torch.Generator] = None,
-                allowed: Optional[torch.Tensor] = None, append_history: bool = False) -> SampleOutput:
+                allowed: Optional[torch.Tensor] = None, append_history: bool = False,
+                noalloc: bool = False) -> SampleOutput:
     """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
     synchronised and ``status`` is returned as a device tensor.
@@ -161,7 +162,13 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     ``history_lengths[r] += 1``, when the row has room), so the next step's
     penalties see it without a host round trip.  ``histories`` and
     ``history_lengths`` must then be int32 device tensors used as they are
-    (row-contiguous histories, contiguous lengths)."""
+    (row-contiguous histories, contiguous lengths).
+
+    ``noalloc``: launch through ``lps_sample_noalloc``, which uses the
+    library's own per-GPU workspace instead of a caller one and allocates
+    nothing (for batches up to ``LPS_NOALLOC_WORKSPACE_BYTES`` of workspace;
+    larger ones raise ``ValueError``).  Calls that overlap in time on one GPU
+    must not both use it."""
     if path not in ("auto", "generic"):
         raise ValueError("path must be 'auto' or 'generic'")
     D.require_device(logits, "logits")
@@ -262,15 +269,20 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_count = D.ptr(out.kept_count)
     a.row_path = D.ptr(out.row_path)
     a.flags = (0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
-    ws_bytes = _lib.load().lps_workspace_bytes(B, V, a.flags)
-    ws = workspace_for(dev, ws_bytes) if ws_bytes else None
-    a.workspace = D.ptr(ws)
-    a.workspace_bytes = ws.numel() if ws is not None else 0
+    if noalloc:
+        a.workspace = 0
+        a.workspace_bytes = 0
+    else:
+        ws_bytes = _lib.load().lps_workspace_bytes(B, V, a.flags)
+        ws = workspace_for(dev, ws_bytes) if ws_bytes else None
+        a.workspace = D.ptr(ws)
+        a.workspace_bytes = ws.numel() if ws is not None else 0
     a.allowed = D.ptr(allowed)
     a.allowed_stride = allowed.stride(0) if allowed is not None else 0
+    entry = "lps_sample_noalloc" if noalloc else "lps_sample"
     with torch.cuda.device(dev):
-        rc = _lib.load().lps_sample(ctypes.byref(a), D.stream_of(dev))
-    _lib.check(rc, "lps_sample")
+        rc = getattr(_lib.load(), entry)(ctypes.byref(a), D.stream_of(dev))
+    _lib.check(rc, entry)
     return out
 
 
