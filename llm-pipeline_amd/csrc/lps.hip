@@ -55,7 +55,7 @@ struct RgWs {
   int32_t* status;
   rg::RgSum* sums;
   float* hist;
-  uint2* cands;
+  uint4* cands;
   size_t bytes;
 };
 
@@ -106,7 +106,7 @@ RgWs rg_layout(void* base, int R, int V) {
   w.status = reinterpret_cast<int32_t*>(p + off); off = round_up(off + (size_t)R * 4, 256);
   w.sums = reinterpret_cast<rg::RgSum*>(p + off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
   w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
-  w.cands = reinterpret_cast<uint2*>(p + off); off = round_up(off + (size_t)R * rg::CAPR * 8, 256);
+  w.cands = reinterpret_cast<uint4*>(p + off); off = round_up(off + (size_t)R * rg::CAPR * 16, 256);
   w.bytes = off;
   return w;
 }

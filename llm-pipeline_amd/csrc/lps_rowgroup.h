@@ -16,7 +16,7 @@
 //   TOPK     a threshold below the chunk's k'-th largest logit (from the
 //            wave-level k'/8-th largest thread maxima), lowered to the start
 //            of its division-collision group; every logit at or above it is
-//            published as a candidate.
+//            a candidate.
 //   NUCLEUS  (and PURE, top_p = 1): an exact mass histogram of the chunk in
 //            LDS: e = exp2(fma(x, c, -ref)), ref = ceil(max * c), binned by
 //            e's exponent and top 7 mantissa bits (the top 32 octaves, 128
@@ -28,31 +28,39 @@
 //            row's reference) and locates two regions: the bins holding the
 //            top-p cut (cumulative mass p * Z from the top) and the bins
 //            holding the draw (u times the kept mass).  Elements in either
-//            region are published as candidates, with the exact mass above
-//            each region.
-// The last workgroup of a row to finish (an arrival count) finalises it: a
-// radix select over the candidates for top-k; for the nucleus, the two region
-// lists rank-sorted in LDS with exact fixed-point prefix masses (radix mass
-// selects when the lists exceed the sort's capacity); then the outputs.  The
-// draw is an inverse CDF in sorted order: kept ids by scaled logit
-// descending, ties lower index first.
+//            region are candidates (one list per region), with the exact mass
+//            above each region.
+// Candidates are gathered in LDS (per-wave segments filled by ballots), sorted
+// in the chunk by (z = fl(x / T) descending, index ascending) with a rank sort,
+// and published sorted; a top-k list stops after its k'-th entry and the
+// entries tied with it.
+// The last workgroup of a row to finish (an arrival count) finalises it: it
+// loads the G sorted lists of each kind, merges them (the rank of an entry is
+// its position in its own list plus a binary search in each other list), and
+// finds the top-k set, the top-p cut and the draw by binary searches over
+// exact fixed-point prefix masses in sorted order.  The draw is an inverse
+// CDF in sorted order: kept ids by scaled logit descending, ties lower index
+// first.
 //
 // A row the kernel cannot finish exactly (e.g. a flat row whose regions hold
-// more candidates than the finaliser's capacity, min-p / typical-p without
-// top-k, entropy requested) is marked LPS_ROW_DEFERRED in the workspace status
-// and sampled by the general kernel, launched after this one with that status
-// as its filter.
+// more candidates than the lists take, min-p / typical-p without top-k,
+// entropy requested) is marked LPS_ROW_DEFERRED in the workspace status and
+// sampled by the general kernel, launched after this one with that status as
+// its filter.
 //
 // Cross-workgroup handoffs (the histogram barrier and the arrival count):
-// every thread of the publishing workgroup stores, then an agent-scope
-// release fence; one thread then adds to the row's counter.  The reader spins
-// on relaxed agent-scope loads and then takes an agent-scope acquire fence
-// before reading the published data.
+// every thread of the publishing workgroup stores, then waits for its stores
+// to complete (they are then in the XCD's L2, which the row's workgroups
+// share); one thread then adds to the row's counter.  The reader spins on the
+// counter with agent-scope loads and reads the published data with
+// agent-scope loads, which are served by that L2 (never by a CU's L1).  A
+// row whose workgroups did not all run on one XCD is deferred.
 #pragma once
 
 #include <cstddef>
 
-#include "lps_fast_kernel.h"
+#include "lps_generic.h"
+#include "lps_wave.h"
 
 // Phase stamps of a timing build (LPS_RG_STAMPS): thread 0 of every
 // workgroup records the 100 MHz real-time counter at phase marks into
@@ -82,30 +90,38 @@ constexpr int HPUB = HB;           // published bins
 constexpr uint32_t BELOW = 0xFFFFu;  // "bin" of masses under the histogram (summed apart)
 constexpr int HE0 = 96;            // float exponent of bin 0: masses from 2^-31
 constexpr int MAXG = 16;           // chunks per row
-constexpr int CAPR = 4096;         // candidates per row (the finaliser holds 4 per thread)
-constexpr int FPT = CAPR / NT;     // finaliser candidates per thread
-constexpr int KEPT = 512;          // top-k kept list
-constexpr int SELB = 2048;         // radix-select digit bins (11 bits)
-constexpr int SELD = 11;
+constexpr int CAPR = 2048;         // published list entries per row (all chunks, both lists)
+constexpr int FT = 256;            // finaliser threads (waves 0-3, one per SIMD; the others leave)
+constexpr int FW = FT / 64;        // finaliser waves
+constexpr int FPT = CAPR / FT;     // finaliser: loaded entries per thread
+constexpr int FP1 = 4;             // finaliser: first-pass slots (loaded before the list lengths are known)
+constexpr int SEGCAP = 128;        // chunk: entries of one list per wave segment
+constexpr int CLMAX = NW * SEGCAP; // chunk: entries of one list
+constexpr int LKM = CAPR;          // finaliser: loaded entries of one list (all chunks)
+constexpr int KM = 1024;           // finaliser: merged (sorted) entries of one list
+constexpr int KPT = KM / FT;       // merged entries per thread in the prefix scans
 constexpr int HPT = HPUB / NT;     // published histogram bins per thread
 constexpr int HLT = HB / NT;       // LDS histogram bins per thread
-constexpr int SPT = SELB / NT;     // select bins per thread
 constexpr double kFix = 17592186044416.0;  // 2^44: fixed-point masses (relative to the row reference)
+constexpr int FAST_KMAX = 256;     // largest top_k / top-N of the row-group kernel
+
+// Row modes, decided per row from its parameters (row_cfg).
+enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEFER = 4 };
 
 // Chunk flags (RgSum.flags); any of them defers the row.
 enum {
-  RF_OVERFLOW = 1,    // more candidates than the workgroup's slots
+  RF_OVERFLOW = 1,    // more candidates than the lists take
   RF_HISTORY = 2,     // a history count does not fit 8 bits
   RF_SPLIT = 4,       // the row's workgroups ran on more than one XCD
   RF_REGION = 8,      // no usable cut / draw region, or the barrier timed out
 };
 
-// Per-chunk summary, one 64-byte record (published for the finaliser).
+// Per-chunk summary (published for the finaliser).
 struct RgSum {
   uint32_t mkey;      // max key of the penalised logits (0xFFFFFFFF: NaN present)
   int32_t amax;       // first index of that key (greedy rows)
   float ref;          // mass reference (an integer, log2 units; -inf: no finite logit)
-  uint32_t spare;
+  uint16_t n1, n2;    // published entries of list 1 (top-k / region 1) and list 2 (region 2)
   uint32_t flags;     // RF_*
   uint32_t xcc;       // XCD that ran the chunk
   uint32_t nab1;      // nucleus: elements above region 1
@@ -114,17 +130,8 @@ struct RgSum {
   double ab1;         // nucleus: exact mass above region 1 (chunk reference)
   double ab2;         // nucleus: exact mass above region 2
   int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row bins; the same in every chunk)
-  uint16_t wc[NW];    // candidates published by each wave (WC_OVER: its segment overflowed);
-                      // stored by the waves themselves, the rest by thread 0 (store_sum)
 };
-constexpr uint16_t WC_OVER = 0xFFFF;
-// Thread 0's part of a chunk summary: every field but the wave counts.
-__device__ __forceinline__ void store_sum(RgSum* d, const RgSum& a) {
-  d->mkey = a.mkey; d->amax = a.amax; d->ref = a.ref; d->spare = a.spare;
-  d->flags = a.flags; d->xcc = a.xcc; d->nab1 = a.nab1; d->nanbin = a.nanbin;
-  d->zsum = a.zsum; d->ab1 = a.ab1; d->ab2 = a.ab2;
-  d->reg[0] = a.reg[0]; d->reg[1] = a.reg[1]; d->reg[2] = a.reg[2]; d->reg[3] = a.reg[3];
-}
+__device__ __forceinline__ void store_sum(RgSum* d, const RgSum& a) { *d = a; }
 
 struct RgParams {
   KParams k;
@@ -138,10 +145,101 @@ struct RgParams {
   int32_t* status;     // [R]
   RgSum* sums;         // row r at sums + r * 2 * MAXG
   float* hist;         // row r at hist + r * G * HPUB
-  uint2* cands;        // row r at cands + r * CAPR: chunk j owns [j * capw, (j + 1) * capw),
-                       // its wave w the segment [w * capw / NW, (w + 1) * capw / NW) of that
-  int capw;            // candidate slots per chunk (a multiple of NW)
+  uint4* cands;        // row r at cands + r * CAPR: chunk j owns [j * capw, (j + 1) * capw): its
+                       // sorted list 1, then its sorted list 2, entries {z key, index, x bits, 0}
+  int capw;            // list entries per chunk
 };
+
+// ---------------------------------------------------------------------------
+// Row configuration.
+// ---------------------------------------------------------------------------
+struct RowCfg {
+  float T, c, topp, minp, typp, rep, pres, freq, u;  // c = log2(e) / T (1 / T -> log2(e) for greedy rows)
+  int topk, ntop, mode, kprime, hlen;
+  int64_t qtok;
+  bool greedy, pen;
+  const int32_t* hrow;
+};
+// Parameters and mode of row r (sampling.py:66-82 filter order; the row-group
+// kernel takes greedy rows, top-k rows with k <= FAST_KMAX, nucleus and pure
+// rows, and defers the rest to the general kernel).
+__device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
+  RowCfg g;
+  g.T = P.temperature ? P.temperature[r] : P.temperature_def;
+  g.topk = P.top_k ? P.top_k[r] : P.top_k_def;
+  g.topp = P.top_p ? P.top_p[r] : P.top_p_def;
+  g.minp = P.min_p ? P.min_p[r] : P.min_p_def;
+  g.typp = P.typical_p ? P.typical_p[r] : P.typical_p_def;
+  g.rep = P.rep ? P.rep[r] : P.rep_def;
+  g.pres = P.pres ? P.pres[r] : P.pres_def;
+  g.freq = P.freq ? P.freq[r] : P.freq_def;
+  g.u = P.uniforms ? P.uniforms[r] : 0.5f;
+  g.qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
+               ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
+               : -1;
+  // a query id outside the vocabulary has probability 0 (as verify_drafts_kernel
+  // treats it); no logit is read for it
+  if (g.qtok >= (int64_t)P.V) g.qtok = -1;
+  if (g.topp != g.topp) g.topp = 1.0f;
+  g.greedy = !(g.T > 0.0f);
+  g.c = __fdiv_rn(kLog2e, g.greedy ? 1.0f : g.T);
+  g.ntop = (P.n_top > 0 && P.top_logprobs) ? P.n_top : 0;
+  int mode;
+  if (g.greedy) mode = MODE_GREEDY;
+  else if (!(g.T >= 1e-4f)) mode = MODE_DEFER;
+  else if (g.topk > 0) mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
+  else if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
+  else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
+  if (P.entropy) mode = MODE_DEFER;
+  if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
+  g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
+  if (g.kprime > FAST_KMAX) mode = MODE_DEFER;
+  g.mode = mode;
+  g.hrow = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
+  int hlen = (g.hrow && P.history_len) ? P.history_len[r] : 0;
+  if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;
+  g.hlen = hlen;
+  g.pen = hlen > 0 && (g.rep != 1.0f || g.pres != 0.0f || g.freq != 0.0f);
+  return g;
+}
+
+// Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end
+// of the division-collision group of x0, so that "z >= fl(x0 / T)" is
+// "x >= result" for every x.  The group is searched at most 64 keys down, all
+// at once: lane l of the wave tests the step from l to l + 1 keys below x0,
+// and the group ends at the first failing lane.  x0 is wave-uniform and every
+// lane of the wave calls this.
+__device__ __forceinline__ float collision_lo(float x0, float T) {
+  const float q = __fdiv_rn(x0, T);
+  const uint32_t k0 = f2key(x0);
+  const uint32_t k = k0 - (threadIdx.x & 63u);
+  const uint64_t fail = wballot(!(k > kNegInfKey + 1u && __fdiv_rn(key2f(k - 1u), T) == q));
+  return key2f(k0 - (fail ? (uint32_t)__builtin_ctzll(fail) : 64u));
+}
+
+// Row order with rows that sample without top-k (nucleus / pure: the longest
+// finalisers) first: virtual row vr -> row, a bijection on [0, R) (R <= 128),
+// the same in every workgroup.
+__device__ __forceinline__ int heavy_first_row(const KParams& P, const int vr) {
+  const int lane = threadIdx.x & 63;
+  auto heavy = [&](int r) -> bool {
+    if (r >= P.R) return false;
+    const float T = P.temperature ? P.temperature[r] : P.temperature_def;
+    const int k = P.top_k ? P.top_k[r] : P.top_k_def;
+    return T > 0.0f && k <= 0;
+  };
+  const uint64_t m1 = wballot(heavy(lane)), m2 = wballot(heavy(lane + 64));
+  const uint64_t v1 = wballot(lane < P.R), v2 = wballot(lane + 64 < P.R);
+  const int nh = __popcll(m1) + __popcll(m2);
+  const bool hv = vr < nh;
+  const uint64_t a = hv ? m1 : (v1 & ~m1), b = hv ? m2 : (v2 & ~m2);
+  const int k = hv ? vr : vr - nh;
+  const int pa = __popcll(a);
+  const uint64_t sel = k < pa ? a : b;
+  const int kk = k < pa ? k : k - pa;
+  const uint64_t w = wballot(((sel >> lane) & 1ull) && (int)lanes_below(sel) == kk);
+  return (k < pa ? 0 : 64) + (int)__builtin_ctzll(w);
+}
 
 // ---------------------------------------------------------------------------
 // Shared memory.
@@ -150,33 +248,44 @@ struct RgX {  // cross-wave exchange slots, each reused only after a barrier
   float f[NW];
   uint32_t u[NW], u2[NW], u3[NW];
   int32_t i1[NW], i2[NW], i3[NW];
-  uint64_t q[NW];
+  uint64_t q[NW], q2[NW];
   double d[NW], d2[NW], d3[NW], d4[NW], d5[NW];
   uint32_t u4[NW];
   int32_t mi[32];
   double md[16];
   uint64_t mq[8];
   float mf[8];
-  int32_t wpre[MAXG * NW];           // finaliser: candidates of each wave segment
-  int32_t opre[MAXG * NW];           // finaliser: prefix of the segments' overflow entries
+  int32_t cn[2][MAXG];               // finaliser: entries of each chunk's lists
+  int32_t cb[2][MAXG + 1];           // finaliser: list prefixes over chunks
+  int32_t opre[MAXG + 1];            // finaliser: prefix of the chunks' entries past the first pass
   float rf[MAXG];                    // the row's chunk references
   float rm[MAXG];                    // the row's chunk maxima (NaN chunk: +inf)
 };
+// Chunk candidate lists: per-wave segments filled by ballots, then compacted.
+struct RgLists {
+  int32_t si[2][NW][SEGCAP];         // segment entries: vocabulary index
+  uint32_t sx[2][NW][SEGCAP];        // their logits (bits)
+  uint64_t ck[2][CLMAX];             // compacted
+  uint32_t cx[2][CLMAX];
+  int32_t scnt[2][NW];               // segment counts (SEGCAP + 1: overflowed)
+};
 template <int NE>
 struct RgChunkS : RgX {
-  uint32_t hc[NT * NE / 4];            // 8-bit history counts of the chunk's ids
-  unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
+  union {
+    struct {
+      uint32_t hc[NT * NE / 4];             // 8-bit history counts of the chunk's ids
+      unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
+    } a;
+    RgLists l;                               // after the counts and the histogram are used
+  };
 };
 struct RgFinalS : RgX {
-  uint32_t cnt[SELB];                   // select histograms: counts
-  unsigned long long mass[SELB];        // select histograms: fixed-point masses
-  int32_t cidx[CAPR];                   // candidate e * NT + t: vocabulary index | region flags
-  float cx[CAPR];                       // candidate logit
-  uint64_t kkey[KEPT];                  // kept list: (z key << 32) | ~index
-  unsigned long long kmass[KEPT];
-  int32_t kord[KEPT];                   // sorted position -> slot
-  unsigned long long kcum[KEPT];        // inclusive prefix in sorted order
-  int32_t lslot[KEPT];                  // nucleus lists: candidate slot of each entry
+  uint64_t lk[2][LKM];                  // loaded lists, chunk by chunk (sorted within a chunk)
+  uint32_t lx[2][LKM];                  // their logits (bits)
+  uint64_t sk[2][KM];                   // merged lists: keys in sorted order
+  uint32_t sx[2][KM];                   // logits (bits)
+  uint64_t sm[2][KM];                   // fixed-point masses
+  uint64_t sc[2][KM];                   // inclusive prefix of the masses
 };
 template <int NE>
 union RgShared {
@@ -190,27 +299,27 @@ union RgShared {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
-// Block reduction of a per-thread value; every thread gets the result.  The
-// slot array is free again after the next barrier.
-template <typename T, typename Op>
+// Block reduction of a per-thread value over W waves; every thread gets the
+// result.  The slot array is free again after the next barrier.
+template <int W = NW, typename T, typename Op>
 __device__ __forceinline__ T bred(T v, T* slot, Op op) {
   v = wreduce(v, op);
   if (lane_id() == 0) slot[wave_id()] = v;
   __syncthreads();
   T r = slot[0];
 #pragma unroll
-  for (int i = 1; i < NW; i++) r = op(r, slot[i]);
+  for (int i = 1; i < W; i++) r = op(r, slot[i]);
   return r;
 }
-// Exclusive prefix over the block in thread order; *total gets the sum.
-template <typename T>
+// Exclusive prefix over the block (W waves) in thread order; *total gets the sum.
+template <int W = NW, typename T>
 __device__ __forceinline__ T bscan(T v, T* total, T* slot) {
   const T inc = wscan_incl(v);
   if (lane_id() == 63) slot[wave_id()] = inc;
   __syncthreads();
   T off = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < NW; i++) {
+  for (int i = 0; i < W; i++) {
     const T s = slot[i];
     off += (i < wave_id()) ? s : (T)0;
     tot += s;
@@ -400,28 +509,6 @@ struct Chk {
   }
 };
 
-// Publishes the slots s < NS for which sel(s) holds into this wave's segment
-// (cap entries at seg), in slot order with lane order inside a slot: one
-// ballot per slot gives every lane its position, so no block scan is needed.
-// Returns the wave's count (the same in every lane; > cap: overflowed).
-template <int NS, class Sel, class Emit>
-__device__ __forceinline__ uint32_t wave_emit(Sel sel, Emit emit, uint2* seg, uint32_t cap) {
-  uint32_t n = 0;
-#pragma unroll
-  for (int s = 0; s < NS; s++) {
-    const bool on = sel(s);
-    const uint64_t m = __builtin_amdgcn_ballot_w64(on);
-    if (m) {
-      if (on) {
-        const uint32_t p =
-            n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        if (p < cap) seg[p] = emit(s);
-      }
-      n += (uint32_t)__popcll(m);
-    }
-  }
-  return n;
-}
 // Region bounds [lo, hi] of chunk bins as u16 pairs for the packed test in
 // emit_regions: L = lo | lo << 16, C = count | count << 16 (0: empty region).
 __device__ __forceinline__ void region_pair(int lo, int hi, uint32_t& L, uint32_t& C) {
@@ -438,11 +525,6 @@ __device__ __forceinline__ uint32_t in_region2(uint32_t w, uint32_t L, uint32_t 
   const u16x2 d = __builtin_bit_cast(u16x2, w) - __builtin_bit_cast(u16x2, L);
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, C), d));
 }
-// A wave's count into the chunk summary (lane 0 of the wave).
-__device__ __forceinline__ void store_wave_count(RgSum* d, uint32_t n, uint32_t cap) {
-  if ((threadIdx.x & 63) == 0) d->wc[threadIdx.x >> 6] = n > cap ? WC_OVER : (uint16_t)n;
-}
-
 // History ids of the row: the first NT are read before the chunk, so the count
 // table is built while the chunk's loads are in flight.
 __device__ __forceinline__ int prefetch_hist(const int32_t* hrow, int hlen) {
@@ -455,7 +537,7 @@ template <int NE>
 __device__ __forceinline__ bool build_counts(RgChunkS<NE>& S, const int32_t* hrow, int hlen, int id0, int lo, int n) {
   constexpr int WORDS = NT * NE / 4;
   static_assert(WORDS % 4 == 0, "whole 16-byte stores");
-  u32x4* h4 = reinterpret_cast<u32x4*>(S.hc);
+  u32x4* h4 = reinterpret_cast<u32x4*>(S.a.hc);
 #pragma unroll
   for (int i = threadIdx.x; i < WORDS / 4; i += NT) h4[i] = u32x4{0u, 0u, 0u, 0u};
   if (threadIdx.x == 0) S.mi[30] = 0;
@@ -465,7 +547,7 @@ __device__ __forceinline__ bool build_counts(RgChunkS<NE>& S, const int32_t* hro
     if (id >= lo && id < lo + n) {
       const int l = id - lo;
       const int sh = 8 * (l & 3);
-      const uint32_t old = atomicAdd(&S.hc[l >> 2], 1u << sh);
+      const uint32_t old = atomicAdd(&S.a.hc[l >> 2], 1u << sh);
       if (((old >> sh) & 0xFFu) >= 254u) sat = true;
     }
   };
@@ -506,147 +588,147 @@ __device__ __forceinline__ void apply_counts(Chk<DT, VPE, NE>& C, const uint32_t
 }
 
 // ---------------------------------------------------------------------------
-// Radix selects of the finaliser over register-resident candidates: thread t
-// holds candidate e * NT + t in ck[e], present when e < np.  MSB-first over
-// key - kmin with 11-bit digits; each level: one histogram pass, one scan.
+// Chunk candidate lists.
 // ---------------------------------------------------------------------------
-struct Range {
-  uint32_t base;
-  int bits;
-};
-template <typename PF>
-__device__ __forceinline__ Range key_range(const uint32_t (&ck)[FPT], PF present, RgFinalS& S) {
-  uint32_t mn = 0xFFFFFFFFu, mx = 0u;
-#pragma unroll
-  for (int e = 0; e < FPT; e++)
-    if (present(e)) { mn = min(mn, ck[e]); mx = max(mx, ck[e]); }
-  mn = bred(mn, S.u, OpMin{});
-  mx = bred(mx, S.u2, OpMax{});
-  Range R;
-  R.base = mn;
-  R.bits = mx > mn ? 32 - __clz(mx - mn) : 0;
-  return R;
+// Sort key of a candidate: (z key << 32) | ~index, z = fl(x / T) (x for greedy
+// rows).  Keys are distinct within a row; descending key order is z
+// descending, ties lower index first (the order of the reference's sort).
+__device__ __forceinline__ uint64_t cand_key(float x, int idx, bool greedy, float T) {
+  const float z = greedy ? x : __fdiv_rn(x, T);
+  return ((uint64_t)f2key(z) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
-// Clears the select histograms (counts, and masses when asked); caller barriers.
-__device__ __forceinline__ void clear_sel(RgFinalS& S, bool masses) {
-  for (int i = threadIdx.x; i < SELB; i += NT) {
-    S.cnt[i] = 0u;
-    if (masses) S.mass[i] = 0ull;
-  }
-}
+__device__ __forceinline__ int key_index(uint64_t k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
+__device__ __forceinline__ uint32_t key_z(uint64_t k) { return (uint32_t)(k >> 32); }
 
-// kk-th largest present key (1 <= kk <= number present).
-template <typename PF>
-__device__ uint32_t sel_count(const uint32_t (&ck)[FPT], PF present, uint32_t kk, RgFinalS& S) {
-  const Range R = key_range(ck, present, S);
-  if (R.bits == 0) { __syncthreads(); return R.base; }
-  uint32_t hi = 0, need = kk;
-  int top = R.bits;
-  while (top > 0) {
-    const int sh = top > SELD ? top - SELD : 0;
-    const int dw = top - sh;
-    clear_sel(S, false);
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < FPT; e++) {
-      if (present(e)) {
-        const uint32_t d = ck[e] - R.base;
-        const uint32_t up = top >= 32 ? 0u : (d >> top);
-        if (up == hi) atomicAdd(&S.cnt[(d >> sh) & ((1u << dw) - 1u)], 1u);
+// Appends this lane's (x, index) to this wave's segment of list l when on:
+// one ballot per slot gives every lane its position (slot order, then lane
+// order).  n is the wave's running count (wave-uniform).
+__device__ __forceinline__ void seg_put(RgLists& L, int l, bool on, uint32_t& n, float x, int idx) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(on);
+  if (m) {
+    if (on) {
+      const uint32_t p = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (p < (uint32_t)SEGCAP) {
+        L.si[l][threadIdx.x >> 6][p] = idx;
+        L.sx[l][threadIdx.x >> 6][p] = __float_as_uint(x);
       }
     }
-    __syncthreads();
-    // bins from the top: thread t owns descending bins SPT t .. SPT t + SPT - 1
-    const int nb = 1 << dw;
-    uint32_t cc[SPT], loc = 0;
-#pragma unroll
-    for (int i = 0; i < SPT; i++) {
-      const int b = nb - 1 - SPT * (int)threadIdx.x - i;
-      cc[i] = b >= 0 ? S.cnt[b] : 0u;
-      loc += cc[i];
-    }
-    uint32_t tot;
-    uint32_t ex = bscan<uint32_t>(loc, &tot, S.u);
-#pragma unroll
-    for (int i = 0; i < SPT; i++) {
-      const int b = nb - 1 - SPT * (int)threadIdx.x - i;
-      if (b >= 0 && ex < need && need <= ex + cc[i]) { S.mi[0] = b; S.mi[1] = (int)ex; }
-      ex += cc[i];
-    }
-    __syncthreads();
-    hi = (hi << dw) | (uint32_t)S.mi[0];
-    need -= (uint32_t)S.mi[1];
-    top = sh;
-    __syncthreads();
+    n += (uint32_t)__popcll(m);
   }
-  return R.base + hi;
+}
+// A wave's segment count (lane 0 of the wave); SEGCAP + 1 marks an overflow.
+__device__ __forceinline__ void seg_done(RgLists& L, int l, uint32_t n) {
+  if ((threadIdx.x & 63) == 0) L.scnt[l][threadIdx.x >> 6] = n > (uint32_t)SEGCAP ? SEGCAP + 1 : (int)n;
 }
 
-// Mass-weighted select: the largest present key v with A + mass(key >= v) > P
-// (requires A <= P < A + total present mass; ok = 0 otherwise).  above =
-// A + mass(key > v); ceq / meq = count and mass of key == v.
-struct MassSel {
-  uint32_t key;
-  uint64_t above;
-  uint32_t ceq;
-  uint64_t meq;
-  int ok;
-};
-template <typename PF>
-__device__ MassSel sel_mass(const uint32_t (&ck)[FPT], const uint64_t (&cm)[FPT], PF present, uint64_t A, uint64_t P,
-                            RgFinalS& S) {
-  MassSel ms{0u, A, 0u, 0ull, 0};
-  const Range R = key_range(ck, present, S);
-  uint32_t hi = 0;
-  int top = R.bits;
-  for (;;) {
-    const int sh = top > SELD ? top - SELD : 0;
-    const int dw = top - sh;
-    clear_sel(S, true);
-    if (threadIdx.x == 0) S.mi[0] = -1;
-    __syncthreads();
+// Sorts the chunk's lists l < nl (their wave segments complete; the caller
+// barriers after seg_done) by key, descending, and writes them to dst: list 0
+// at [0, np0), list 1 at [np0, np0 + np1), entries {z key, index, x bits, 0}.  List 0
+// stops after rank lim0 - 1 and the entries whose z equals that entry's z
+// (lim0 = 0: no limit).  np[l] receives the counts; returns false when a
+// segment overflowed or the lists exceed cap (nothing written then).
+// Every thread calls it; it ends with a barrier.
+__device__ __forceinline__ bool sort_publish(RgLists& L, RgX& X, int nl, int lim0, bool greedy, float T, uint4* dst, int cap,
+                                             int (&np)[2]) {
+  const int tid = threadIdx.x;
+  int n[2] = {0, 0}, pre[2][NW];
+  bool over = false;
 #pragma unroll
-    for (int e = 0; e < FPT; e++) {
-      if (present(e)) {
-        const uint32_t d = ck[e] - R.base;
-        const uint32_t up = top >= 32 ? 0u : (d >> top);
-        if (up == hi) {
-          const uint32_t b = dw > 0 ? ((d >> sh) & ((1u << dw) - 1u)) : 0u;
-          atomicAdd(&S.cnt[b], 1u);
-          if (cm[e]) atomicAdd(&S.mass[b], (unsigned long long)cm[e]);
-        }
-      }
-    }
-    __syncthreads();
-    const int nb = 1 << dw;
-    uint64_t mm[SPT], loc = 0;
+  for (int l = 0; l < 2; l++)
 #pragma unroll
-    for (int i = 0; i < SPT; i++) {
-      const int b = nb - 1 - SPT * (int)threadIdx.x - i;
-      mm[i] = b >= 0 ? S.mass[b] : 0ull;
-      loc += mm[i];
+    for (int w = 0; w < NW; w++) {
+      const int c = l < nl ? L.scnt[l][w] : 0;
+      over |= c > SEGCAP;
+      pre[l][w] = n[l];
+      n[l] += c > SEGCAP ? SEGCAP : c;
     }
-    uint64_t tot;
-    uint64_t ex = ms.above + bscan<uint64_t>(loc, &tot, S.q);
-#pragma unroll
-    for (int i = 0; i < SPT; i++) {
-      const int b = nb - 1 - SPT * (int)threadIdx.x - i;
-      if (b >= 0 && ex <= P && P < ex + mm[i]) { S.mi[0] = b; S.mi[1] = (int)S.cnt[b]; S.mq[0] = ex; S.mq[1] = mm[i]; }
-      ex += mm[i];
-    }
+  if (over || n[0] + n[1] > cap) {
+    np[0] = np[1] = 0;
     __syncthreads();
-    if (S.mi[0] < 0) { __syncthreads(); return ms; }
-    hi = (hi << dw) | (uint32_t)S.mi[0];
-    ms.above = S.mq[0];
-    ms.ceq = (uint32_t)S.mi[1];
-    ms.meq = S.mq[1];
-    top = sh;
-    __syncthreads();
-    if (top == 0) break;
+    return false;
   }
-  ms.key = R.base + hi;
-  ms.ok = 1;
-  return ms;
+  // compact the segments (entry f of list l: the segment whose prefix holds it)
+#pragma unroll
+  for (int l = 0; l < 2; l++) {
+    for (int f = tid; f < n[l]; f += NT) {
+      int w = 0, b = 0;
+#pragma unroll
+      for (int q = 1; q < NW; q++) {
+        const bool in = f >= pre[l][q];
+        w = in ? q : w;
+        b = in ? pre[l][q] : b;
+      }
+      const uint32_t xb = L.sx[l][w][f - b];
+      L.ck[l][f] = cand_key(__uint_as_float(xb), L.si[l][w][f - b], greedy, T);
+      L.cx[l][f] = xb;
+    }
+  }
+  if (tid == 0) X.mi[8] = 0x7FFFFFFF;
+  __syncthreads();
+  // ranks: 2^lg adjacent lanes share an entry, each counting the keys above it
+  // in one slice of its list; list 1 (when present) follows list 0 in the
+  // entry numbering
+  const int N = n[0] + n[1];
+  const int lg = N <= 64 ? 3 : N <= 128 ? 2 : N <= 256 ? 1 : 0;
+  const int per = NT >> lg, part = tid & ((1 << lg) - 1);
+  int rk[CLMAX * 2 / NT];
+  int np0 = n[0];
+#pragma unroll
+  for (int it = 0; it < CLMAX * 2 / NT; it++) {
+    rk[it] = -1;
+    const int e = (tid >> lg) + it * per;
+    if (it * per >= N) continue;
+    int rank = 0;
+    if (e < N) {
+      const int l = e < n[0] ? 0 : 1;
+      const int f = l ? e - n[0] : e;
+      const int nl_ = l ? n[1] : n[0];
+      const uint64_t* ck = L.ck[l];
+      const uint64_t key = ck[f];
+      const int len = (nl_ + (1 << lg) - 1) >> lg;
+      const int q1 = min(nl_, part * len + len);
+      int q = part * len;
+      for (; q + 4 <= q1; q += 4) {
+        const uint64_t a0 = ck[q], a1 = ck[q + 1], a2 = ck[q + 2], a3 = ck[q + 3];
+        rank += (a0 > key ? 1 : 0) + (a1 > key ? 1 : 0) + (a2 > key ? 1 : 0) + (a3 > key ? 1 : 0);
+      }
+      for (; q < q1; q++) rank += ck[q] > key ? 1 : 0;
+    }
+    for (int o = 1; o < (1 << lg); o <<= 1) rank += __shfl_xor(rank, o);
+    rk[it] = e < N ? rank : -1;
+    // list 0's limit: the z key of the entry ranked lim0 - 1
+    if (e < n[0] && part == 0 && lim0 > 0 && rank == lim0 - 1) X.mi[9] = (int)key_z(L.ck[0][e]);
+  }
+  if (lim0 > 0 && lim0 < n[0]) {
+    __syncthreads();
+    // entries ranked from lim0 on stay when tied in z with the entry ranked lim0 - 1:
+    // their ranks are contiguous, so the count is the first rank of a lower z
+    const uint32_t zl = (uint32_t)X.mi[9];
+    int first_out = 0x7FFFFFFF;
+#pragma unroll
+    for (int it = 0; it < CLMAX * 2 / NT; it++) {
+      const int e = (tid >> lg) + it * per;
+      if (part == 0 && rk[it] >= lim0 && e < n[0] && key_z(L.ck[0][e]) != zl) first_out = min(first_out, rk[it]);
+    }
+    if (first_out != 0x7FFFFFFF) atomicMin(&X.mi[8], first_out);
+    __syncthreads();
+    np0 = min(n[0], X.mi[8]);
+  }
+  // write in sorted order
+#pragma unroll
+  for (int it = 0; it < CLMAX * 2 / NT; it++) {
+    const int e = (tid >> lg) + it * per;
+    if (part != 0 || rk[it] < 0 || e >= N) continue;
+    const int l = e < n[0] ? 0 : 1;
+    const int f = l ? e - n[0] : e;
+    if (l == 0 && rk[it] >= np0) continue;
+    const uint64_t key = L.ck[l][f];
+    dst[(l ? np0 : 0) + rk[it]] = make_uint4(key_z(key), (uint32_t)key_index(key), L.cx[l][f], 0u);
+  }
+  np[0] = np0;
+  np[1] = n[1];
+  __syncthreads();
+  return true;
 }
 
 // The division-collision group of z = fl(x0 / T): [lo, hi] of every x with

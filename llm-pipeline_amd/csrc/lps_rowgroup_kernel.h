@@ -17,7 +17,8 @@ __device__ __forceinline__ bool wait_count(uint32_t* p, uint32_t n) {
 // Chunk phase.  Returns the row's mode (MODE_DEFER: nothing published).
 // ===========================================================================
 template <int DT, int VPE, int NE>
-__device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j) {
+__device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j,
+                                           const RowCfg& g) {
   using CK = Chk<DT, VPE, NE>;
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -31,7 +32,6 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   // ---- the row's parameters and first history ids, then the chunk's loads ----
   // (issued first so that they are not queued behind the chunk's 16-byte loads)
   RG_STAMP(0);
-  const RowCfg g = row_cfg(P, r);
   const int32_t* hrow0 = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
   const int hid = (hrow0 && (int64_t)tid < P.history_stride) ? hrow0[tid] : -1;
   CK C;
@@ -41,13 +41,13 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   const int mode = g.mode;
   const bool greedy = g.greedy;
   const float T = g.T;
-  const float c = __fdiv_rn(kLog2e, greedy ? 1.0f : T);
+  const float c = g.c;
   uint32_t flags = 0;
 
   // ---- penalties ----
   if (g.pen) {
     if (!build_counts<NE>(S, g.hrow, g.hlen, tid < g.hlen ? hid : -1, v0 * VPE, nv * VPE)) flags |= RF_HISTORY;
-    apply_counts(C, S.hc, nv, g.rep, g.pres, g.freq);
+    apply_counts(C, S.a.hc, nv, g.rep, g.pres, g.freq);
   }
 
   RG_STAMP(1);
@@ -57,7 +57,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   for (int s = 0; s < NE; s++) tm = fmaxf(tm, C.x[s]);
   const bool hist_mode = mode == MODE_NUCLEUS || mode == MODE_PURE;
   if (hist_mode) {  // clear the histogram before the barrier of the max
-    u32x4* h4 = reinterpret_cast<u32x4*>(S.hist);
+    u32x4* h4 = reinterpret_cast<u32x4*>(S.a.hist);
 #pragma unroll
     for (int i = 0; i < HB * 8 / 16 / NT; i++) h4[i * NT + tid] = u32x4{0u, 0u, 0u, 0u};
   }
@@ -72,10 +72,8 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   sm.ref = ref;
   sm.xcc = xcc_id();
   sm.reg[0] = sm.reg[1] = sm.reg[2] = sm.reg[3] = 1 << 30;
-  // this wave's candidate segment
-  const uint32_t wcap = (uint32_t)(F.capw / NW);
-  uint2* wseg = F.cands + (int64_t)r * CAPR + (int64_t)j * F.capw + (int64_t)wv * wcap;
-  uint32_t wn = 0;
+  // this chunk's published lists
+  uint4* cbase = F.cands + (int64_t)r * CAPR + (int64_t)j * F.capw;
   const bool want_lp = P.chosen_logprob || g.ntop > 0;
   RG_STAMP(14);
 
@@ -127,12 +125,19 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       const uint32_t v1[1] = {f2key(tm)};
       const uint32_t wth = wave_kth_largest<1>(v1, m);
       uint32_t th = bred(wth, S.u, OpMin{});
+      RG_STAMP(12);
       if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
       // -inf is never a candidate (it has no mass); NaN always is (!(x < t))
       const float xth = fmaxf(key2f(th), -3.40282347e38f);
-      wn = wave_emit<NE>([&](int s) { return !(C.x[s] < xth); },
-                         [&](int s) { return make_uint2(__float_as_uint(C.x[s]), (uint32_t)CK::index(v0, s)); },
-                         wseg, wcap);
+      uint32_t n = 0;
+#pragma unroll
+      for (int s = 0; s < NE; s++) seg_put(S.l, 0, !(C.x[s] < xth), n, C.x[s], CK::index(v0, s));
+      seg_done(S.l, 0, n);
+      __syncthreads();
+      RG_STAMP(13);
+      int np[2];
+      if (!sort_publish(S.l, S, 1, g.kprime, greedy, T, cbase, F.capw, np)) flags |= RF_OVERFLOW;
+      sm.n1 = (uint16_t)np[0];
     }
   }
 
@@ -150,7 +155,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
         const float e = emass(C.x[s], c, ref);
         const uint32_t b = ebin(e);
         // masses under the histogram go to a per-lane spare slot (no branch, no conflicts)
-        atomicAdd(&S.hist[b != BELOW ? b : (uint32_t)(HB + lane)],
+        atomicAdd(&S.a.hist[b != BELOW ? b : (uint32_t)(HB + lane)],
                   (1ull << 48) | (unsigned long long)(__float_as_uint(e) & 0xFFFFu));
         zlow += b == BELOW ? e : 0.0f;
         bins[s >> 1] |= b << (16 * (s & 1));
@@ -168,7 +173,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
 #pragma unroll
       for (int i = 0; i < HLT; i++) {
         const int b = tid + NT * i;
-        const unsigned long long a = S.hist[b];
+        const unsigned long long a = S.a.hist[b];
         double m = bin_mass_u(b, a);
         if (b == HB_NAN) { nanc = (uint32_t)(a >> 48); m = 0.0; }
         zs += m;
@@ -254,7 +259,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
 #pragma unroll
     for (int i = 0; i < HPT; i++) msum += mrg[i];
     double stot;
-    const double sx = bscan<double>(msum, &stot, S.d2);
+    const double sx = bscan<NW, double>(msum, &stot, S.d2);
     // ---- regions: bins whose cumulative interval meets the targets ----
     const double eps = 1e-6 * Z;
     const bool nuc = mode == MODE_NUCLEUS;
@@ -322,7 +327,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
 #pragma unroll
     for (int i = 0; i < HLT; i++) {
       const int b = tid + NT * i;
-      const unsigned long long a = S.hist[b];
+      const unsigned long long a = S.a.hist[b];
       const double m = b == HB_NAN ? 0.0 : bin_mass_u(b, a);
       if (b > h1 && b != HB_NAN) { ab1 += m; nab += (uint32_t)(a >> 48); }
       if (b > h2) ab2 += m;
@@ -336,53 +341,51 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     sm.ab1 = 0.0; sm.ab2 = 0.0; sm.nab1 = 0;
 #pragma unroll
     for (int i = 0; i < NW; i++) { sm.ab1 += S.d4[i]; sm.ab2 += S.d5[i]; sm.nab1 += S.u4[i]; }
-    if (Mfin) {
-      // the elements of either region, published by wave ballots (bins in pairs)
-      static_assert(NE % 2 == 0, "bin pairs");
-      uint32_t L1, C1, L2, C2;
-      region_pair(l1, h1, L1, C1);
-      region_pair(l2, h2, L2, C2);
-      uint32_t n = 0;
+    // the elements of either region: list 0 (region 1, nucleus rows) and
+    // list 1 (region 2, unless the draw is skipped), tested on bin pairs
+    static_assert(NE % 2 == 0, "bin pairs");
+    uint32_t L1, C1, L2, C2;
+    region_pair(l1, h1, L1, C1);
+    region_pair(l2, h2, L2, C2);
+    if (!Mfin) C1 = 0u;
+    if (!Mfin || P.skip_draw) C2 = 0u;
+    uint32_t n1 = 0, n2 = 0;
 #pragma unroll
-      for (int k = 0; k < NE / 2; k++) {
-        const uint32_t t1 = in_region2(bins[k], L1, C1), t2 = in_region2(bins[k], L2, C2);
-        const uint32_t sl = t1 | t2;
+    for (int k = 0; k < NE / 2; k++) {
+      const uint32_t t1 = in_region2(bins[k], L1, C1), t2 = in_region2(bins[k], L2, C2);
+      if (__builtin_amdgcn_ballot_w64((t1 | t2) != 0u) == 0ull) continue;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const bool on = (sl >> (16 * h) & 0xFFFFu) != 0u;
-          const uint64_t m = __builtin_amdgcn_ballot_w64(on);
-          if (m) {
-            if (on) {
-              const uint32_t p =
-                  n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-              const int s2 = 2 * k + h;
-              const uint32_t f = ((t1 >> (16 * h) & 0xFFFFu) ? (1u << 30) : 0u) |
-                                 ((t2 >> (16 * h) & 0xFFFFu) ? (1u << 31) : 0u);
-              if (p < wcap) wseg[p] = make_uint2(__float_as_uint(C.x[s2]), (uint32_t)CK::index(v0, s2) | f);
-            }
-            n += (uint32_t)__popcll(m);
-          }
-        }
+      for (int h = 0; h < 2; h++) {
+        const int s2 = 2 * k + h;
+        seg_put(S.l, 0, (t1 >> (16 * h) & 0xFFFFu) != 0u, n1, C.x[s2], CK::index(v0, s2));
+        seg_put(S.l, 1, (t2 >> (16 * h) & 0xFFFFu) != 0u, n2, C.x[s2], CK::index(v0, s2));
       }
-      wn = n;
     }
+    seg_done(S.l, 0, n1);
+    seg_done(S.l, 1, n2);
+    __syncthreads();
+    RG_STAMP(13);
+    int np[2];
+    if (!sort_publish(S.l, S, 2, 0, false, T, cbase, F.capw, np)) flags |= RF_OVERFLOW;
+    sm.n1 = (uint16_t)np[0];
+    sm.n2 = (uint16_t)np[1];
   }
 
   // ---- the chunk's summary, then the arrival count ----
   RG_STAMP(7);
   sm.flags = flags;
   if (tid == 0) store_sum(sums + MAXG + j, sm);
-  store_wave_count(sums + MAXG + j, wn, wcap);
   return mode;
 }
 
-// Block-wide penalised logit of one id (legality bit, history count).
+// Penalised logit of one id (legality bit, history count), computed by the
+// finaliser's FT threads.
 template <int DT>
-__device__ float penal_logit(const KParams& P, const RowCfg& g, const char* row, int r, int id, RgX& S) {
+__device__ __forceinline__ float penal_logit(const KParams& P, const RowCfg& g, const char* row, int r, int id, RgX& S) {
   uint32_t c = 0;
   if (g.pen)
-    for (int k = threadIdx.x; k < g.hlen; k += NT) c += g.hrow[k] == id ? 1u : 0u;
-  c = bred(c, S.u2, OpAdd{});
+    for (int k = threadIdx.x; k < g.hlen; k += FT) c += g.hrow[k] == id ? 1u : 0u;
+  c = bred<FW>(c, S.u2, OpAdd{});
   float x = load1<DT>(row, id);
   if (!id_allowed(row_allowed(P, r), id)) x = -INFINITY;
   if (g.pen && c) x = penalize(x, (int)c, g.rep, g.pres, g.freq);
@@ -394,91 +397,235 @@ __device__ float penal_logit(const KParams& P, const RowCfg& g, const char* row,
 // Finaliser: the last chunk workgroup of row r.  Returns 0 when the row is
 // done, else a reason code (the row is then sampled by the general kernel).
 // ===========================================================================
+// First position in [lo, hi) where pred holds, for a predicate that is false
+// then true over the range (hi when it never holds), found by one wave with
+// ballots: 64 blocks per level, two levels for ranges up to 4096.  Every lane
+// of the wave calls it with the same arguments; no barrier.
+template <class Pr>
+__device__ __forceinline__ int wave_first_true(int lo, int hi, Pr pred) {
+  const int lane = threadIdx.x & 63;
+  int n = hi - lo;
+  if (n <= 0) return hi;
+  if (n > 64) {
+    // lane i tests the last position of block i (blocks of bs)
+    const int bs = (n + 63) >> 6;
+    const int q = min(lo + (lane + 1) * bs, hi) - 1;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pred(q));
+    if (!m) return hi;
+    const int b = (int)__builtin_ctzll(m);
+    const int nlo = lo + b * bs;
+    hi = min(lo + (b + 1) * bs, hi);  // pred(hi - 1) holds
+    lo = nlo;
+    n = hi - lo;
+  }
+  const uint64_t m = __builtin_amdgcn_ballot_w64(lane < n && pred(lo + lane));
+  return m ? lo + (int)__builtin_ctzll(m) : hi;
+}
+// Exclusive prefix over the finaliser's FT threads in thread order of two
+// values at once (one barrier); t0 / t1 get the totals.
+__device__ __forceinline__ void bscan2(uint64_t v0, uint64_t v1, uint64_t& e0, uint64_t& e1, uint64_t& t0, uint64_t& t1,
+                                       uint64_t* s0, uint64_t* s1) {
+  const uint64_t i0 = wscan_incl(v0), i1 = wscan_incl(v1);
+  if (lane_id() == 63) { s0[wave_id()] = i0; s1[wave_id()] = i1; }
+  __syncthreads();
+  uint64_t o0 = 0, o1 = 0, a0 = 0, a1 = 0;
+#pragma unroll
+  for (int i = 0; i < FW; i++) {
+    const uint64_t x0 = s0[i], x1 = s1[i];
+    o0 += (i < wave_id()) ? x0 : 0ull;
+    o1 += (i < wave_id()) ? x1 : 0ull;
+    a0 += x0;
+    a1 += x1;
+  }
+  e0 = o0 + i0 - v0;
+  e1 = o1 + i1 - v1;
+  t0 = a0;
+  t1 = a1;
+}
+// Inclusive prefixes of the masses of merged lists 0 and 1 over positions
+// [0, n0) and [0, n1): thread t holds positions KPT t .. KPT t + KPT - 1.
+// Ends with a barrier.
+__device__ __forceinline__ void scan_lists(RgFinalS& S, int n0, int n1) {
+  uint64_t m0[KPT], m1[KPT], l0 = 0, l1 = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int p = KPT * (int)threadIdx.x + i;
+    m0[i] = p < n0 ? S.sm[0][p] : 0ull;
+    m1[i] = p < n1 ? S.sm[1][p] : 0ull;
+    l0 += m0[i];
+    l1 += m1[i];
+  }
+  uint64_t e0, e1, t0, t1;
+  bscan2(l0, l1, e0, e1, t0, t1, S.q, S.q2);
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int p = KPT * (int)threadIdx.x + i;
+    e0 += m0[i];
+    e1 += m1[i];
+    if (p < n0) S.sc[0][p] = e0;
+    if (p < n1) S.sc[1][p] = e1;
+  }
+  __syncthreads();
+}
+// Merges the loaded lists (S.lk[l], chunk q's sorted list at [cb[q], cb[q] +
+// cn[q])) into sorted order: entry f of list l (chunk c, position p) has rank
+// p plus the entries above it in every other chunk's list, found by a
+// binary search there (2^D bounds the lists' lengths).  The FT threads take
+// the entries of both lists densely; the searches of one entry in the other
+// chunks run in one loop, so their reads are issued together.  Each entry is
+// written to its rank (ranks >= KM are dropped) with its logit and mass.
+template <int MG>
+__device__ __forceinline__ void merge_lists(RgFinalS& S, int G, int D, int N0, int N1, float Rm) {
+  int cn[2][MG], cb[2][MG];
+#pragma unroll
+  for (int q = 0; q < MG; q++) {
+    cn[0][q] = q < G ? S.cn[0][q] : 0;
+    cn[1][q] = q < G ? S.cn[1][q] : 0;
+    cb[0][q] = q < G ? S.cb[0][q] : 0;
+    cb[1][q] = q < G ? S.cb[1][q] : 0;
+  }
+  for (int f = threadIdx.x; f < N0 + N1; f += FT) {
+    const int l = f < N0 ? 0 : 1;
+    const int fl = l ? f - N0 : f;
+    // the entry's chunk: the last with cb <= fl
+    int c = 0;
+#pragma unroll
+    for (int q = 1; q < MG; q++) c = (q < G && (l ? cb[1][q] : cb[0][q]) <= fl) ? q : c;
+    const uint64_t key = S.lk[l][fl];
+    int ps[MG];
+#pragma unroll
+    for (int q = 0; q < MG; q++) ps[q] = 0;
+    for (int sb = D - 1; sb >= 0; sb--) {
+      const int step = 1 << sb;
+      uint64_t v[MG];
+#pragma unroll
+      for (int q = 0; q < MG; q++) {
+        const int n = l ? cn[1][q] : cn[0][q], bq = l ? cb[1][q] : cb[0][q];
+        v[q] = S.lk[l][bq + min(ps[q] + step, max(n, 1)) - 1];
+      }
+#pragma unroll
+      for (int q = 0; q < MG; q++) {
+        const int n = l ? cn[1][q] : cn[0][q];
+        const int t = ps[q] + step;
+        ps[q] = (q != c && t <= n && v[q] > key) ? t : ps[q];
+      }
+    }
+    int rank = fl - (l ? cb[1][0] : cb[0][0]);
+#pragma unroll
+    for (int q = 1; q < MG; q++) rank = q == c ? fl - (l ? cb[1][q] : cb[0][q]) : rank;
+#pragma unroll
+    for (int q = 0; q < MG; q++) rank += ps[q];
+    if (rank < KM) {
+      S.sk[l][rank] = key;
+      S.sx[l][rank] = S.lx[l][fl];
+      S.sm[l][rank] = zmass_fix(key2f(key_z(key)), Rm);
+    }
+  }
+}
+__device__ __forceinline__ void merge_lists_g(RgFinalS& S, int G, int D, int N0, int N1, float Rm) {
+  if (G <= 2) merge_lists<2>(S, G, D, N0, N1, Rm);
+  else if (G <= 4) merge_lists<4>(S, G, D, N0, N1, Rm);
+  else if (G <= 8) merge_lists<8>(S, G, D, N0, N1, Rm);
+  else merge_lists<MAXG>(S, G, D, N0, N1, Rm);
+}
+
 template <int DT, int VPE>
-__device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r) {
+__device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g) {
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = F.G;
   const int V = P.V;
   const char* row = row_ptr<DT>(P, r);
   const RgSum* sums = F.sums + (int64_t)r * 2 * MAXG + MAXG;
-  const uint2* cands = F.cands + (int64_t)r * CAPR;
+  const uint4* cands = F.cands + (int64_t)r * CAPR;
   if (tid == 0) {  // the row's counters back to zero for the next launch
     F.counters[(int64_t)r * 32] = 0u;
     F.counters[(int64_t)r * 32 + 2] = 0u;
   }
-  const RowCfg g = row_cfg(P, r);
   const int mode = g.mode;
   const bool greedy = g.greedy;
   const float T = g.T;
-  const float c = __fdiv_rn(kLog2e, greedy ? 1.0f : T);
-
-  // ---- candidates, first pass: entry k0 of wave segment s0, loaded before the
-  // counts are known (in flight with the summaries); the rest after them ----
+  const float c = g.c;
   const int capw = F.capw;
-  const int nseg = G * NW;
-  const int lgK = 31 - __builtin_clz(NT / nseg);  // entries per segment in the first pass
-  const int s0 = tid >> lgK, k0 = tid & ((1 << lgK) - 1);
-  auto seg_slot = [&](int sg, int k) -> int { return (sg / NW) * capw + (sg % NW) * (capw / NW) + k; };
-  uint2 cv0 = make_uint2(0u, 0u);
-  if (s0 < nseg) cv0 = ld_pub(cands + seg_slot(s0, k0));
 
-  // ---- F1: the chunk summaries (wave 0) ----
+  // ---- first pass of the lists, loaded before their lengths are known (in
+  // flight with the summaries): entry i < K0 of chunk c is flat entry
+  // f = c K0 + i, held by thread f % FT in slot f / FT (slots < FP1) ----
+  const int lgK = 31 - __builtin_clz((FP1 * FT) / G);
+  const int K0 = 1 << lgK;
+  uint4 cv[FPT];
+#pragma unroll
+  for (int e = 0; e < FP1; e++) {
+    const int f = e * FT + tid, c0 = f >> lgK;
+    cv[e] = c0 < G ? ld_pub(cands + c0 * capw + (f & (K0 - 1))) : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int e = FP1; e < FPT; e++) cv[e] = make_uint4(0u, 0u, 0u, 0u);
+
+  // ---- F1: the chunk summaries (wave 0; lane q < G holds chunk q's).  The
+  // chunks are combined with readlanes, field by field, so the combines of
+  // different fields are independent ----
   if (wv == 0) {
     RgSum a{};
     if (lane < G) a = ld_pub(sums + lane);
-    const uint32_t xm = wreduce(lane < G ? (1u << a.xcc) : 0u, OpOr{});
-    uint32_t fl = wreduce(lane < G ? a.flags : 0u, OpOr{});
+    uint32_t fl = 0, xm = 0, mk = 0, nab = 0, nanb = 0;
+    float R = -INFINITY;
+    int nmax = 0, n1b = 0, n2b = 0, ob = 0, n1t = 0, n2t = 0, ot = 0;
+    for (int q = 0; q < G; q++) {
+      fl |= rdlane(a.flags, q);
+      xm |= 1u << rdlane(a.xcc, q);
+      mk = max(mk, rdlane(a.mkey, q));
+      const float rq = rdlane(a.ref, q);
+      if (rq != INFINITY && rq != -INFINITY) R = fmaxf(R, rq);
+      nab += rdlane(a.nab1, q);
+      nanb = max(nanb, rdlane(a.nanbin, q));
+      const int c1 = (int)rdlane((uint32_t)a.n1, q), c2 = (int)rdlane((uint32_t)a.n2, q);
+      const int co = c1 + c2 > K0 ? c1 + c2 - K0 : 0;
+      nmax = max(nmax, max(c1, c2));
+      // this lane's prefixes (chunks before it)
+      n1b += q < lane ? c1 : 0;
+      n2b += q < lane ? c2 : 0;
+      ob += q < lane ? co : 0;
+      n1t += c1;
+      n2t += c2;
+      ot += co;
+    }
     if (__builtin_popcount(xm) > 1) fl |= RF_SPLIT;
-    const uint32_t mk = wmax(lane < G ? a.mkey : 0u);
-    const int am = wmin(lane < G && a.mkey == mk ? a.amax : 0x7FFFFFFF);
-    const bool af = lane < G && a.ref != INFINITY && a.ref != -INFINITY;
-    const float R = wmax(af ? a.ref : -INFINITY);
-    const double sc = af ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
-    const double Z = wsum(af ? a.zsum * sc : 0.0);
-    const double A1 = wsum(af ? a.ab1 * sc : 0.0);
-    const double A2 = wsum(af ? a.ab2 * sc : 0.0);
-    const uint32_t nab = wsum(lane < G ? a.nab1 : 0u);
-    const uint32_t nanb = wmax(lane < G ? a.nanbin : 0u);
-    // segment counts; overflow beyond the first pass, prefixed over segments
-    uint32_t ntot = 0, nover = 0, over = 0;
-    if (lane < G) {
-#pragma unroll
-      for (int q = 0; q < NW; q++) {
-        const uint32_t n = a.wc[q];
-        over |= n == WC_OVER ? 1u : 0u;
-        const uint32_t nn = n == WC_OVER ? 0u : n;
-        S.wpre[lane * NW + q] = (int)nn;
-        ntot += nn;
-        nover += nn > (1u << lgK) ? nn - (1u << lgK) : 0u;
+    int am = 0x7FFFFFFF;
+    double Z = 0.0, A1 = 0.0, A2 = 0.0;
+    for (int q = 0; q < G; q++) {
+      if (rdlane(a.mkey, q) == mk) am = min(am, (int)rdlane((uint32_t)a.amax, q));
+      const float rq = rdlane(a.ref, q);
+      if (rq != INFINITY && rq != -INFINITY) {
+        const double sc = ldexp(1.0, (int)(rq - R));
+        Z += rdlane(a.zsum, q) * sc;
+        A1 += rdlane(a.ab1, q) * sc;
+        A2 += rdlane(a.ab2, q) * sc;
       }
     }
-    if (wreduce(over, OpOr{})) fl |= RF_OVERFLOW;
-    const uint32_t ncand = wsum(ntot);
-    const uint32_t oinc = wscan_incl(nover);
     if (lane < G) {
-      uint32_t o = oinc - nover;
-#pragma unroll
-      for (int q = 0; q < NW; q++) {
-        const uint32_t nn = (uint32_t)S.wpre[lane * NW + q];
-        S.opre[lane * NW + q] = (int)o;
-        o += nn > (1u << lgK) ? nn - (1u << lgK) : 0u;
-      }
-      S.rf[lane] = af ? a.ref : -INFINITY;
+      S.cn[0][lane] = (int)a.n1;
+      S.cn[1][lane] = (int)a.n2;
+      S.cb[0][lane] = n1b;
+      S.cb[1][lane] = n2b;
+      S.opre[lane] = ob;
+      S.rf[lane] = (a.ref != INFINITY && a.ref != -INFINITY) ? a.ref : -INFINITY;
       S.rm[lane] = a.mkey == 0xFFFFFFFFu ? INFINITY : key2f(a.mkey);
     }
     if (lane == 0) {
+      S.cb[0][G] = n1t;
+      S.cb[1][G] = n2t;
+      S.opre[G] = ot;
       S.mi[16] = (int)fl;
       S.mi[17] = (int)mk;
       S.mi[18] = am;
       S.mi[19] = (int)nab;
       S.mi[20] = (int)nanb;
       S.mi[21] = a.reg[0]; S.mi[22] = a.reg[1]; S.mi[23] = a.reg[2]; S.mi[24] = a.reg[3];
-      S.mi[25] = (int)ncand;
+      S.mi[25] = nmax;
       S.md[0] = Z; S.md[1] = A1; S.md[2] = A2;
       S.mf[0] = R;
     }
-    if (lane == 63) S.mi[26] = (int)oinc;  // overflow entries of the row
   }
   __syncthreads();
   RG_STAMP(25);
@@ -493,121 +640,88 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     if (has_nan || xmax == INFINITY || __fdiv_rn(xmax, T) == INFINITY) status |= LPS_ROW_NONFINITE;
     else if (xmax == -INFINITY) status |= LPS_ROW_EMPTY;
   }
-  const float zmax = greedy ? xmax : __fdiv_rn(xmax, T);
+  const bool hmode = mode == MODE_NUCLEUS || mode == MODE_PURE;
   // the row's mass reference (logprob, nucleus and pure rows published theirs)
-  const float Rref = (mode == MODE_NUCLEUS || mode == MODE_PURE || S.mf[0] != -INFINITY)
+  const float Rref = (hmode || S.mf[0] != -INFINITY)
                          ? S.mf[0]
                          : (xmax != INFINITY && xmax != -INFINITY ? ceilf(__fmul_rn(xmax, c)) : 0.0f);
+  // masses of merged entries: against the row reference (nucleus, pure) or the
+  // row maximum (top-k)
+  const float Rm = hmode ? Rref : (xmax != INFINITY && xmax != -INFINITY ? ceilf(__fmul_rn(xmax, c)) : 0.0f);
   const double Zfull = S.md[0];
-  // ln of sum exp(z) over the row: Z is in units of 2^Rref of exp2(x c)
-  const double lnZ = Zfull > 0.0 ? log(Zfull) + (double)Rref * 0.6931471805599453 : 0.0;
   float u = g.u;
   if (!(u >= 0.0f)) u = 0.0f;
   if (u >= 1.0f) u = 0.99999994f;
+  const int N1 = S.cb[0][G], N2 = S.cb[1][G], NO = S.opre[G];
+  if (N1 > LKM || N2 > LKM || NO > (FPT - FP1) * FT) return 13;
+  const int D = 32 - __builtin_clz((uint32_t)max(S.mi[25], 1));
 
-  // ---- candidates in register slots e * NT + t: e = 0 the first pass, e >= 1
-  // the overflow entries (o = (e - 1) * NT + t of the row's overflow list) ----
-  uint32_t ck[FPT];
-  uint64_t cm[FPT];
-  uint32_t cf[FPT];  // region flags (nucleus)
-  const int NC = __builtin_amdgcn_readfirstlane(S.mi[25]);
-  const int NO = __builtin_amdgcn_readfirstlane(S.mi[26]);
-  if (NO > (FPT - 1) * NT) return 13;
-  const bool p0 = s0 < nseg && k0 < S.wpre[min(s0, nseg - 1)];
-  auto present = [&](int e) -> bool { return e == 0 ? p0 : (e - 1) * NT + tid < NO; };
-  // slot of overflow entry o: the last segment whose overflow prefix is <= o
-  auto over_slot = [&](int o) -> int {
-    int lo = 0, hi = nseg - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (S.opre[mid] <= o) lo = mid; else hi = mid - 1;
-    }
-    return seg_slot(lo, (1 << lgK) + o - S.opre[lo]);
-  };
+  // ---- the entries: slots e < FP1 the first pass, slots e >= FP1 the rest
+  // (entry o = (e - FP1) FT + tid of the row's overflow: chunk c with
+  // opre[c] <= o < opre[c + 1], index K0 + o - opre[c]) ----
   {
-    uint2 cv[FPT];
-    cv[0] = cv0;
+    int ci[FPT], ii[FPT];
 #pragma unroll
-    for (int e = 1; e < FPT; e++) {
-      cv[e] = make_uint2(0u, 0u);
-      if ((e - 1) * NT < NO && present(e)) cv[e] = ld_pub(cands + over_slot((e - 1) * NT + tid));
+    for (int e = 0; e < FPT; e++) {
+      ci[e] = -1;
+      ii[e] = 0;
+    }
+#pragma unroll
+    for (int e = 0; e < FP1; e++) {
+      const int f = e * FT + tid;
+      const int cc = f >> lgK, i = f & (K0 - 1);
+      const int ccc = min(cc, G - 1);
+      const bool pr = cc < G && i < S.cn[0][ccc] + S.cn[1][ccc];
+      ci[e] = pr ? cc : -1;
+      ii[e] = i;
+    }
+    if (NO > 0) {
+#pragma unroll
+      for (int e = FP1; e < FPT; e++) {
+        const int o = (e - FP1) * FT + tid;
+        if (o < NO) {
+          int cc = 0;
+          for (int q = 1; q < G; q++) cc = S.opre[q] <= o ? q : cc;
+          ci[e] = cc;
+          ii[e] = K0 + o - S.opre[cc];
+          cv[e] = ld_pub(cands + cc * capw + ii[e]);
+        }
+      }
     }
 #pragma unroll
     for (int e = 0; e < FPT; e++) {
-      ck[e] = 0u;
-      cf[e] = 0u;
-      cm[e] = 0ull;
-      if (e > 0 && (e - 1) * NT >= NO) continue;
-      const int sl = e * NT + tid;
-      const bool pr = present(e);
-      const float xv = __uint_as_float(cv[e].x);
-      const float zv = greedy ? xv : __fdiv_rn(xv, T);
-      ck[e] = pr ? f2key(zv) : 0u;
-      cf[e] = pr ? (cv[e].y >> 30) : 0u;
-      S.cidx[sl] = (int32_t)(cv[e].y & 0x3FFFFFFFu);
-      S.cx[sl] = xv;
-      // a candidate's mass is a function of its scaled logit z alone, so ids
-      // tied at one z weigh the same (the chunks' histograms used x; the two
-      // differ by a rounding or two)
-      cm[e] = (pr && (mode == MODE_NUCLEUS || mode == MODE_PURE)) ? zmass_fix(zv, Rref) : 0ull;
-      if (pr && xv != xv) status |= LPS_ROW_NONFINITE;
+      if (ci[e] < 0) continue;
+      const int cc = ci[e], i = ii[e];
+      const int n1c = S.cn[0][cc];
+      const int l = i < n1c ? 0 : 1;
+      const int p = l ? i - n1c : i;
+      const uint64_t key = ((uint64_t)cv[e].x << 32) | (uint64_t)(0xFFFFFFFFu - cv[e].y);
+      S.lk[l][S.cb[l][cc] + p] = key;
+      S.lx[l][S.cb[l][cc] + p] = cv[e].z;
+      const float xv = __uint_as_float(cv[e].z);
+      if (xv != xv) status |= LPS_ROW_NONFINITE;
     }
   }
-  status = bred(status, S.i1, OpOr{});
-  __syncthreads();
+  status = bred<FW>(status, S.i1, OpOr{});
   RG_STAMP(26);
   if (greedy) status = 0;
-  auto cidx = [&](int e) -> int { return S.cidx[e * NT + tid]; };
+
+  // ---- merge the chunks' sorted lists ----
+  RG_STAMP(16);
+  merge_lists_g(S, G, D, N1, N2, Rm);
+  __syncthreads();
+  RG_STAMP(27);
 
   int64_t token = -1;
   float cut = -INFINITY, qprob = 0.0f, chosen_z = NAN;
   int32_t ties = -1, kept_n = 0;
   int ntop_out = 0;
   const int64_t qtok = g.qtok;
+  const int K = min(N1, KM);  // merged positions of list 0 present
 
   if (status == 0 && g.kprime > 0) {
     // ======================= top-k (and top-N logprobs) =======================
-    const int keff = mode == MODE_TOPK ? (g.topk < V ? g.topk : V) : 0;
-    int kc = keff > g.ntop ? keff : g.ntop;
-    if (kc > NC) kc = NC;
-    if (kc <= 0) return 3;
-    const uint32_t kth = sel_count(ck, present, (uint32_t)kc, S);
-    RG_STAMP(27);
-    // the kept list: keys >= kth
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int e = 0; e < FPT; e++) cnt += (present(e) && ck[e] >= kth) ? 1u : 0u;
-    uint32_t K;
-    uint32_t p = bscan<uint32_t>(cnt, &K, S.u);
-    if (K > (uint32_t)KEPT) return 4;
-    const float Rt = xmax != INFINITY && xmax != -INFINITY ? ceilf(__fmul_rn(xmax, c)) : 0.0f;
-#pragma unroll
-    for (int e = 0; e < FPT; e++) {
-      if (present(e) && ck[e] >= kth) {
-        const int ix = cidx(e);
-        S.kkey[p] = ((uint64_t)ck[e] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)ix);
-        S.kmass[p] = zmass_fix(key2f(ck[e]), Rt);
-        p++;
-      }
-    }
-    __syncthreads();
-    // rank sort (keys are distinct: the index is part of the key)
-    for (int i = tid; i < (int)K; i += NT) {
-      const uint64_t ki = S.kkey[i];
-      int rank = 0;
-      int q = 0;
-      for (; q + 4 <= (int)K; q += 4) {
-        const uint64_t t0 = S.kkey[q], t1 = S.kkey[q + 1], t2 = S.kkey[q + 2], t3 = S.kkey[q + 3];
-        rank += (t0 > ki ? 1 : 0) + (t1 > ki ? 1 : 0) + (t2 > ki ? 1 : 0) + (t3 > ki ? 1 : 0);
-      }
-      for (; q < (int)K; q++) rank += S.kkey[q] > ki ? 1 : 0;
-      S.kord[rank] = i;
-    }
-    __syncthreads();
-    RG_STAMP(28);
-    auto kz = [&](int pos) -> uint32_t { return (uint32_t)(S.kkey[S.kord[pos]] >> 32); };
-    auto kix = [&](int pos) -> int { return (int)(0xFFFFFFFFu - (uint32_t)S.kkey[S.kord[pos]]); };
-    ntop_out = g.ntop < (int)K ? g.ntop : (int)K;
+    ntop_out = g.ntop < K ? g.ntop : K;
     if (mode == MODE_GREEDY) {
       token = gam;
       cut = xmax;
@@ -616,80 +730,62 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       qprob = (qtok >= 0 && qtok == gam) ? 1.0f : 0.0f;
       chosen_z = xmax;
     } else {
-      // the top-k set: sorted positions whose key reaches the keff-th
-      if (keff > (int)K || keff <= 0) return 5;
-      const uint32_t kk = kz(keff - 1);
-      int nk = (int)K;
-      {
-        int lastk = -1;
-        for (int pz = tid; pz < (int)K; pz += NT)
-          if (kz(pz) >= kk) lastk = max(lastk, pz);
-        nk = bred(lastk, S.i2, OpMax{}) + 1;
-      }
-      // inclusive prefix of the kept masses in sorted order
-      {
-        const uint64_t mv = tid < nk ? (uint64_t)S.kmass[S.kord[tid]] : 0ull;
-        uint64_t tot;
-        const uint64_t ex = bscan<uint64_t>(mv, &tot, S.q);
-        if (tid < nk) S.kcum[tid] = ex + mv;
-        __syncthreads();
-      }
-      const uint64_t Zk = S.kcum[nk - 1];
+      const int keff = g.topk < V ? g.topk : V;
+      if (keff > K || keff <= 0) return 5;
+      // the top-k set: every position whose z reaches the keff-th (ties kept)
+      const uint32_t kk = key_z(S.sk[0][keff - 1]);
+      const int nk = wave_first_true(keff, K, [&](int p) { return key_z(S.sk[0][p]) < kk; });
+      if (nk == K && K < N1) return 4;  // ties past the merged capacity
+      scan_lists(S, nk, 0);
+      const uint64_t Zk = S.sc[0][nk - 1];
       int nf = nk;
       if (g.topp < 1.0f) {  // keep sorted position p iff p == 0 or cum[p-1] <= top_p * Zk
         const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zk : 0.0;
         uint64_t limit = (uint64_t)pl;
         if (limit >= Zk) limit = Zk - 1;
-        int first = 0x7FFFFFFF;
-        if (tid >= 1 && tid < nk && S.kcum[tid - 1] > limit) first = tid;
-        nf = min(nf, bred(first, S.i3, OpMin{}));
-        __syncthreads();
+        nf = wave_first_true(1, nk, [&](int p) { return S.sc[0][p - 1] > limit; });
       }
       if (g.minp > 0.0f) {  // keep mass >= min_p * (the top mass)
-        const float e0 = (float)((double)S.kmass[S.kord[0]] / kFix);
+        const float e0 = (float)((double)S.sm[0][0] / kFix);
         int first = 0x7FFFFFFF;
-        if (tid < nf && (float)((double)S.kmass[S.kord[tid]] / kFix) < __fmul_rn(g.minp, e0)) first = tid;
-        const int f = bred(first, S.i1, OpMin{});
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+          const int p = KPT * tid + i;
+          if (p < nf && (float)((double)S.sm[0][p] / kFix) < __fmul_rn(g.minp, e0)) first = min(first, p);
+        }
+        const int f = bred<FW>(first, S.i2, OpMin{});
         if (f < nf) nf = f;
         if (nf == 0) status |= LPS_ROW_EMPTY;
       }
       // typical-p with top-k active: the row then holds -inf, and the reference keeps only the argmax
       if (status == 0 && g.typp < 1.0f) nf = 1;
       if (status == 0) {
-        const uint64_t Zf = S.kcum[nf - 1];
-        const uint32_t ckey = kz(nf - 1);
+        const uint64_t Zf = S.sc[0][nf - 1];
+        const uint32_t ckey = key_z(S.sk[0][nf - 1]);
         cut = key2f(ckey);
-        if (P.kept_ties || P.kept_count) {
-          uint32_t ea = 0, ek = 0, nfin = 0;
-          if (tid < (int)K) {
-            const uint32_t kq = kz(tid);
-            ea = kq == ckey ? 1u : 0u;
-            ek = (kq == ckey && tid < nf) ? 1u : 0u;
-            nfin = (tid < nf && kq != kNegInfKey) ? 1u : 0u;
-          }
-          ea = bred(ea, S.u, OpAdd{});
-          ek = bred(ek, S.u2, OpAdd{});
-          nfin = bred(nfin, S.u3, OpAdd{});
-          __syncthreads();
-          ties = ek == ea ? -1 : (int32_t)ek;
-          kept_n = (int32_t)nfin;
-        }
+        // ids tied with the last kept one: contiguous around it
+        const int f0 = wave_first_true(0, nf, [&](int p) { return key_z(S.sk[0][p]) <= ckey; });
+        const int l0 = wave_first_true(nf, K, [&](int p) { return key_z(S.sk[0][p]) < ckey; });
+        if (l0 == K && K < N1) return 4;
+        ties = (l0 - f0) == (nf - f0) ? -1 : (int32_t)(nf - f0);
+        kept_n = nf;
         // inverse CDF in sorted order
         uint64_t target = (uint64_t)((double)u * (double)Zf);
         if (target >= Zf) target = Zf - 1;
-        if (tid == 0) { S.mi[4] = nf - 1; S.mi[5] = -1; }
-        __syncthreads();
-        if (tid < nf) {
-          const uint64_t hi_ = S.kcum[tid], lo_ = tid > 0 ? S.kcum[tid - 1] : 0ull;
-          if (lo_ <= target && target < hi_) S.mi[4] = tid;
-          if (qtok >= 0 && kix(tid) == qtok) S.mi[5] = tid;
+        const int ps = wave_first_true(0, nf, [&](int p) { return S.sc[0][p] > target; });
+        token = key_index(S.sk[0][ps]);
+        chosen_z = key2f(key_z(S.sk[0][ps]));
+        if (qtok >= 0) {
+          if (tid == 0) S.mi[5] = -1;
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < KPT; i++) {
+            const int p = KPT * tid + i;
+            if (p < nf && key_index(S.sk[0][p]) == qtok) S.mi[5] = p;
+          }
+          __syncthreads();
+          if (S.mi[5] >= 0) qprob = (float)((double)S.sm[0][S.mi[5]] / (double)Zf);
         }
-        __syncthreads();
-        const int ps = S.mi[4];
-        token = kix(ps);
-        chosen_z = key2f(kz(ps));
-        if (S.mi[5] >= 0) qprob = (float)((double)S.kmass[S.kord[S.mi[5]]] / (double)Zf);
       }
     }
   } else if (status == 0 && mode == MODE_GREEDY) {
@@ -699,17 +795,20 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     kept_n = 1;
     qprob = (qtok >= 0 && qtok == gam) ? 1.0f : 0.0f;
     chosen_z = xmax;
-  } else if (status == 0 && (mode == MODE_NUCLEUS || mode == MODE_PURE)) {
+  } else if (status == 0 && hmode) {
     // ======================= nucleus / pure =======================
     const bool nuc = mode == MODE_NUCLEUS;
+    const bool want2 = !P.skip_draw;
     const int lo1 = S.mi[21], hi1 = S.mi[22], lo2 = S.mi[23], hi2 = S.mi[24];
     const double Z = S.md[0];
     const uint64_t Zfx = (uint64_t)(Z * kFix);
+    if ((nuc && N1 > KM) || (want2 && N2 > KM)) return 7;
     uint32_t vkey = 0, n_tie = kNoTie;
     uint64_t Zkept = Zfx;
+    int tie_lim = 0x7FFFFFFF;  // kept ids at the cut key: index <= tie_lim
     // whether every id whose z equals fl(x / T) lies inside row bins [lo, hi]
-    // under the binning of each chunk that can hold it (one wave)
-    // (one wave; lane w checks chunk w)
+    // under the binning of each chunk that can hold it (one wave; lane w
+    // checks chunk w)
     auto group_inside = [&](float x, int lo, int hi) -> bool {
       const Group gr = collision_group(x, T);
       bool bad = false;
@@ -725,230 +824,76 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       }
       return gr.ok != 0 && __builtin_amdgcn_ballot_w64(bad) == 0ull;
     };
-    // the kk-th lowest index among the candidates of key v selected by sel
-    auto kth_index = [&](auto sel, uint32_t v, uint32_t kk) -> int {
-      uint32_t ik[FPT];
-#pragma unroll
-      for (int e = 0; e < FPT; e++) ik[e] = (sel(e) && ck[e] == v) ? 0xFFFFFFFFu - (uint32_t)cidx(e) : 0u;
-      auto has = [&](int e) -> bool { return sel(e) && ck[e] == v; };
-      return (int)(0xFFFFFFFFu - sel_count(ik, has, kk, S));
-    };
-    int tie_lim = 0x7FFFFFFF;  // kept ids at the cut key: index <= tie_lim
-    const bool want2 = !P.skip_draw;
-    // ---- region lists: region 1 at kkey[0, N1), region 2 at kkey[N1, N1 + N2) ----
-    uint32_t c12 = 0;
-#pragma unroll
-    for (int e = 0; e < FPT; e++)
-      if (present(e)) c12 += ((nuc && (cf[e] & 1u)) ? 1u : 0u) + ((want2 && (cf[e] & 2u)) ? 0x10000u : 0u);
-    uint32_t t12;
-    const uint32_t p12 = bscan<uint32_t>(c12, &t12, S.u);
-    const int N1 = (int)(t12 & 0xFFFFu), N2 = (int)(t12 >> 16), NL = N1 + N2;
-    if (NL <= KEPT) {
-      // ======== lists: rank sort, exact prefix masses in sorted order ========
-      uint32_t q1 = p12 & 0xFFFFu, q2 = (uint32_t)N1 + (p12 >> 16);
-#pragma unroll
-      for (int e = 0; e < FPT; e++) {
-        if (!present(e)) continue;
-        const uint64_t key = ((uint64_t)ck[e] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)cidx(e));
-        if (nuc && (cf[e] & 1u)) { S.kkey[q1] = key; S.kmass[q1] = cm[e]; S.lslot[q1] = e * NT + tid; q1++; }
-        if (want2 && (cf[e] & 2u)) { S.kkey[q2] = key; S.kmass[q2] = cm[e]; S.lslot[q2] = e * NT + tid; q2++; }
-      }
-      if (tid == 0) S.mi[13] = -1;
-      __syncthreads();
-      RG_STAMP(16);
-      {  // rank sort: keys are distinct within a list (the index is part of the key);
-         // 2^lg adjacent lanes share an entry, each comparing one slice of its list
-        const int lg = NL <= 64 ? 3 : NL <= 128 ? 2 : NL <= 256 ? 1 : 0;
-        const int ie = tid >> lg, part = tid & ((1 << lg) - 1);
-        const int b = ie < N1 ? 0 : N1, n = ie < N1 ? N1 : N2;
-        int rank = 0;
-        if (ie < NL) {
-          const uint64_t ki = S.kkey[ie];
-          const int len = (n + (1 << lg) - 1) >> lg;
-          const int q1 = min(b + n, b + part * len + len);
-          int q = b + part * len;
-          for (; q + 8 <= q1; q += 8) {
-            uint64_t kq[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) kq[i] = S.kkey[q + i];
-#pragma unroll
-            for (int i = 0; i < 8; i++) rank += kq[i] > ki ? 1 : 0;
-          }
-          for (; q < q1; q++) rank += S.kkey[q] > ki ? 1 : 0;
-        }
-        for (int o = 1; o < (1 << lg); o <<= 1) rank += __shfl_xor(rank, o);
-        if (ie < NL && part == 0) S.kord[b + rank] = ie;
-      }
-      __syncthreads();
-      RG_STAMP(17);
-      {  // inclusive prefix of the masses in sorted order (list 2's from kcum[N1 - 1])
-        const uint64_t mv = tid < NL ? (uint64_t)S.kmass[S.kord[tid]] : 0ull;
-        uint64_t tot;
-        const uint64_t ex = bscan<uint64_t>(mv, &tot, S.q);
-        if (tid < NL) S.kcum[tid] = ex + mv;
-        __syncthreads();
-      }
-      RG_STAMP(27);
-      // every thread finds the cut and the draw by binary search over the
-      // prefixes; the two collision-group checks run on two waves at once
-      auto zkey_at = [&](int pos) -> uint32_t { return (uint32_t)(S.kkey[S.kord[pos]] >> 32); };
-      uint64_t ckey = 0;  // the last kept id's sort key
-      int qc = -1, pd = -1;
-      if (nuc) {
-        // sorted position p of the row is kept iff its exclusive prefix <= limit
-        const uint64_t A1 = (uint64_t)(S.md[1] * kFix);
-        const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zfx : 0.0;
-        uint64_t limit = (uint64_t)pl;
-        if (limit >= Zfx) limit = Zfx - 1;
-        int lo = 0, hi = N1;  // the first dropped position
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (A1 + (mid > 0 ? S.kcum[mid - 1] : 0ull) <= limit) lo = mid + 1; else hi = mid;
-        }
-        // the cut must fall inside the list: something kept, something dropped
-        if (lo == 0 || A1 + S.kcum[N1 - 1] <= limit) return 6;
-        qc = lo - 1;
-        ckey = S.kkey[S.kord[qc]];
-        vkey = (uint32_t)(ckey >> 32);
-        // the ids at the cut's z are contiguous around qc
-        int f0 = 0, f1 = qc;  // the first position with z key <= vkey
-        while (f0 < f1) {
-          const int mid = (f0 + f1) >> 1;
-          if (zkey_at(mid) <= vkey) f1 = mid; else f0 = mid + 1;
-        }
-        int l0 = qc + 1, l1 = N1;  // the first position with z key < vkey
-        while (l0 < l1) {
-          const int mid = (l0 + l1) >> 1;
-          if (zkey_at(mid) < vkey) l1 = mid; else l0 = mid + 1;
-        }
-        const uint32_t ea = (uint32_t)(l0 - f0), ek = (uint32_t)(qc + 1 - f0);
-        n_tie = ek == ea ? kNoTie : ek;
-        if (n_tie != kNoTie) tie_lim = (int)(0xFFFFFFFFu - (uint32_t)ckey);
-        Zkept = A1 + S.kcum[qc];
-        kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)lo);
-        ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
-        cut = key2f(vkey);
-      } else {
-        kept_n = -1;  // filled below when asked
-      }
-      if (want2) {
-        const uint64_t A2 = (uint64_t)(S.md[2] * kFix);
-        uint64_t target = (uint64_t)((double)u * (double)Zkept);
-        if (target >= Zkept) target = Zkept - 1;
-        const uint64_t b2 = N1 > 0 ? S.kcum[N1 - 1] : 0ull;
-        int lo = 0, hi = N2;  // the first position whose inclusive prefix passes the target
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (A2 + (S.kcum[N1 + mid] - b2) <= target) lo = mid + 1; else hi = mid;
-        }
-        if (lo == N2 || target < A2) return 9;
-        pd = lo;
-      }
-      if (wv == 0 && nuc) {  // the cut's collision group lies inside region 1 in every chunk
-        const bool ok = group_inside(S.cx[S.lslot[S.kord[qc]]], lo1, hi1);
-        if (lane == 0) S.mi[12] = ok ? 1 : 0;
-      }
-      if (wv == 1 && want2) {  // the drawn id's group inside region 2
-        const bool ok = group_inside(S.cx[S.lslot[S.kord[N1 + pd]]], lo2, hi2);
-        if (lane == 0) S.mi[14] = ok ? 1 : 0;
-      }
-      __syncthreads();
-      if (nuc && !S.mi[12]) return 8;
-      if (want2) {
-        if (!S.mi[14]) return 11;
-        const uint64_t dkey = S.kkey[S.kord[N1 + pd]];
-        token = (int64_t)(0xFFFFFFFFu - (uint32_t)dkey);
-        chosen_z = key2f((uint32_t)(dkey >> 32));
-        // the drawn id must be kept
-        if (nuc && dkey < ckey) return 12;
-      }
-      RG_STAMP(29);
-    } else if (nuc) {
-      // ---- the cut: exact mass select over the region-1 candidates ----
+    scan_lists(S, nuc ? N1 : 0, want2 ? N2 : 0);
+    RG_STAMP(28);
+    uint64_t ckey = 0;  // the last kept id's sort key
+    int qc = -1, pd = -1;
+    if (nuc) {
+      // sorted position p of the row is kept iff its exclusive prefix <= limit
       const uint64_t A1 = (uint64_t)(S.md[1] * kFix);
       const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zfx : 0.0;
       uint64_t limit = (uint64_t)pl;
       if (limit >= Zfx) limit = Zfx - 1;
-      auto in1 = [&](int e) -> bool { return present(e) && (cf[e] & 1u); };
-      const MassSel ms = sel_mass(ck, cm, in1, A1, limit, S);
-      RG_STAMP(27);
-      if (!ms.ok || ms.ceq == 0) return 6;
-      vkey = ms.key;
-      // ids tied at the cut key weigh the same: the kept ones are the lowest
-      // indices while their exclusive prefix stays <= limit
-      const uint64_t m1 = ms.meq / ms.ceq;
-      uint64_t nt = m1 ? (limit - ms.above) / m1 + 1 : (uint64_t)ms.ceq;
-      if (nt > ms.ceq) nt = ms.ceq;
-      n_tie = nt >= ms.ceq ? kNoTie : (uint32_t)nt;
-      if (n_tie != kNoTie) tie_lim = kth_index(in1, vkey, n_tie);
-      Zkept = ms.above + (uint64_t)nt * m1;
-      // the cut's collision group must lie inside region 1 in every chunk
-      if (tid == 0) S.mi[11] = -1;
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < FPT; e++)
-        if (in1(e) && ck[e] == vkey) S.mi[11] = e * NT + tid;
-      __syncthreads();
-      if (wv == 0) {
-        const bool ok = S.mi[11] >= 0 && group_inside(S.cx[S.mi[11]], lo1, hi1);
-        if (lane == 0) S.mi[12] = ok ? 1 : 0;
-      }
-      uint32_t ngt = 0;
-#pragma unroll
-      for (int e = 0; e < FPT; e++) ngt += (in1(e) && ck[e] > vkey) ? 1u : 0u;
-      ngt = bred(ngt, S.u, OpAdd{});
-      if (!S.mi[12]) return 8;
-      kept_n = (int32_t)((uint32_t)S.mi[19] + ngt + (uint32_t)nt);
+      // the first dropped position
+      const int lo = wave_first_true(0, N1, [&](int p) { return A1 + (p > 0 ? S.sc[0][p - 1] : 0ull) > limit; });
+      // the cut must fall inside the list: something kept, something dropped
+      if (lo == 0 || A1 + S.sc[0][N1 - 1] <= limit) return 6;
+      qc = lo - 1;
+      ckey = S.sk[0][qc];
+      vkey = key_z(ckey);
+      // the ids at the cut's z are contiguous around qc
+      const int f0 = wave_first_true(0, qc, [&](int p) { return key_z(S.sk[0][p]) <= vkey; });
+      const int l0 = wave_first_true(qc + 1, N1, [&](int p) { return key_z(S.sk[0][p]) < vkey; });
+      const uint32_t ea = (uint32_t)(l0 - f0), ekk = (uint32_t)(qc + 1 - f0);
+      n_tie = ekk == ea ? kNoTie : ekk;
+      if (n_tie != kNoTie) tie_lim = key_index(ckey);
+      Zkept = A1 + S.sc[0][qc];
+      kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)lo);
       ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
       cut = key2f(vkey);
-      __syncthreads();
     } else {
       kept_n = -1;  // filled below when asked
     }
-    // ---- the draw: exact mass select over the region-2 candidates ----
-    if (NL > KEPT && want2) {
+    if (want2) {
       const uint64_t A2 = (uint64_t)(S.md[2] * kFix);
       uint64_t target = (uint64_t)((double)u * (double)Zkept);
       if (target >= Zkept) target = Zkept - 1;
-      auto in2 = [&](int e) -> bool { return present(e) && (cf[e] & 2u); };
-      RG_STAMP(28);
-      const MassSel ds = sel_mass(ck, cm, in2, A2, target, S);
-      RG_STAMP(29);
-      if (!ds.ok || ds.ceq == 0) return 9;
-      // the tie holding the target, lowest index first (ties weigh the same)
-      const uint64_t m2 = ds.meq / ds.ceq;
-      uint64_t jt = m2 ? (target - ds.above) / m2 : 0;
-      if (jt >= ds.ceq) jt = ds.ceq - 1;
-      token = kth_index(in2, ds.key, (uint32_t)jt + 1u);
-      // one candidate of the drawn key, for its logit and collision group
-      if (tid == 0) S.mi[13] = -1;
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < FPT; e++)
-        if (in2(e) && ck[e] == ds.key) S.mi[13] = e * NT + tid;
-      __syncthreads();
-      if (wv == 0) {
-        const bool ok = S.mi[13] >= 0 && group_inside(S.cx[S.mi[13]], lo2, hi2);
-        if (lane == 0) S.mi[14] = ok ? 1 : 0;
-      }
-      __syncthreads();
-      if (!S.mi[14]) return 11;
-      chosen_z = key2f(ds.key);
-      // the drawn id must be kept
-      if (nuc && (ds.key < vkey || (ds.key == vkey && n_tie != kNoTie && token > tie_lim))) return 12;
+      // the first position whose inclusive prefix passes the target
+      const int lo = wave_first_true(0, N2, [&](int p) { return A2 + S.sc[1][p] > target; });
+      if (lo == N2 || target < A2) return 9;
+      pd = lo;
     }
+    if (wv == 0 && nuc) {  // the cut's collision group lies inside region 1 in every chunk
+      const bool ok = group_inside(__uint_as_float(S.sx[0][qc]), lo1, hi1);
+      if (lane == 0) S.mi[12] = ok ? 1 : 0;
+    }
+    if (wv == 1 && want2) {  // the drawn id's group inside region 2
+      const bool ok = group_inside(__uint_as_float(S.sx[1][pd]), lo2, hi2);
+      if (lane == 0) S.mi[14] = ok ? 1 : 0;
+    }
+    __syncthreads();
+    if (nuc && !S.mi[12]) return 8;
+    if (want2) {
+      if (!S.mi[14]) return 11;
+      const uint64_t dkey = S.sk[1][pd];
+      token = (int64_t)key_index(dkey);
+      chosen_z = key2f(key_z(dkey));
+      // the drawn id must be kept
+      if (nuc && dkey < ckey) return 12;
+    }
+    RG_STAMP(29);
     if (!nuc && P.kept_count) {
       // every finite logit is kept: count the -inf ones (a pass over the row)
       uint32_t ninf = 0;
       const int nvec = F.nvec;
-      for (int v = tid; v < nvec; v += NT) {
+      for (int v = tid; v < nvec; v += FT) {
         float xx[VPE > 1 ? VPE : 1];
         loadv<DT, VPE>(row, (int64_t)v * VPE, xx);
         const uint8_t* am = row_allowed(P, r);
 #pragma unroll
         for (int e = 0; e < VPE; e++) ninf += (xx[e] == -INFINITY || !id_allowed(am, (int64_t)v * VPE + e)) ? 1u : 0u;
       }
-      ninf = bred(ninf, S.u2, OpAdd{});
+      ninf = bred<FW>(ninf, S.u2, OpAdd{});
       kept_n = V - (int)ninf;
       __syncthreads();
     }
@@ -963,17 +908,21 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   if (P.skip_draw && !greedy) token = -1;
 
   // ---- outputs ----
+  // ln of sum exp(z) over the row: Z is in units of 2^Rref of exp2(x c)
+  double lnZ = 0.0;
+  if ((P.chosen_logprob || g.ntop > 0) && wv == 0 && Zfull > 0.0) lnZ = log(Zfull) + (double)Rref * 0.6931471805599453;
   if (P.chosen_logprob && tid == 0) {
     float lp = NAN;
     if (token >= 0 && Zfull > 0.0 && chosen_z == chosen_z) lp = (float)((double)chosen_z - lnZ);
     P.chosen_logprob[r] = lp;
   }
   if (g.ntop > 0 && status == 0) {
-    for (int q = tid; q < P.n_top; q += NT) {
+    // (n_top <= 64: wave 0 writes them)
+    for (int q = tid; q < P.n_top; q += 64) {
       if (q < ntop_out) {
-        const uint64_t kk = S.kkey[S.kord[q]];
-        P.top_logprobs[(int64_t)r * P.n_top + q] = (float)((double)key2f((uint32_t)(kk >> 32)) - lnZ);
-        if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = (int64_t)(0xFFFFFFFFu - (uint32_t)kk);
+        const uint64_t kk = S.sk[0][q];
+        P.top_logprobs[(int64_t)r * P.n_top + q] = (float)((double)key2f(key_z(kk)) - lnZ);
+        if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = (int64_t)key_index(kk);
       } else {
         P.top_logprobs[(int64_t)r * P.n_top + q] = -INFINITY;
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = -1;
@@ -991,7 +940,6 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     if (P.kept_count) P.kept_count[r] = kept_n;
     if (P.row_path) P.row_path[r] = 0;
   }
-  (void)zmax;
   return 0;
 }
 
@@ -1006,7 +954,8 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   const int j = slot % F.G;
   if (r >= F.k.R) return;
   if (F.heavy_first) r = heavy_first_row(F.k, r);
-  const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j);
+  const RowCfg g = row_cfg(F.k, r);
+  const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1020,10 +969,11 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
     if (SU.c.mi[7]) acquire_one();
   }
   __syncthreads();
-  if (!SU.c.mi[7]) return;
+  // the finaliser runs on waves 0 .. FW - 1 (one per SIMD); the others leave
+  if (!SU.c.mi[7] || threadIdx.x >= FT) return;
   acquire_agent();
   RG_STAMP(24);
-  const int reason = final_phase<DT, VPE>(F, SU.f, r);
+  const int reason = final_phase<DT, VPE>(F, SU.f, r, g);
   RG_STAMP(31);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }
