@@ -89,11 +89,26 @@ def build_args(w, dev, logits_dev, out, lib_mod):
     return a
 
 
-def fast_path_kernel(w) -> str:
-    """The kernel lps_sample runs for every row it can finish exactly: the
-    row-group kernel (chunks of a row on one XCD, the last to arrive
-    finalising the row)."""
-    return "rowgroup_kernel"
+def fast_path_kernel(w, flags: int = 0) -> str:
+    """The kernels lps_sample runs for the rows it can finish exactly (the
+    launch plan of lps.hip): the row-group kernel (chunks of a row on one XCD,
+    the last to arrive finalising the row) when the batch's chunk grid fits
+    one resident round of the 256 CUs; for larger batches the streaming kernel
+    (one workgroup per greedy / top-k row) and the row-group kernel for the
+    other rows, one of them skipped by a row-kind hint."""
+    import math
+    from lps import _lib
+    fp32 = w.logits.element_size() == 4
+    vpe = 4 if fp32 else 8
+    nvec = w.V // vpe
+    ne = 24 if (fp32 and w.B <= 16 and math.ceil(nvec / (512 * 6)) <= 16) else 80
+    G = math.ceil(nvec / (512 * (ne // vpe)))
+    big = math.ceil(w.B / 8) * 8 * G > 256 and w.V <= 163840
+    if not big or flags & _lib.LPS_FLAG_ROWS_NUCLEUS:
+        return "rowgroup_kernel"
+    if flags & _lib.LPS_FLAG_ROWS_TOPK:
+        return "stream_kernel"
+    return "stream_kernel + rowgroup_kernel"
 
 
 def timed_replays(launch, K, Wm, nbuf, use_graph=True):
@@ -775,7 +790,10 @@ def main():
         "tl": torch.empty((B, max(w.n_top, 1)), dtype=torch.float32, device=dev),
         "ti": torch.empty((B, max(w.n_top, 1)), dtype=torch.int64, device=dev),
     }
-    io["flags"] = 1 if args.generic else 0
+    # row-kind hint from the host-side parameters (as Sampler.sample_token
+    # passes it): a large batch launches only the kernels its rows need
+    from lps import row_kind_flags
+    io["flags"] = _lib.LPS_FLAG_GENERIC if args.generic else row_kind_flags(w.temperature, w.top_k)
     if args.allowed_frac is not None:
         from lps import pack_allowed
         gm = torch.Generator().manual_seed(11)
@@ -828,7 +846,7 @@ def main():
                               "1024 ids/row, chosen + top-20 logprobs"}[args.config],
            "batch_rows": B, "vocab": w.V, "input_dtype": str(w.logits.dtype).replace("torch.", ""),
            "logits_buffers_rotated": nbuf, "hip_graph": use_graph, "algorithmic_bytes_per_call": abytes,
-           "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w) + " + gen_row_kernel (deferred-row filter)",
+           "kernel": "gen_row_kernel" if args.generic else fast_path_kernel(w, io["flags"]) + " + gen_row_kernel (deferred-row filter)",
            "deferred_rows": int(deferred)}
     if args.allowed_frac is not None:
         cfg["legality_mask"] = f"random, {args.allowed_frac:.0%} of ids legal per row, packed bits"
@@ -848,7 +866,7 @@ def main():
         "config": cfg,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None if args.generic else hbm_traffic(fast_path_kernel(w), args.config)},
+                     "traffic": None if args.generic else hbm_traffic(fast_path_kernel(w, io["flags"]).split(" ")[0], args.config)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

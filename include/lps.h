@@ -69,7 +69,7 @@ enum {
 /* lps_sample_args.flags */
 enum {
   LPS_FLAG_GENERIC = 1,        /* use the general one-workgroup-per-row kernel only */
-  LPS_FLAG_APPEND_HISTORY = 2  /* also append each row's sampled token (when >= 0) to its history:
+  LPS_FLAG_APPEND_HISTORY = 2, /* also append each row's sampled token (when >= 0) to its history:
                                 * history[r, history_len[r]] = token, history_len[r] += 1, when
                                 * history_len[r] < history_stride (a full row is left as is).
                                 * The history arrays are then written, so the next step's
@@ -77,6 +77,12 @@ enum {
                                 * reference appends on the host, continuous_batching.py:404,
                                 * and passes the list back, sampling.py:125).  Requires history
                                 * and history_len. */
+  /* Row-kind hints (performance only: a row that breaks a hint is still sampled
+   * exactly, by the general kernel).  Large batches run greedy and top-k rows
+   * one workgroup per row and the other rows on the row-group kernel; a hint
+   * lets the launch skip the kernel no row needs. */
+  LPS_FLAG_ROWS_TOPK = 4,      /* every row is greedy (temperature <= 0) or has top_k > 0 */
+  LPS_FLAG_ROWS_NUCLEUS = 8    /* no row is greedy or has top_k > 0 */
 };
 
 /* Residual used by lps_spec_verify on the first rejected position. */

@@ -6,6 +6,7 @@
 #include <mutex>
 
 #include "lps_rowgroup.h"
+#include "lps_stream.h"
 #include "lps_generic.h"
 #include "lps_lmhead.h"
 #include "lps_softmax.h"
@@ -111,12 +112,44 @@ RgWs rg_layout(void* base, int R, int V) {
   return w;
 }
 
+// CUs of the current device (cached per device): one resident round of
+// row-group workgroups.
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+  }
+  return cus[dev];
+}
+
 template <int DT, int VPE, int NE>
-hipError_t launch_rg(const rg::RgParams& F, hipStream_t s) {
+hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   const unsigned grid = (unsigned)((F.k.R + 7) / 8 * 8 * F.G);
-  hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // batches of more than one resident round of chunk workgroups: greedy and
+  // top-k rows stream through one workgroup each (stream_kernel), the
+  // row-group kernel takes the others; the row-kind hints skip a kernel no row
+  // needs (a row the hint misjudges is deferred to the general kernel)
+  bool big = false;
+  if constexpr (VPE > 1) big = grid > (unsigned)device_cus() && F.k.V <= rg::STREAM_VMAX;
+  const bool run_stream = big && !(flags & LPS_FLAG_ROWS_NUCLEUS);
+  const bool run_rg = !(run_stream && (flags & LPS_FLAG_ROWS_TOPK));
+  if constexpr (VPE > 1) {
+    if (run_stream) {
+      F.stream_only = run_rg ? 0 : 1;
+      hipLaunchKernelGGL((st::stream_kernel<DT, VPE>), dim3(F.k.R), dim3(st::SNT), 0, s, F);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      F.skip_topk = 1;
+    }
+  }
+  if (run_rg) {
+    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   // rows the row-group kernel deferred: the general algorithm, one 1024-thread
   // workgroup per row (the others return at once)
   KParams G = F.k;
@@ -126,13 +159,13 @@ hipError_t launch_rg(const rg::RgParams& F, hipStream_t s) {
 }
 
 template <int DT>
-hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, hipStream_t s) {
-  if (p.vpe == 1) return launch_rg<DT, 1, 40>(F, s);
+hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, int flags, hipStream_t s) {
+  if (p.vpe == 1) return launch_rg<DT, 1, 40>(F, flags, s);
   if constexpr (DT == LPS_DTYPE_F32) {
-    if (p.ne == 24) return launch_rg<DT, 4, 24>(F, s);
-    return launch_rg<DT, 4, 80>(F, s);
+    if (p.ne == 24) return launch_rg<DT, 4, 24>(F, flags, s);
+    return launch_rg<DT, 4, 80>(F, flags, s);
   } else {
-    return launch_rg<DT, 8, 80>(F, s);
+    return launch_rg<DT, 8, 80>(F, flags, s);
   }
 }
 
@@ -196,6 +229,8 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   F.cv = p.cv;
   F.nvec = p.nvec;
   F.heavy_first = 0;
+  F.skip_topk = 0;
+  F.stream_only = 0;
   F.counters = w.counters;
   F.status = w.status;
   F.sums = w.sums;
@@ -203,9 +238,9 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   F.cands = w.cands;
   F.capw = p.capw;
   switch (dtype) {
-    case LPS_DTYPE_F32: return dispatch_rg_dt<LPS_DTYPE_F32>(F, p, s);
-    case LPS_DTYPE_BF16: return dispatch_rg_dt<LPS_DTYPE_BF16>(F, p, s);
-    default: return dispatch_rg_dt<LPS_DTYPE_F16>(F, p, s);
+    case LPS_DTYPE_F32: return dispatch_rg_dt<LPS_DTYPE_F32>(F, p, flags, s);
+    case LPS_DTYPE_BF16: return dispatch_rg_dt<LPS_DTYPE_BF16>(F, p, flags, s);
+    default: return dispatch_rg_dt<LPS_DTYPE_F16>(F, p, flags, s);
   }
 }
 

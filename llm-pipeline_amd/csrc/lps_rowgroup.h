@@ -71,8 +71,17 @@
     if (threadIdx.x == 0 && blockIdx.x < 8192)                                                    \
       ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = __builtin_amdgcn_s_memrealtime();             \
   } while (0)
+// a stamp taken once value v is available
+#define RG_STAMP_DEP(i, v)                                                                       \
+  do {                                                                                            \
+    if (threadIdx.x == 0 && blockIdx.x < 8192) {                                                  \
+      __asm__ volatile("" ::"v"(v));                                                              \
+      ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = __builtin_amdgcn_s_memrealtime();             \
+    }                                                                                             \
+  } while (0)
 #else
 #define RG_STAMP(i) ((void)0)
+#define RG_STAMP_DEP(i, v) ((void)0)
 #endif
 
 namespace lps {
@@ -104,6 +113,8 @@ constexpr int HPT = HPUB / NT;     // published histogram bins per thread
 constexpr int HLT = HB / NT;       // LDS histogram bins per thread
 constexpr double kFix = 17592186044416.0;  // 2^44: fixed-point masses (relative to the row reference)
 constexpr int FAST_KMAX = 256;     // largest top_k / top-N of the row-group kernel
+constexpr int STREAM_KMAX = 128;   // largest top_k / top-N of the streaming kernel
+constexpr int STREAM_VMAX = 163840;  // largest vocabulary of the streaming kernel
 
 // Row modes, decided per row from its parameters (row_cfg).
 enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEFER = 4 };
@@ -141,6 +152,8 @@ struct RgParams {
   int cv;              // vectors per chunk (the last chunk may hold fewer)
   int nvec;            // vectors per row
   int heavy_first;     // dispatch rows without top-k first
+  int skip_topk;       // the streaming kernel's rows (stream_takes) ran there: skip them
+  int stream_only;     // the row-group kernel is not launched: the streaming kernel defers the others
   uint32_t* counters;  // [R * 32]: [0] arrivals, [2] histogram barrier; zero between launches
   int32_t* status;     // [R]
   RgSum* sums;         // row r at sums + r * 2 * MAXG
@@ -201,6 +214,12 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   g.hlen = hlen;
   g.pen = hlen > 0 && (g.rep != 1.0f || g.pres != 0.0f || g.freq != 0.0f);
   return g;
+}
+
+// Rows the streaming kernel (one workgroup per row) takes when it runs:
+// greedy and top-k rows with k' <= STREAM_KMAX.
+__device__ __forceinline__ bool stream_takes(const RowCfg& g) {
+  return (g.mode == MODE_GREEDY || g.mode == MODE_TOPK) && g.kprime <= STREAM_KMAX;
 }
 
 // Smallest x whose fl(x / T) equals fl(x0 / T) (x0 finite, T > 0): the lower end

@@ -258,24 +258,35 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     double msum = 0.0;
 #pragma unroll
     for (int i = 0; i < HPT; i++) msum += mrg[i];
+    // region bounds are collected with LDS atomics by the few threads whose
+    // bins meet a target (cleared here, before the scan's barrier)
+    if (tid == 0) {
+      S.mi[0] = 1 << 30; S.mi[1] = -1; S.mi[2] = 1 << 30; S.mi[3] = -1;
+      S.u3[0] = 0u;
+    }
     double stot;
     const double sx = bscan<NW, double>(msum, &stot, S.d2);
     // ---- regions: bins whose cumulative interval meets the targets ----
     const double eps = 1e-6 * Z;
     const bool nuc = mode == MODE_NUCLEUS;
     const double Pm = nuc ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
-    int lo = 1 << 30, hi = -1;
-    {
+    if (nuc) {
+      int lo = 1 << 30, hi = -1;
       double a = sx;
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
         const int b = HB - 1 - HPT * tid - i;
-        if (nuc && mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) { lo = min(lo, b); hi = max(hi, b); }
+        if (mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) { lo = min(lo, b); hi = max(hi, b); }
         a += mrg[i];
       }
+      if (hi >= 0) {
+        atomicMin(&S.mi[0], lo);
+        atomicMax(&S.mi[1], hi);
+      }
     }
-    const int lo1 = nuc ? bred(lo, S.i1, OpMin{}) : (1 << 30);
-    const int hi1 = nuc ? bred(hi, S.i2, OpMax{}) : (1 << 30);
+    __syncthreads();
+    const int lo1 = nuc ? S.mi[0] : (1 << 30);
+    const int hi1 = nuc ? S.mi[1] : (1 << 30);
     // cumulative mass at the top of region 1 and at its bottom: the kept mass
     // lies between them, and the draw at u times it
     if (nuc && hi1 >= 0) {
@@ -293,25 +304,32 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const float u = fminf(fmaxf(g.u == g.u ? g.u : 0.0f, 0.0f), 0.99999994f);
     const double t_lo = (nuc ? (double)u * S.md[1] : (double)u * Z) - eps;
     const double t_hi = (nuc ? (double)u * S.md[2] : (double)u * Z) + eps;
-    lo = 1 << 30;
-    hi = -1;
-    double nest = 0.0;
     {
+      int lo = 1 << 30, hi = -1;
+      uint32_t nest = 0;  // elements in either region (an upper estimate: bin mass / the bin's least mass)
       double a = sx;
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
         const int b = HB - 1 - HPT * tid - i;
         const bool in2 = mrg[i] > 0.0 && a <= t_hi && a + mrg[i] >= t_lo;
         if (in2) { lo = min(lo, b); hi = max(hi, b); }
-        if (in2 || (b >= lo1 && b <= hi1)) nest += mrg[i] / bin_base(b);
+        if (in2 || (b >= lo1 && b <= hi1))
+          nest += (uint32_t)ceilf(__fmul_rn((float)mrg[i], ldexpf(1.0f, 134 - ((b >> 7) + HE0))) /
+                                  (float)(128 + (b & 127)));
         a += mrg[i];
       }
+      if (hi >= 0) {
+        atomicMin(&S.mi[2], lo);
+        atomicMax(&S.mi[3], hi);
+      }
+      if (nest) atomicAdd(&S.u3[0], nest);
     }
-    const int lo2 = bred(lo, S.i3, OpMin{});
-    const int hi2 = bred(hi, S.i1, OpMax{});
-    nest = bred(nest, S.d3, OpAdd{});
+    __syncthreads();
+    const int lo2 = S.mi[2];
+    const int hi2 = S.mi[3];
+    const uint32_t nest = S.u3[0];
     if (hi2 < 0 || !rfin) flags |= RF_REGION;
-    if (nest > (double)CAPR) flags |= RF_OVERFLOW;
+    if (nest > (uint32_t)CAPR) flags |= RF_OVERFLOW;
     sm.reg[0] = nuc ? lo1 : (1 << 30);
     sm.reg[1] = nuc ? hi1 : (1 << 30);
     sm.reg[2] = hi2 >= 0 ? lo2 : (1 << 30);
@@ -529,6 +547,114 @@ __device__ __forceinline__ void merge_lists_g(RgFinalS& S, int G, int D, int N0,
   else merge_lists<MAXG>(S, G, D, N0, N1, Rm);
 }
 
+// Inclusive prefix of masses m[0, n) into c[0, n) over FT threads (KPT
+// positions per thread, n <= KM).  Ends with a barrier.
+__device__ __forceinline__ void scan_one(const uint64_t* m, uint64_t* c, int n, uint64_t* slot) {
+  uint64_t v[KPT], loc = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int p = KPT * (int)threadIdx.x + i;
+    v[i] = p < n ? m[p] : 0ull;
+    loc += v[i];
+  }
+  uint64_t tot;
+  uint64_t ex = bscan<FW>(loc, &tot, slot);
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int p = KPT * (int)threadIdx.x + i;
+    ex += v[i];
+    if (p < n) c[p] = ex;
+  }
+  __syncthreads();
+}
+
+// Outcome of a sampling row decided on its sorted candidates.
+struct Decision {
+  int64_t token = -1;
+  float cut = -INFINITY, qprob = 0.0f, chosen_z = NAN;
+  int32_t ties = -1, kept_n = 0;
+  int ntop_out = 0;
+  int status = 0;
+};
+
+// The top-k row's filters and draw (sampling.py:66-85, 149-238) on its
+// sorted candidates: sk[0, K) in sorted order (z descending, ties lower index
+// first), sm their fixed-point masses, sc scratch for the prefix; K < Ntot
+// when candidates past capacity exist.  Greedy rows take the argmax gam.
+// Runs on the FT threads; returns 0, or a reason code to defer the row.
+__device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_t* sk, const uint64_t* sm, uint64_t* sc,
+                                           int K, int Ntot, float u, int gam, float xmax, RgX& X, Decision& d) {
+  const int tid = threadIdx.x;
+  const int64_t qtok = g.qtok;
+  d.ntop_out = g.ntop < K ? g.ntop : K;
+  if (g.mode == MODE_GREEDY) {
+    d.token = gam;
+    d.cut = xmax;
+    d.ties = 1;
+    d.kept_n = 1;
+    d.qprob = (qtok >= 0 && qtok == gam) ? 1.0f : 0.0f;
+    d.chosen_z = xmax;
+    return 0;
+  }
+  const int keff = g.topk < V ? g.topk : V;
+  if (keff > K || keff <= 0) return 5;
+  // the top-k set: every position whose z reaches the keff-th (ties kept)
+  const uint32_t kk = key_z(sk[keff - 1]);
+  const int nk = wave_first_true(keff, K, [&](int p) { return key_z(sk[p]) < kk; });
+  if (nk == K && K < Ntot) return 4;  // ties past the capacity
+  scan_one(sm, sc, nk, X.q);
+  const uint64_t Zk = sc[nk - 1];
+  int nf = nk;
+  if (g.topp < 1.0f) {  // keep sorted position p iff p == 0 or cum[p-1] <= top_p * Zk
+    const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zk : 0.0;
+    uint64_t limit = (uint64_t)pl;
+    if (limit >= Zk) limit = Zk - 1;
+    nf = wave_first_true(1, nk, [&](int p) { return sc[p - 1] > limit; });
+  }
+  if (g.minp > 0.0f) {  // keep mass >= min_p * (the top mass)
+    const float e0 = (float)((double)sm[0] / kFix);
+    int first = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < KPT; i++) {
+      const int p = KPT * tid + i;
+      if (p < nf && (float)((double)sm[p] / kFix) < __fmul_rn(g.minp, e0)) first = min(first, p);
+    }
+    const int f = bred<FW>(first, X.i2, OpMin{});
+    if (f < nf) nf = f;
+    if (nf == 0) d.status |= LPS_ROW_EMPTY;
+  }
+  // typical-p with top-k active: the row then holds -inf, and the reference keeps only the argmax
+  if (d.status == 0 && g.typp < 1.0f) nf = 1;
+  if (d.status != 0) return 0;
+  const uint64_t Zf = sc[nf - 1];
+  const uint32_t ckey = key_z(sk[nf - 1]);
+  d.cut = key2f(ckey);
+  // ids tied with the last kept one: contiguous around it
+  const int f0 = wave_first_true(0, nf, [&](int p) { return key_z(sk[p]) <= ckey; });
+  const int l0 = wave_first_true(nf, K, [&](int p) { return key_z(sk[p]) < ckey; });
+  if (l0 == K && K < Ntot) return 4;
+  d.ties = (l0 - f0) == (nf - f0) ? -1 : (int32_t)(nf - f0);
+  d.kept_n = nf;
+  // inverse CDF in sorted order
+  uint64_t target = (uint64_t)((double)u * (double)Zf);
+  if (target >= Zf) target = Zf - 1;
+  const int ps = wave_first_true(0, nf, [&](int p) { return sc[p] > target; });
+  d.token = key_index(sk[ps]);
+  d.chosen_z = key2f(key_z(sk[ps]));
+  if (qtok >= 0) {
+    if (tid == 0) X.mi[5] = -1;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPT; i++) {
+      const int p = KPT * tid + i;
+      if (p < nf && key_index(sk[p]) == qtok) X.mi[5] = p;
+    }
+    __syncthreads();
+    if (X.mi[5] >= 0) d.qprob = (float)((double)sm[X.mi[5]] / (double)Zf);
+  }
+  return 0;
+}
+
 template <int DT, int VPE>
 __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g) {
   const KParams& P = F.k;
@@ -568,6 +694,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   if (wv == 0) {
     RgSum a{};
     if (lane < G) a = ld_pub(sums + lane);
+    RG_STAMP_DEP(19, a.mkey);
     uint32_t fl = 0, xm = 0, mk = 0, nab = 0, nanb = 0;
     float R = -INFINITY;
     int nmax = 0, n1b = 0, n2b = 0, ob = 0, n1t = 0, n2t = 0, ot = 0;
@@ -591,6 +718,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       ot += co;
     }
     if (__builtin_popcount(xm) > 1) fl |= RF_SPLIT;
+    RG_STAMP_DEP(20, fl);
     int am = 0x7FFFFFFF;
     double Z = 0.0, A1 = 0.0, A2 = 0.0;
     for (int q = 0; q < G; q++) {
@@ -721,73 +849,11 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 
   if (status == 0 && g.kprime > 0) {
     // ======================= top-k (and top-N logprobs) =======================
-    ntop_out = g.ntop < K ? g.ntop : K;
-    if (mode == MODE_GREEDY) {
-      token = gam;
-      cut = xmax;
-      ties = 1;
-      kept_n = 1;
-      qprob = (qtok >= 0 && qtok == gam) ? 1.0f : 0.0f;
-      chosen_z = xmax;
-    } else {
-      const int keff = g.topk < V ? g.topk : V;
-      if (keff > K || keff <= 0) return 5;
-      // the top-k set: every position whose z reaches the keff-th (ties kept)
-      const uint32_t kk = key_z(S.sk[0][keff - 1]);
-      const int nk = wave_first_true(keff, K, [&](int p) { return key_z(S.sk[0][p]) < kk; });
-      if (nk == K && K < N1) return 4;  // ties past the merged capacity
-      scan_lists(S, nk, 0);
-      const uint64_t Zk = S.sc[0][nk - 1];
-      int nf = nk;
-      if (g.topp < 1.0f) {  // keep sorted position p iff p == 0 or cum[p-1] <= top_p * Zk
-        const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zk : 0.0;
-        uint64_t limit = (uint64_t)pl;
-        if (limit >= Zk) limit = Zk - 1;
-        nf = wave_first_true(1, nk, [&](int p) { return S.sc[0][p - 1] > limit; });
-      }
-      if (g.minp > 0.0f) {  // keep mass >= min_p * (the top mass)
-        const float e0 = (float)((double)S.sm[0][0] / kFix);
-        int first = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-          const int p = KPT * tid + i;
-          if (p < nf && (float)((double)S.sm[0][p] / kFix) < __fmul_rn(g.minp, e0)) first = min(first, p);
-        }
-        const int f = bred<FW>(first, S.i2, OpMin{});
-        if (f < nf) nf = f;
-        if (nf == 0) status |= LPS_ROW_EMPTY;
-      }
-      // typical-p with top-k active: the row then holds -inf, and the reference keeps only the argmax
-      if (status == 0 && g.typp < 1.0f) nf = 1;
-      if (status == 0) {
-        const uint64_t Zf = S.sc[0][nf - 1];
-        const uint32_t ckey = key_z(S.sk[0][nf - 1]);
-        cut = key2f(ckey);
-        // ids tied with the last kept one: contiguous around it
-        const int f0 = wave_first_true(0, nf, [&](int p) { return key_z(S.sk[0][p]) <= ckey; });
-        const int l0 = wave_first_true(nf, K, [&](int p) { return key_z(S.sk[0][p]) < ckey; });
-        if (l0 == K && K < N1) return 4;
-        ties = (l0 - f0) == (nf - f0) ? -1 : (int32_t)(nf - f0);
-        kept_n = nf;
-        // inverse CDF in sorted order
-        uint64_t target = (uint64_t)((double)u * (double)Zf);
-        if (target >= Zf) target = Zf - 1;
-        const int ps = wave_first_true(0, nf, [&](int p) { return S.sc[0][p] > target; });
-        token = key_index(S.sk[0][ps]);
-        chosen_z = key2f(key_z(S.sk[0][ps]));
-        if (qtok >= 0) {
-          if (tid == 0) S.mi[5] = -1;
-          __syncthreads();
-#pragma unroll
-          for (int i = 0; i < KPT; i++) {
-            const int p = KPT * tid + i;
-            if (p < nf && key_index(S.sk[0][p]) == qtok) S.mi[5] = p;
-          }
-          __syncthreads();
-          if (S.mi[5] >= 0) qprob = (float)((double)S.sm[0][S.mi[5]] / (double)Zf);
-        }
-      }
-    }
+    Decision d;
+    const int rc = topk_decide(g, V, S.sk[0], S.sm[0], S.sc[0], K, N1, u, gam, xmax, S, d);
+    if (rc) return rc;
+    token = d.token; cut = d.cut; qprob = d.qprob; chosen_z = d.chosen_z;
+    ties = d.ties; kept_n = d.kept_n; ntop_out = d.ntop_out; status |= d.status;
   } else if (status == 0 && mode == MODE_GREEDY) {
     token = gam;
     cut = xmax;
@@ -955,6 +1021,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (r >= F.k.R) return;
   if (F.heavy_first) r = heavy_first_row(F.k, r);
   const RowCfg g = row_cfg(F.k, r);
+  if (F.skip_topk && stream_takes(g)) return;
   const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);

@@ -4,7 +4,7 @@ the llm-pipeline inference engine (``llm_pipeline.inference`` exports
 ``src/llm_pipeline/inference/__init__.py:4,17,37-38``)."""
 
 from .batch import (SampleOutput, SamplingParams, allowed_from_constraint, pack_allowed, pad_histories,
-                    raise_on_status, sample_rows)
+                    raise_on_status, row_kind_flags, sample_rows)
 from .sampling import Sampler, SamplingConfig
 from .speculative import SpecDecStats, SpecVerifyOutput, spec_verify, verify_drafts_batched
 from .lmhead import lm_head
@@ -19,6 +19,7 @@ __all__ = [
     "SamplingParams",
     "SampleOutput",
     "sample_rows",
+    "row_kind_flags",
     "pack_allowed",
     "allowed_from_constraint",
     "SamplerState",

@@ -36,6 +36,8 @@ LPS_MAX_HISTORY_DISTINCT = 1536
 
 LPS_FLAG_GENERIC = 1
 LPS_FLAG_APPEND_HISTORY = 2
+LPS_FLAG_ROWS_TOPK = 4
+LPS_FLAG_ROWS_NUCLEUS = 8
 
 LPS_RESIDUAL_TARGET = 0
 LPS_RESIDUAL_LEVIATHAN = 1

@@ -98,6 +98,36 @@ class SampleOutput:
     row_path: Optional[torch.Tensor] = None         # int32 [B]: 0 fast kernel, 1 general kernel
 
 
+def row_kind_flags(temperature, top_k) -> int:
+    """Row-kind hint flags for ``lps_sample`` from host-side per-row
+    temperatures and top-k values (scalars, sequences or CPU tensors):
+    ``LPS_FLAG_ROWS_TOPK`` when every row is greedy (temperature <= 0) or has
+    top_k > 0, ``LPS_FLAG_ROWS_NUCLEUS`` when none is, else 0 (also for device
+    tensors, whose values the host does not hold).  The hints only choose which
+    kernels a large batch launches; a row that breaks one is still sampled
+    exactly, by the general kernel."""
+    def host(v):
+        if isinstance(v, torch.Tensor):
+            return v.reshape(-1) if v.device.type == "cpu" else None
+        return torch.as_tensor(v).reshape(-1)
+    T, k = host(temperature), host(top_k)
+    if T is None or k is None:
+        return 0
+    n = max(T.numel(), k.numel())
+    if n == 0:
+        return 0
+    T = T.float().expand(n) if T.numel() == 1 else T.float()
+    k = k.long().expand(n) if k.numel() == 1 else k.long()
+    if T.numel() != n or k.numel() != n:
+        return 0
+    topk_row = ~(T > 0) | (k > 0)
+    if bool(topk_row.all()):
+        return _lib.LPS_FLAG_ROWS_TOPK
+    if not bool(topk_row.any()):
+        return _lib.LPS_FLAG_ROWS_NUCLEUS
+    return 0
+
+
 def pad_histories(histories: Iterable[Sequence[int]], device) -> tuple:
     """Per-row token lists -> padded ``int32 [B, H]`` and lengths ``int32 [B]``."""
     hs = [list(h) for h in histories]
@@ -142,7 +172,7 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
                 query_tokens: Optional[torch.Tensor] = None, skip_draw: bool = False, kept_set: bool = False,
                 path: str = "auto", generator: Optional[torch.Generator] = None,
                 allowed: Optional[torch.Tensor] = None, append_history: bool = False,
-                noalloc: bool = False) -> SampleOutput:
+                noalloc: bool = False, row_kind_hint: int = 0) -> SampleOutput:
     """Sample one token per row of ``logits [B, V]`` (rows may be strided, the
     vocabulary dimension must be contiguous).  Asynchronous: nothing is
     synchronised and ``status`` is returned as a device tensor.
@@ -163,6 +193,10 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     penalties see it without a host round trip.  ``histories`` and
     ``history_lengths`` must then be int32 device tensors used as they are
     (row-contiguous histories, contiguous lengths).
+
+    ``row_kind_hint``: ``row_kind_flags(...)`` of the rows' host-side
+    parameters, when the caller has them; it only selects the kernels a large
+    batch launches (a row that breaks it is still sampled exactly).
 
     ``noalloc``: launch through ``lps_sample_noalloc``, which uses the
     library's own per-GPU workspace instead of a caller one and allocates
@@ -268,7 +302,10 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_ties = D.ptr(out.kept_ties)
     a.kept_count = D.ptr(out.kept_count)
     a.row_path = D.ptr(out.row_path)
-    a.flags = (0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
+    if row_kind_hint & ~(_lib.LPS_FLAG_ROWS_TOPK | _lib.LPS_FLAG_ROWS_NUCLEUS):
+        raise ValueError("row_kind_hint takes LPS_FLAG_ROWS_TOPK / LPS_FLAG_ROWS_NUCLEUS only")
+    a.flags = ((0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
+               | row_kind_hint)
     if noalloc:
         a.workspace = 0
         a.workspace_bytes = 0

@@ -22,7 +22,7 @@ from typing import Any, Dict, List, Optional
 import torch
 
 from . import _device as D
-from .batch import SamplingParams, pad_histories, raise_on_status, sample_rows
+from .batch import SamplingParams, pad_histories, raise_on_status, row_kind_flags, sample_rows
 
 
 @dataclass
@@ -91,7 +91,9 @@ class Sampler:
             raise ValueError(f"logits must be [batch_size, vocab_size]; got {tuple(logits.shape)}")
         B = logits.shape[0]
         dev = logits.device
+        hint = 0
         if params is None:
+            hint = row_kind_flags(config.temperature, config.top_k)
             params = SamplingParams.build(
                 B, dev, temperature=config.temperature, top_k=config.top_k, top_p=config.top_p,
                 min_p=config.min_p, typical_p=config.typical_p, repetition_penalty=config.repetition_penalty,
@@ -102,7 +104,7 @@ class Sampler:
             history_lengths = torch.full((B,), h.numel(), dtype=torch.int32, device=dev)
         out = sample_rows(logits, params, uniforms, histories=histories, history_lengths=history_lengths,
                           logprobs=bool(config.logprobs), top_logprobs=int(config.top_logprobs),
-                          generator=generator, allowed=allowed)
+                          generator=generator, allowed=allowed, row_kind_hint=hint)
         self.last_output = out
         if strict is None:
             strict = not torch.cuda.is_current_stream_capturing()

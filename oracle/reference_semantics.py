@@ -316,8 +316,10 @@ def logprobs_row(z_pre: torch.Tensor, token: int, n_top: int):
     pre-filter logits (temperature 1 for greedy rows) at the chosen id, plus
     the top-``n_top`` ``(logprob, id)`` pairs, ties lower-index-first.  The
     nearest reference code is ``advanced_sampling.py:81-82`` (log_softmax then
-    topk)."""
-    lp = F.log_softmax(z_pre.reshape(1, -1), dim=-1).reshape(-1)
+    topk).  Computed in fp64: an fp32 log_softmax over a 151936-id row is
+    itself off by up to ~1e-5 (its fp32 row sum), the size of the tolerance
+    the GPU values are held to."""
+    lp = F.log_softmax(z_pre.double().reshape(1, -1), dim=-1).reshape(-1)
     chosen = float(lp[token].item())
     # log_softmax is monotone in z: rank by z itself (ties lower index first)
     order = np.lexsort((np.arange(lp.numel()), -z_pre.reshape(-1).double().numpy()))[:n_top]

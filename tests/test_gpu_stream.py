@@ -1,0 +1,151 @@
+"""The streaming kernel (one workgroup per greedy / top-k row, for batches whose
+row-group grid exceeds one resident round) against the CPU oracle, through the
+C ABI; and the row-kind hints, which choose the launched kernels but never the
+result (a row that breaks a hint is sampled by the general kernel)."""
+
+import numpy as np
+import pytest
+import torch
+
+from lps import _lib, row_kind_flags
+from tests import parity as PY
+from tests import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOPK = _lib.LPS_FLAG_ROWS_TOPK
+NUC = _lib.LPS_FLAG_ROWS_NUCLEUS
+
+
+def _print(msg):
+    print(msg, flush=True)
+
+
+def _deferral_reasons(out, dev, B):
+    """Reason codes of the rows the fast kernels deferred (the workspace's
+    status words, LPS_ROW_DEFERRED | reason << 8), by row."""
+    from lps import batch
+    ws = batch._WS[(dev.index, torch.cuda.current_stream(dev).cuda_stream)]
+    st = ws[131072:131072 + 4 * B].view(torch.int32).cpu()
+    rows = (out.row_path.cpu() != 0).nonzero().flatten().tolist()
+    return {r: int(st[r]) >> 8 for r in rows}
+
+
+def _big(B, V, dtype, seed, kinds="mixed", H=48, logprobs=False, n_top=0):
+    """B rows over a small vocabulary (one chunk per row, so B > 256 makes the
+    grid larger than one resident round): ties, penalties with out-of-range
+    and repeated history ids, and, by kinds, greedy / top-k / nucleus rows."""
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    x = torch.randn((B, V), generator=g) * 2.5
+    x[::7] = torch.round(x[::7] * 2)                                    # ties
+    x = x.to(dtype)
+    T = torch.from_numpy(rng.choice([0.0, 0.6, 1.0, 1.4], size=B).astype(np.float32))
+    k = torch.from_numpy(rng.choice([1, 20, 40, 63, 64, 65, 100, 128], size=B).astype(np.int32))
+    if kinds == "mixed":
+        k = torch.where(torch.arange(B) % 5 == 0, torch.zeros_like(k), k)
+        T = torch.where(torch.arange(B) % 10 == 0, torch.ones_like(T), T)
+    elif kinds == "nucleus":
+        k = torch.zeros_like(k)
+        T = torch.where(T > 0, T, torch.ones_like(T))
+    p = torch.from_numpy(rng.choice([1.0, 0.9, 0.5], size=B).astype(np.float32))
+    f = lambda v: torch.full((B,), v, dtype=torch.float32)
+    hist = torch.from_numpy(rng.integers(-3, V + 3, size=(B, H)).astype(np.int32))
+    hist[:, : H // 4] = hist[:, H // 4: H // 2]                          # repeated ids (frequency counts)
+    hl = torch.from_numpy(rng.integers(0, H + 1, size=B).astype(np.int32))
+    return W.Workload("big", x, T, k, p, f(0.0), f(1.0), f(1.2), f(0.4), f(0.25), hist, hl,
+                      torch.rand((B,), generator=g), logprobs=logprobs, n_top=n_top)
+
+
+def test_c5_full_size_every_row(dev):
+    """c5 at its own size (B=512 fp16, greedy and top-k 40 / top-p 0.92 rows,
+    repetition penalty over 1024 ids, chosen and top-20 logprobs) with the hint
+    Sampler.sample_token passes: the streaming kernel alone; every row against
+    the oracle, logprobs included."""
+    w = W.c5()
+    assert row_kind_flags(w.temperature, w.top_k) == TOPK
+    out = PY.run_workload(w, dev)
+    assert (out.row_path.cpu() == 0).all()
+    rep = PY.check_rows(w, out, lp=True)
+    _print(f"c5 B=512 streaming kernel: {rep}")
+
+
+@pytest.mark.parametrize("hint", [0, TOPK, NUC])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_large_mixed_batch_any_hint(dev, dtype, hint):
+    """A mixed batch larger than one resident round: greedy and top-k rows on
+    the streaming kernel, nucleus / pure rows on the row-group kernel (hint 0);
+    a hint that misjudges rows changes only the path (general kernel), never
+    the result."""
+    B, V = 320, 4096
+    w = _big(B, V, dtype, seed=17 + int(dtype == torch.float32))
+    out = PY.run_workload(w, dev, row_kind_hint=hint)
+    PY.check_rows(w, out)
+    path = out.row_path.cpu()
+    topk_rows = ~(w.temperature > 0) | (w.top_k > 0)
+    plain = torch.arange(B) % 7 != 0      # tie-heavy rows may overflow a wave's segment and defer
+    _print(f"{dtype} hint {hint}: deferred rows and reasons {_deferral_reasons(out, dev, B)}")
+    if hint == 0:
+        assert (path[plain] == 0).all()
+    elif hint == TOPK:
+        assert (path[topk_rows & plain] == 0).all() and (path[~topk_rows] == 1).all()
+    _print(f"{dtype} hint {hint}: general-kernel rows {int(path.sum())}/{B}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_large_topk_batch_logprobs(dev, dtype):
+    """Greedy and top-k rows only (k up to the streaming kernel's 128, and past
+    it), with chosen and top-N logprobs, penalties and ties."""
+    B, V = 300, 6000
+    w = _big(B, V, dtype, seed=23, kinds="topk", logprobs=True, n_top=20)
+    w.top_k[5] = 129          # past the streaming kernel's k': the row-group kernel's row
+    w.temperature[5] = 0.8
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out, lp=True)
+    plain = torch.arange(B) % 7 != 0      # tie-heavy rows may overflow a wave's segment and defer
+    _print(f"{dtype}: deferred rows and reasons {_deferral_reasons(out, dev, B)}")
+    # row 5 (k' = 129) is the row-group kernel's, which the batch's row-kind
+    # hint (every row greedy or top-k) does not launch: the general kernel's
+    assert int(out.row_path[5]) == 1
+    plain[5] = False
+    assert (out.row_path.cpu()[plain] == 0).all()
+    _print(f"{dtype} top-k batch: {rep}; general-kernel rows {int(out.row_path.sum())}/{B}")
+
+
+def test_large_batch_legality_mask(dev):
+    """Legality bits on the streaming kernel equal -inf logits, bit for bit,
+    and both match the oracle."""
+    B, V = 288, 8192
+    w = _big(B, V, torch.bfloat16, seed=31, kinds="topk", logprobs=True, n_top=8)
+    g = torch.Generator().manual_seed(2)
+    legal = torch.rand((B, V), generator=g) < 0.7
+    legal[:, 0] = True
+    a = PY.run_workload(w, dev, allowed=legal.to(dev))
+    wm = W.Workload(**{**w.__dict__, "logits": w.logits.masked_fill(~legal, float("-inf"))})
+    b = PY.run_workload(wm, dev)
+    assert torch.equal(a.tokens, b.tokens)
+    assert torch.equal(a.kept_count, b.kept_count)
+    assert torch.equal(a.chosen_logprob, b.chosen_logprob)
+    PY.check_rows(wm, a, lp=True)
+
+
+def test_large_batch_nonfinite_rows(dev):
+    """NaN / +inf / all -inf rows on the streaming kernel: sampling rows report
+    the reference's rejection, greedy rows take torch.argmax's first NaN."""
+    B, V = 272, 4096
+    w = _big(B, V, torch.float32, seed=41, kinds="topk")
+    x = w.logits.clone()
+    x[3, 100] = float("nan"); w.temperature[3] = 0.9; w.top_k[3] = 20
+    x[4, 7] = float("inf"); w.temperature[4] = 0.9; w.top_k[4] = 20
+    x[5] = float("-inf"); w.temperature[5] = 0.9; w.top_k[5] = 20
+    x[6, 50] = float("nan"); x[6, 30] = float("nan"); w.temperature[6] = 0.0
+    w.logits = x
+    out = PY.run_workload(w, dev)
+    st = out.status.cpu()
+    tok = out.tokens.cpu()
+    assert st[3] == _lib.LPS_ROW_NONFINITE and tok[3] == -1
+    assert st[4] == _lib.LPS_ROW_NONFINITE and tok[4] == -1
+    assert st[5] == _lib.LPS_ROW_EMPTY and tok[5] == -1
+    assert st[6] == 0 and tok[6] == 30
+    ok = [i for i in range(B) if i not in (3, 4, 5, 6)]
+    PY.check_rows(w, out, rows=ok)

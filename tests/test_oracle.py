@@ -225,11 +225,14 @@ def test_logprobs_library():
     g = torch.Generator().manual_seed(8)
     z = torch.round(torch.randn(100, generator=g) * 3)    # ties
     chosen, vals, ids = O.logprobs_row(z, 17, 20)
-    lp = torch.log_softmax(z, -1)
+    lp = torch.log_softmax(z.double(), -1)
     assert chosen == lp[17].item()
+    # closed form, with an exactly rounded sum
+    zz = z.double().tolist()
+    assert abs(chosen - (zz[17] - math.log(math.fsum(math.exp(v) for v in zz)))) < 1e-12
     order = torch.sort(z, descending=True, stable=True).indices[:20].tolist()
     assert ids.tolist() == order
-    assert np.array_equal(vals, lp[order].numpy())
+    assert np.array_equal(vals, lp[order].numpy().astype(np.float32))
 
 
 def test_entropy_closed_form():
