@@ -139,7 +139,8 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   if constexpr (VPE > 1) {
     if (run_stream) {
       F.stream_only = run_rg ? 0 : 1;
-      hipLaunchKernelGGL((st::stream_kernel<DT, VPE>), dim3(F.k.R), dim3(st::SNT), 0, s, F);
+      if (F.k.allowed) hipLaunchKernelGGL((st::stream_kernel<DT, VPE, true>), dim3(F.k.R), dim3(st::SNT), 0, s, F);
+      else hipLaunchKernelGGL((st::stream_kernel<DT, VPE, false>), dim3(F.k.R), dim3(st::SNT), 0, s, F);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       F.skip_topk = 1;

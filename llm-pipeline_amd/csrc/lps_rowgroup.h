@@ -176,20 +176,31 @@ struct RowCfg {
 // Parameters and mode of row r (sampling.py:66-82 filter order; the row-group
 // kernel takes greedy rows, top-k rows with k <= FAST_KMAX, nucleus and pure
 // rows, and defers the rest to the general kernel).
+// A per-row parameter, or its default for a NULL array.  The load is issued
+// unconditionally (a NULL array reads a dummy word, then its value is
+// dropped), so every parameter load of a row is in flight at once instead of
+// one dependent round trip each.
+__device__ int32_t rg_dummy_word[2];
+template <typename T>
+__device__ __forceinline__ T param_or(const T* p, int64_t i, T def) {
+  const T* q = p ? p + i : reinterpret_cast<const T*>(rg_dummy_word);
+  const T v = *q;
+  return p ? v : def;
+}
 __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   RowCfg g;
-  g.T = P.temperature ? P.temperature[r] : P.temperature_def;
-  g.topk = P.top_k ? P.top_k[r] : P.top_k_def;
-  g.topp = P.top_p ? P.top_p[r] : P.top_p_def;
-  g.minp = P.min_p ? P.min_p[r] : P.min_p_def;
-  g.typp = P.typical_p ? P.typical_p[r] : P.typical_p_def;
-  g.rep = P.rep ? P.rep[r] : P.rep_def;
-  g.pres = P.pres ? P.pres[r] : P.pres_def;
-  g.freq = P.freq ? P.freq[r] : P.freq_def;
-  g.u = P.uniforms ? P.uniforms[r] : 0.5f;
-  g.qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
-               ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
-               : -1;
+  g.T = param_or(P.temperature, r, P.temperature_def);
+  g.topk = param_or(P.top_k, r, P.top_k_def);
+  g.topp = param_or(P.top_p, r, P.top_p_def);
+  g.minp = param_or(P.min_p, r, P.min_p_def);
+  g.typp = param_or(P.typical_p, r, P.typical_p_def);
+  g.rep = param_or(P.rep, r, P.rep_def);
+  g.pres = param_or(P.pres, r, P.pres_def);
+  g.freq = param_or(P.freq, r, P.freq_def);
+  g.u = param_or(P.uniforms, r, 0.5f);
+  const bool hasq = P.query_tokens && (r % P.rows_inner) < P.query_inner;
+  g.qtok = param_or(hasq ? P.query_tokens : (const int64_t*)nullptr,
+                    (int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner), (int64_t)-1);
   // a query id outside the vocabulary has probability 0 (as verify_drafts_kernel
   // treats it); no logit is read for it
   if (g.qtok >= (int64_t)P.V) g.qtok = -1;
@@ -209,7 +220,7 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   if (g.kprime > FAST_KMAX) mode = MODE_DEFER;
   g.mode = mode;
   g.hrow = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
-  int hlen = (g.hrow && P.history_len) ? P.history_len[r] : 0;
+  int hlen = param_or(g.hrow ? P.history_len : (const int32_t*)nullptr, r, 0);
   if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;
   g.hlen = hlen;
   g.pen = hlen > 0 && (g.rep != 1.0f || g.pres != 0.0f || g.freq != 0.0f);

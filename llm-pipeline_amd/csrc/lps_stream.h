@@ -26,10 +26,14 @@
 //     maxima (k' = max(top_k, top-N logprobs)), lowered to the start of its
 //     division-collision group, and is raised the same way over the segment
 //     when it fills past half.  Each wave thus keeps at least k' of its own
-//     logits at or above its threshold, so the row's k'-th largest scaled
-//     logit lies at or above the largest wave threshold theta*, and every
-//     logit of the row's top-k' set (ties included) is a candidate of its
-//     wave.  No barrier is taken inside the stream.
+//     logits at or above its threshold.  Every wave also publishes (LDS) a
+//     share: its ceil(k'/8)-th largest logit so far, lowered the same way;
+//     the eight waves hold at least k' logits at or above the smallest share.
+//     So the row's k'-th largest scaled logit lies at or above theta*, the
+//     larger of the largest own threshold and the smallest share, and every
+//     logit of the row's top-k' set (ties included) is at or above the
+//     emission threshold max(own, smallest share) of its wave at any time.
+//     No barrier is taken inside the stream.
 // After the stream:
 //   - history ids: each distinct id's logit is read, masked, penalised
 //     (penalize: repetition once per distinct id, then frequency and presence)
@@ -82,8 +86,10 @@ struct StShared : RgX {
     } seg;
     uint64_t ck[POOL];                  // pool keys
   } b;
+  uint4 km[256];                        // kill masks: the words' -inf positions of a VPE-bit kill pattern
   int32_t segn[SNW];                    // segment counts (SEG + 1: overflowed)
-  float segth[SNW];                     // wave thresholds
+  float segth[SNW];                     // wave thresholds (each wave: >= k' own logits at or above)
+  float segjt[SNW];                     // joint shares (each wave: >= ceil(k'/8) own logits at or above)
   int32_t pn;                           // pool count
 };
 static_assert(sizeof(StShared) <= 80 * 1024, "two workgroups per CU");
@@ -91,6 +97,22 @@ static_assert(sizeof(StShared) <= 80 * 1024, "two workgroups per CU");
 // Raises the wave's threshold over its segment (every lane of the wave calls
 // it): the kc-th largest buffered logit, lowered to the start of its
 // collision group, then keeps the entries at or above it, in order.
+// The joint threshold: the smallest published share.  Every wave has at least
+// ceil(k'/8) of its own logits at or above its share, so the eight waves hold
+// at least k' logits at or above the smallest (a wave that has not published
+// yet counts as -inf).  Every lane of the wave calls it.
+__device__ __forceinline__ float joint_threshold(const StShared& S) {
+  float t = S.segjt[0];
+#pragma unroll
+  for (int v = 1; v < SNW; v++) t = fminf(t, S.segjt[v]);
+  return t;
+}
+// Lower end of the collision group of the key th (greedy rows: th itself), as
+// a threshold float no lower than -FLT_MAX.
+__device__ __forceinline__ float key_threshold(uint32_t th, bool greedy, float T) {
+  if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
+  return fmaxf(key2f(th), -3.40282347e38f);
+}
 __device__ __forceinline__ void wave_refine(StShared& S, int w, uint32_t& n, int kc, bool greedy, float T, float& theta) {
   const int lane = threadIdx.x & 63;
   const int nn = (int)min(n, (uint32_t)SEG);
@@ -104,14 +126,18 @@ __device__ __forceinline__ void wave_refine(StShared& S, int w, uint32_t& n, int
     ib[q] = e < nn ? S.b.seg.i[w][e] : 0;
     kv[q] = e < nn ? f2key(__uint_as_float(xb[q])) : 0u;
   }
-  uint32_t th = wave_kth_largest<SEG / 64>(kv, (uint32_t)kc);
-  if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
-  theta = fmaxf(theta, fmaxf(key2f(th), -3.40282347e38f));
+  // own threshold (k'-th) and joint share (ceil(k'/8)-th): the segment holds
+  // every own logit at or above the current emission threshold, which is at
+  // most the share, so both are exact over the wave's own logits seen so far
+  theta = fmaxf(theta, key_threshold(wave_kth_largest<SEG / 64>(kv, (uint32_t)kc), greedy, T));
+  const float share = key_threshold(wave_kth_largest<SEG / 64>(kv, (uint32_t)((kc + SNW - 1) / SNW)), greedy, T);
+  if (lane == 0) S.segjt[w] = fmaxf(S.segjt[w], share);
+  const float te = fmaxf(theta, joint_threshold(S));
   uint32_t m = 0;
 #pragma unroll
   for (int q = 0; q < SEG / 64; q++) {
     const int e = lane + 64 * q;
-    const bool keep = e < nn && !(__uint_as_float(xb[q]) < theta);
+    const bool keep = e < nn && !(__uint_as_float(xb[q]) < te);
     const uint64_t bm = __builtin_amdgcn_ballot_w64(keep);
     if (keep) {
       const uint32_t p = m + lanes_below(bm);
@@ -123,14 +149,105 @@ __device__ __forceinline__ void wave_refine(StShared& S, int w, uint32_t& n, int
   n = m;
 }
 
-template <int DT, int VPE>
+// The key of the m-th largest non-NaN value of x over the wave (M values per
+// lane; every lane calls it): a 32-step search over keys, each step one float
+// comparison per value against the step's key.
+template <int M>
+__device__ __forceinline__ uint32_t wave_kth_largest_x(const float (&x)[M], uint32_t m) {
+  uint32_t t = 0;
+#pragma unroll 1
+  for (int b = 31; b >= 0; b--) {
+    const uint32_t c = t | (1u << b);
+    const float th = key2f(c);
+    uint32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < M; i++) n += (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(x[i] >= th));
+    if (n >= m) t = c;
+  }
+  return t;
+}
+
+// AM: the launch carries legality masks (P.allowed non-null).
+template <int DT, int VPE, bool AM>
 __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   __shared__ StShared S;
   const KParams& P = F.k;
   const int r = blockIdx.x;
   if (r >= P.R) return;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // (the wave index through readfirstlane: the compiler then knows it is
+  // wave-uniform, and the chunk loop below is a scalar loop)
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  RG_STAMP(0);
+  // ---- the stream's constants; the first three tiles and the first history
+  // ids are loaded before anything else (the row's parameters decide below
+  // whether this kernel takes the row; the loads of a row it does not take
+  // are dropped) ----
+  const int V = P.V;
+  const char* row = row_ptr<DT>(P, r);
+  const uint8_t* am = AM ? row_allowed(P, r) : nullptr;
+  const int nvec = F.nvec;
+  constexpr int CV = 64 * SVT;      // vectors per chunk (one wave's unit of work)
+  constexpr int NE = SVT * VPE;     // logits per thread per tile
+  const int nch = (nvec + CV - 1) / CV;
+  const uint8_t* bmb = reinterpret_cast<const uint8_t*>(S.a.bm);
+  constexpr uint32_t VMASK = (1u << VPE) - 1u;
+  // -inf in every element of a 32-bit word of the row
+  constexpr uint32_t NEGW = DT == LPS_DTYPE_F32 ? 0xFF800000u : (DT == LPS_DTYPE_BF16 ? 0xFF80FF80u : 0xFC00FC00u);
+  // legality / history bits of vector v (VPE bits: 8 ids per byte, or a nibble)
+  auto bits_of = [&](const uint8_t* base, int v) -> uint32_t {
+    if constexpr (VPE == 8) return base[v];
+    else return ((uint32_t)base[v >> 1] >> ((v & 1) * 4)) & VMASK;
+  };
+  // id of slot s of chunk h (the lane's id base is laundered per use, so the
+  // per-slot constants are not hoisted into registers for the whole loop)
+  auto vid = [&](int h, int s) {
+    int b = lane * VPE;
+    __asm__ volatile("" : "+v"(b));
+    return b + h * CV * VPE + (s / VPE) * 64 * VPE + (s % VPE);
+  };
+
+  // Chunk h's loads (h is clamped to the last chunk, so every call issues the
+  // same loads and the compiler's load counters stay exact): four 16-byte
+  // vectors per lane, and with masks their legality bytes.
+  auto load_tile = [&](u32x4 (&d)[SVT], uint32_t (&ab)[SVT], int h) {
+    h = min(h, nch - 1);
+#pragma unroll
+    for (int i = 0; i < SVT; i++) {
+      const int v = min(h * CV + i * 64 + lane, nvec - 1);
+      d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + (int64_t)v * 16));
+    }
+#pragma unroll
+    for (int i = 0; i < SVT; i++) {
+      const int v = min(h * CV + i * 64 + lane, nvec - 1);
+      if constexpr (AM) ab[i] = VPE == 8 ? (uint32_t)am[v] : (uint32_t)am[v >> 1];
+      else ab[i] = 0xFFu;
+    }
+  };
+  // (the history ids first, then the row's parameters, then the chunks: loads
+  // issued behind the whole GPU's first chunks would wait for them)
+  const int32_t* hrow0 = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
+  const int32_t* hsrc = hrow0 ? hrow0 : reinterpret_cast<const int32_t*>(row);
+  const int hraw0 = hsrc[min((int64_t)tid, max(P.history_stride - 1, (int64_t)0))];
+  const int hraw1 = hsrc[min((int64_t)(tid + SNT), max(P.history_stride - 1, (int64_t)0))];
+  __asm__ volatile("" ::: "memory");
   const RowCfg g = row_cfg(P, r);
+  __asm__ volatile("" ::: "memory");
+  // chunks: each wave takes chunks wv, wv + 8, wv + 16, then the next free one
+  // (a counter in LDS), so waves that run faster take more of the row
+  int c0 = wv, c1 = wv + SNW, c2 = wv + 2 * SNW;
+  u32x4 b0[SVT], b1[SVT], b2[SVT];
+  uint32_t a0[SVT], a1[SVT], a2[SVT];
+  // (in this order: the loop's waits count on b1 being followed by b2's loads)
+  load_tile(b0, a0, c0);
+  __asm__ volatile("" ::: "memory");
+  load_tile(b1, a1, c1);
+  __asm__ volatile("" ::: "memory");
+  load_tile(b2, a2, c2);
+  __asm__ volatile("" ::: "memory");
+  const int hid0 = (hrow0 && (int64_t)tid < P.history_stride) ? hraw0 : -1;
+  const int hid1 = (hrow0 && (int64_t)(tid + SNT) < P.history_stride) ? hraw1 : -1;
+
+  RG_STAMP_DEP(9, g.T);
   if (!stream_takes(g)) {
     // the row-group kernel's rows; deferred when it is not launched
     if (F.stream_only && tid == 0) F.status[r] = LPS_ROW_DEFERRED | (16 << 8);
@@ -138,13 +255,24 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   }
   const bool greedy = g.greedy;
   const float T = g.T, c = g.c;
-  const int V = P.V;
   const int kc = g.kprime;
   const bool want_lp = P.chosen_logprob || g.ntop > 0;
-  const char* row = row_ptr<DT>(P, r);
-  const uint8_t* am = row_allowed(P, r);
   const bool pen = g.pen;
+  const bool kill = pen || am;
 
+  // ---- kill-mask table: pattern p (bit e = element e of a vector) -> the
+  // bits of the vector's four words that belong to killed elements ----
+  if (tid < 256) {
+    uint32_t mk[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if constexpr (VPE == 8)
+        mk[j] = (((tid >> (2 * j)) & 1) ? 0x0000FFFFu : 0u) | (((tid >> (2 * j + 1)) & 1) ? 0xFFFF0000u : 0u);
+      else
+        mk[j] = ((tid >> j) & 1) ? 0xFFFFFFFFu : 0u;
+    }
+    S.km[tid] = make_uint4(mk[0], mk[1], mk[2], mk[3]);
+  }
   // ---- the history: bitmap of the distinct in-range ids, and their counts ----
   if (pen) {
     const int nw = (V + 31) >> 5;
@@ -154,129 +282,142 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
       S.hcnt[i] = 0;
     }
   }
+  if (lane == 0) S.segjt[wv] = -3.40282347e38f;
   if (tid == 0) {
     S.mi[0] = 0;
+    S.mi[1] = 0;
+    S.mi[2] = 0;  // chunks taken past the first three of every wave
+    S.mi[3] = 0;  // distinct-id list length (no frequency penalty)
     S.pn = 0;
   }
   __syncthreads();
+  RG_STAMP(11);
+  // (without a frequency penalty an id's count does not matter: the bitmap
+  // decides membership, and the thread whose bit-set finds the bit clear
+  // appends the id to a list, in place of the hash table)
+  const bool counts = g.freq != 0.0f;
   if (pen) {
     bool full = false;
-    for (int j = tid; j < g.hlen; j += SNT) {
-      const int id = g.hrow[j];
-      if (id < 0 || id >= V) continue;
-      atomicOr(&S.a.bm[id >> 5], 1u << (id & 31));
+    uint32_t fresh = 0;  // distinct ids this thread inserted
+    auto insert = [&](int id) {
+      if (id < 0 || id >= V) return;
+      const uint32_t bit = 1u << (id & 31);
+      const uint32_t had = atomicOr(&S.a.bm[id >> 5], bit) & bit;
+      if (!counts) {
+        if (!had) {
+          const int p = atomicAdd(&S.mi[3], 1);
+          if (p < HASH_CAP) {
+            S.hkey[p] = id;
+            S.hcnt[p] = 1;
+          } else {
+            full = true;
+          }
+          fresh++;
+        }
+        return;
+      }
       uint32_t sl = hash_id(id);
       int p = 0;
       for (; p < HASH_CAP; p++) {
         const int old = atomicCAS(&S.hkey[sl], -1, id);
         if (old == -1 || old == id) {
           atomicAdd(&S.hcnt[sl], 1);
+          fresh += old == -1 ? 1u : 0u;
           break;
         }
         sl = (sl + 1) & (HASH_CAP - 1);
       }
       if (p == HASH_CAP) full = true;
-    }
+    };
+    if (tid < g.hlen) insert(hid0);
+    if (tid + SNT < g.hlen) insert(hid1);
+    for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) insert(g.hrow[j]);
+    if (fresh) atomicAdd(&S.mi[1], (int)fresh);
     if (full) S.mi[0] = 1;
   }
   __syncthreads();
-  bool defer_hist = false;
-  if (pen) {
-    uint32_t used = 0;
-    for (int i = tid; i < HASH_CAP; i += SNT) used += S.hkey[i] >= 0 ? 1u : 0u;
-    used = bred<SNW>(used, S.u, OpAdd{});
-    defer_hist = S.mi[0] != 0 || used > (uint32_t)LPS_MAX_HISTORY_DISTINCT;
-  }
+  RG_STAMP(10);
+  const bool defer_hist = pen && (S.mi[0] != 0 || S.mi[1] > LPS_MAX_HISTORY_DISTINCT);
 
-  // ---- the stream ----
-  const int nvec = F.nvec;
-  constexpr int TV = SNT * SVT;     // vectors per tile
-  constexpr int NE = SVT * VPE;     // logits per thread per tile
-  const int ntiles = (nvec + TV - 1) / TV;
-  const uint8_t* bmb = reinterpret_cast<const uint8_t*>(S.a.bm);
-  const bool kill = pen || am;
-  constexpr uint32_t VMASK = (1u << VPE) - 1u;
-  // legality / history bits of vector v (VPE bits: 8 ids per byte, or a nibble)
-  auto bits_of = [&](const uint8_t* base, int v) -> uint32_t {
-    if constexpr (VPE == 8) return base[v];
-    else return ((uint32_t)base[v >> 1] >> ((v & 1) * 4)) & VMASK;
-  };
-  auto vid = [&](int t, int s) { return (t * TV + (s / VPE) * SNT + tid) * VPE + (s % VPE); };
-
-  float bx = -INFINITY;             // thread maximum (greedy rows: with its first index)
+  RG_STAMP(1);
+  float bx = -INFINITY;             // thread maximum
+  int bt = -1;                      // greedy rows: first chunk holding it (its index is found after the stream)
+  bool first = true;                // the wave's first chunk (sets the threshold)
   int bi = 0x7FFFFFFF;
   int nanidx = 0x7FFFFFFF;          // first NaN id seen by this thread
   float ref = -INFINITY;            // logprob mass reference of this thread
   double zs = 0.0;
-  float theta = 3.40282347e38f;     // wave threshold (set after the first tile)
+  float theta = -3.40282347e38f;    // wave threshold (set on the wave's first chunk; a wave
+                                    // without chunks claims nothing)
   uint32_t nseg = 0;                // wave segment count (wave-uniform)
   bool over = false;
 
-  u32x4 cur[SVT], nxt[SVT];
-  uint32_t acur[SVT], anxt[SVT];
-  auto load_tile = [&](u32x4 (&d)[SVT], uint32_t (&ab)[SVT], int t) {
+  // Tile t's logits of this thread: history ids, illegal ids and vectors past
+  // the row set to -inf on the packed words (one LDS mask lookup per vector),
+  // then unpacked.
+  auto unpack_tile = [&](u32x4 (&raw)[SVT], const uint32_t (&ab)[SVT], int t, float (&x)[NE]) {
+    const bool part = (t + 1) * CV > nvec;
+    if (kill || part) {
+      uint32_t kb[SVT], any = 0;
 #pragma unroll
-    for (int i = 0; i < SVT; i++) {
-      const int v = min(t * TV + i * SNT + tid, nvec - 1);
-      d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + (int64_t)v * 16));
+      for (int i = 0; i < SVT; i++) {
+        const int v = t * CV + i * 64 + lane;
+        const uint32_t legal = AM ? (VPE == 8 ? ab[i] : ab[i] >> ((v & 1) * 4)) : VMASK;
+        kb[i] = v < nvec ? ((~legal & VMASK) | (pen ? bits_of(bmb, v) : 0u)) : VMASK;
+        any |= kb[i];
+      }
+      if (__builtin_amdgcn_ballot_w64(any != 0u)) {
+#pragma unroll
+        for (int i = 0; i < SVT; i++) {
+          const uint4 m = S.km[kb[i]];
+          raw[i].x = (m.x & NEGW) | (~m.x & raw[i].x);
+          raw[i].y = (m.y & NEGW) | (~m.y & raw[i].y);
+          raw[i].z = (m.z & NEGW) | (~m.z & raw[i].z);
+          raw[i].w = (m.w & NEGW) | (~m.w & raw[i].w);
+        }
+      }
     }
 #pragma unroll
-    for (int i = 0; i < SVT; i++) ab[i] = am ? bits_of(am, min(t * TV + i * SNT + tid, nvec - 1)) : VMASK;
-  };
-  load_tile(cur, acur, 0);
-  for (int t = 0; t < ntiles; t++) {
-    if (t + 1 < ntiles) load_tile(nxt, anxt, t + 1);
-    float x[NE];
-#pragma unroll
     for (int i = 0; i < SVT; i++) {
-      const int v = t * TV + i * SNT + tid;
-      const bool ok = v < nvec;
-      const uint32_t w[4] = {cur[i].x, cur[i].y, cur[i].z, cur[i].w};
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
       if constexpr (DT == LPS_DTYPE_F32) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) x[i * 4 + e] = ok ? __uint_as_float(w[e]) : -INFINITY;
+        for (int e = 0; e < 4; e++) x[i * 4 + e] = __uint_as_float(w[e]);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          x[i * 8 + e] = ok ? (DT == LPS_DTYPE_BF16 ? __uint_as_float(h << 16) : f16_to_f32(h)) : -INFINITY;
-        }
-      }
-      if (kill) {
-        const uint32_t kb = (~acur[i] & VMASK) | ((pen && ok) ? bits_of(bmb, v) : 0u);
-        if (__builtin_amdgcn_ballot_w64(kb != 0u)) {
-#pragma unroll
-          for (int e = 0; e < VPE; e++) x[i * VPE + e] = ((kb >> e) & 1u) ? -INFINITY : x[i * VPE + e];
+          x[i * 8 + e] = DT == LPS_DTYPE_BF16 ? __uint_as_float(h << 16) : f16_to_f32(h);
         }
       }
     }
-    // tile maximum and NaN
-    float m = -INFINITY;
-    bool tn = false;
+  };
+  // One tile: maxima (NaN-propagating), logprob mass, candidates.  Returns
+  // true when the wave's segment overflowed.
+  auto process_tile = [&](u32x4 (&raw)[SVT], const uint32_t (&ab)[SVT], int t) -> bool {
+    float x[NE];
+    unpack_tile(raw, ab, t, x);
+    float vm[SVT];  // vector maxima (NaN when the vector holds one)
 #pragma unroll
-    for (int s = 0; s < NE; s++) {
-      m = fmaxf(m, x[s]);
-      tn |= x[s] != x[s];
+    for (int i = 0; i < SVT; i++) {
+      float a = x[i * VPE];
+#pragma unroll
+      for (int e = 1; e < VPE; e++) a = __builtin_elementwise_maximum(a, x[i * VPE + e]);
+      vm[i] = a;
     }
-    if (tn) {
+    float m = vm[0];
+#pragma unroll
+    for (int i = 1; i < SVT; i++) m = __builtin_elementwise_maximum(m, vm[i]);
+    if (m != m) {  // a NaN: its first id
 #pragma unroll
       for (int s = 0; s < NE; s++)
         if (x[s] != x[s]) nanidx = min(nanidx, vid(t, s));
-    }
-    if (greedy) {
-      if (m > bx) {  // first index of the new maximum (ids rise with s)
-        int f = 0x7FFFFFFF;
-#pragma unroll
-        for (int s = NE - 1; s >= 0; s--)
-          if (x[s] == m) f = vid(t, s);
-        bx = m;
-        bi = f;
-      }
-    } else {
-      bx = fmaxf(bx, m);
+    } else if (m > bx) {
+      bx = m;
+      bt = t;
     }
     // logprob mass against this thread's reference
-    if (want_lp && m != -INFINITY && m != INFINITY) {
+    if (want_lp && m == m && m != -INFINITY && m != INFINITY) {
       const float nref = ceilf(__fmul_rn(m, c));
       if (nref > ref) {
         zs = ref == -INFINITY ? 0.0 : ldexp(zs, (int)(ref - nref));
@@ -290,45 +431,54 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
         zs += (double)a;
       }
     }
-    // candidates
-    if (kc > 0) {
-      if (t == 0) {
-        // the wave's first threshold: at least kc logits of its first tile lie at or above it
-        uint32_t th;
-        if (kc <= 64) {
-          const uint32_t v1[1] = {f2key(m)};
-          th = wave_kth_largest<1>(v1, (uint32_t)kc);
-        } else {
-          float m2 = -INFINITY;  // the thread's second largest of the tile
-          bool seen = false;
+    if (kc <= 0) return false;
+    if (first) {
+      first = false;
+      // the wave's first threshold: at least kc logits of its first tile lie at or above it
+      const float mt = m == m ? m : -INFINITY;
+      uint32_t th;
+      if (kc <= 64) {
+        const uint32_t v1[1] = {f2key(mt)};
+        th = wave_kth_largest<1>(v1, (uint32_t)kc);
+      } else {
+        float m2 = -INFINITY;  // the thread's second largest of the tile
+        bool seen = false;
 #pragma unroll
-          for (int s = 0; s < NE; s++) {
-            const bool first = !seen && x[s] == m;
-            seen |= first;
-            m2 = first ? m2 : fmaxf(m2, x[s]);
-          }
-          const uint32_t v2[2] = {f2key(m), f2key(m2)};
-          th = wave_kth_largest<2>(v2, (uint32_t)kc);
+        for (int s = 0; s < NE; s++) {
+          const bool first = !seen && x[s] == mt;
+          seen |= first;
+          m2 = first ? m2 : fmaxf(m2, x[s]);
         }
-        if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
-        theta = fmaxf(key2f(th), -3.40282347e38f);
-        // a first tile whose candidates would fill half the segment (short
-        // rows, large k'): the exact kc-th largest of the wave's tile instead
-        uint32_t cnt = 0;
-#pragma unroll
-        for (int s = 0; s < NE; s++) cnt += (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(x[s] >= theta));
-        if (cnt > (uint32_t)(SEG / 2)) {
-          uint32_t kv[NE];
-#pragma unroll
-          for (int s = 0; s < NE; s++) kv[s] = x[s] == x[s] ? f2key(x[s]) : 0u;
-          th = wave_kth_largest<NE>(kv, (uint32_t)kc);
-          if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
-          theta = fmaxf(theta, fmaxf(key2f(th), -3.40282347e38f));
-        }
+        const uint32_t v2[2] = {f2key(mt), f2key(m2)};
+        th = wave_kth_largest<2>(v2, (uint32_t)kc);
       }
+      theta = key_threshold(th, greedy, T);
+      {  // the wave's first joint share: ceil(k'/8) lane maxima at or above it
+        const uint32_t v1[1] = {f2key(mt)};
+        const float share = key_threshold(wave_kth_largest<1>(v1, (uint32_t)((kc + SNW - 1) / SNW)), greedy, T);
+        if (lane == 0) S.segjt[wv] = share;
+      }
+      // a first tile whose candidates would fill half the segment (short
+      // rows, large k'): the exact kc-th largest of the wave's tile instead
+      uint32_t cnt = 0;
 #pragma unroll
-      for (int s = 0; s < NE; s++) {
-        const bool on = x[s] >= theta;
+      for (int s = 0; s < NE; s++) cnt += (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(x[s] >= theta));
+      if (cnt > (uint32_t)(SEG / 2)) {
+        th = wave_kth_largest_x<NE>(x, (uint32_t)kc);
+        if (!greedy && th > kNegInfKey + 1u && th != 0xFFFFFFFFu) th = f2key(collision_lo(key2f(th), T));
+        theta = fmaxf(theta, fmaxf(key2f(th), -3.40282347e38f));
+      }
+    }
+    // candidates (at or above the wave's own threshold and the joint one):
+    // vectors whose maximum reaches it in any lane, then their elements
+    const float te = fmaxf(theta, joint_threshold(S));
+#pragma unroll
+    for (int i = 0; i < SVT; i++) {
+      if (!__builtin_amdgcn_ballot_w64(vm[i] >= te)) continue;
+#pragma unroll
+      for (int e = 0; e < VPE; e++) {
+        const int s = i * VPE + e;
+        const bool on = x[s] >= te;
         const uint64_t bm = __builtin_amdgcn_ballot_w64(on);
         if (bm) {
           if (on) {
@@ -341,24 +491,63 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
           nseg += (uint32_t)__popcll(bm);
         }
       }
-      if (nseg > (uint32_t)SEG) {
-        over = true;
-        break;
-      }
-      if (nseg > (uint32_t)(SEG / 2)) wave_refine(S, wv, nseg, kc, greedy, T, theta);
     }
+    if (nseg > (uint32_t)SEG) return true;
+    if (nseg > (uint32_t)(SEG / 2)) wave_refine(S, wv, nseg, kc, greedy, T, theta);
+    return false;
+  };
+  // three chunk buffers: once a chunk is processed its buffer loads the wave's
+  // next chunk, so two chunks of loads are in flight behind the one processed;
+  // the chunks a wave takes rise, so its ids rise with them
+  auto take = [&]() -> int {
+    int h = 0;
+    if (lane == 0) h = atomicAdd(&S.mi[2], 1);
+    return __builtin_amdgcn_readfirstlane(h) + 3 * SNW;
+  };
+  // Every step issues its buffer's next load (the last chunk again once the
+  // row is done), so every path into the loop's head has issued the same loads
+  // in the same order and the compiler's load-count waits stay two chunks deep.
+  auto step = [&](u32x4 (&d)[SVT], uint32_t (&ab)[SVT], int& h) {
+    const bool live = h < nch && !over;
+    if (live) over = process_tile(d, ab, h);
+    h = (live && !over) ? take() : nch;
+    load_tile(d, ab, h);
+  };
+  do {
+    step(b0, a0, c0);
+    step(b1, a1, c1);
+    step(b2, a2, c2);
+  } while (c0 < nch && !over);
+  RG_STAMP(2);
+  // the history ids' logits (id 0 for empty slots: no divergent loads),
+  // loaded before the barrier below
+  constexpr int HPT_ = HASH_CAP / SNT;
+  constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
+  uint32_t hraw[HPT_];
+  int hid[HPT_];
 #pragma unroll
-    for (int i = 0; i < SVT; i++) {
-      cur[i] = nxt[i];
-      acur[i] = anxt[i];
-    }
+  for (int q = 0; q < HPT_; q++) {
+    hid[q] = pen ? S.hkey[tid + q * SNT] : -1;
+    const int64_t o = (int64_t)max(hid[q], 0) * ES;
+    if constexpr (ES == 4) hraw[q] = *reinterpret_cast<const uint32_t*>(row + o);
+    else hraw[q] = *reinterpret_cast<const unsigned short*>(row + o);
+  }
+  // greedy rows: the first index of the thread's maximum, from its first tile holding it
+  if (greedy && bt >= 0) {
+    load_tile(b0, a0, bt);
+    float x[NE];
+    unpack_tile(b0, a0, bt, x);
+#pragma unroll
+    for (int s = NE - 1; s >= 0; s--)
+      if (x[s] == bx) bi = vid(bt, s);
   }
   if (lane == 0) {
     S.segn[wv] = over ? SEG + 1 : (int)nseg;
-    S.segth[wv] = kc > 0 ? theta : 3.40282347e38f;
+    S.segth[wv] = theta;
   }
   __syncthreads();
-  float ths = -3.40282347e38f;  // theta*: the largest wave threshold
+  // theta*: the largest own threshold, or the joint one when larger
+  float ths = joint_threshold(S);
   bool seg_over = false;
 #pragma unroll
   for (int w = 0; w < SNW; w++) {
@@ -381,20 +570,19 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     pk[q] = pk[q] && !(__uint_as_float(px[q]) < ths);
   }
 
-  // ---- history ids: read, mask, penalise, fold in ----
-  constexpr int HPT_ = HASH_CAP / SNT;
+  RG_STAMP(3);
+  // ---- history ids: mask, penalise, fold in ----
   uint32_t hx[HPT_];
-  int hid[HPT_];
   bool hk[HPT_];
 #pragma unroll
   for (int q = 0; q < HPT_; q++) {
     const int s = tid + q * SNT;
-    const int id = pen ? S.hkey[s] : -1;
+    const int id = hid[q];
     hk[q] = false;
-    hid[q] = id;
     hx[q] = 0u;
     if (id >= 0) {
-      float xv = load1<DT, false>(row, id);
+      float xv = ES == 4 ? __uint_as_float(hraw[q])
+                         : (DT == LPS_DTYPE_BF16 ? __uint_as_float(hraw[q] << 16) : f16_to_f32(hraw[q]));
       if (!id_allowed(am, id)) xv = -INFINITY;
       xv = penalize(xv, S.hcnt[s], g.rep, g.pres, g.freq);
       hx[q] = __float_as_uint(xv);
@@ -420,9 +608,28 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   }
 
   // ---- the row: maximum, first argmax, NaN, log-sum-exp ----
+  // maximum and first argmax, first NaN, logprob reference: one barrier
   const uint64_t bk = ((uint64_t)f2key(bx) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)bi);
-  const uint64_t rk = bred<SNW>(bk, S.q, OpMax{});
-  const int nanr = bred<SNW>(nanidx, S.i1, OpMin{});
+  {
+    const uint64_t wk = wreduce(bk, OpMax{});
+    const int wn = wreduce(nanidx, OpMin{});
+    const float wr = wreduce(ref, OpMax{});
+    if (lane == 0) {
+      S.q[wv] = wk;
+      S.i1[wv] = wn;
+      S.rf[wv] = wr;
+    }
+  }
+  __syncthreads();
+  uint64_t rk = S.q[0];
+  int nanr = S.i1[0];
+  float R = S.rf[0];
+#pragma unroll
+  for (int w = 1; w < SNW; w++) {
+    rk = max(rk, S.q[w]);
+    nanr = min(nanr, S.i1[w]);
+    R = fmaxf(R, S.rf[w]);
+  }
   float xmax = key2f((uint32_t)(rk >> 32));
   int gam = key_index(rk);
   if (nanr != 0x7FFFFFFF) {
@@ -431,9 +638,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   }
   const bool xfin = xmax == xmax && xmax != INFINITY && xmax != -INFINITY;
   double Z = 0.0;
-  float R = -INFINITY;
   if (want_lp) {
-    R = bred<SNW>(ref, S.rf, OpMax{});
     const double zsc = (ref != -INFINITY && R != -INFINITY) ? ldexp(zs, (int)(ref - R)) : 0.0;
     Z = bred<SNW>(zsc, S.d, OpAdd{});
     if (!xfin) Z = 0.0;
@@ -445,6 +650,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   }
   int reason = defer_hist ? 14 : (seg_over ? 15 : 0);
 
+  RG_STAMP(4);
   // ---- pool, part 2: keys (z descending, index ascending); every segment
   // entry was read before the barriers of the reductions above ----
   const float Rm = xfin ? ceilf(__fmul_rn(xmax, c)) : 0.0f;
@@ -495,18 +701,29 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   }
   if (reason == 0 && kc > 0 && n > KM) reason = 16;
 
+  RG_STAMP(5);
   // ---- rank sort: each wave ranks 64 entries at a time against every key ----
   if (reason == 0 && kc > 0) {
+    if (tid < 8 && n + tid < ((n + 7) & ~7)) S.b.ck[n + tid] = 0ull;  // (n <= KM < POOL)
+    __syncthreads();
     for (int e0 = wv * 64; e0 < n; e0 += SNT) {
       const int e = e0 + lane;
       const uint64_t key = e < n ? S.b.ck[e] : 0ull;
+      // (eight keys per step, read as four 16-byte broadcasts issued together;
+      // the pool is padded with zero keys up to a multiple of 8, none of which
+      // ranks above an entry)
       int rank = 0;
-      int q = 0;
-      for (; q + 2 <= n; q += 2) {
-        const uint64_t a0 = S.b.ck[q], a1 = S.b.ck[q + 1];
-        rank += (a0 > key ? 1 : 0) + (a1 > key ? 1 : 0);
+      const uint4* k4 = reinterpret_cast<const uint4*>(S.b.ck);
+      for (int q = 0; q < n; q += 8) {
+        uint4 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) w[j] = k4[(q >> 1) + j];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint64_t a0 = ((uint64_t)w[j].y << 32) | w[j].x, a1 = ((uint64_t)w[j].w << 32) | w[j].z;
+          rank += (a0 > key ? 1 : 0) + (a1 > key ? 1 : 0);
+        }
       }
-      if (q < n) rank += S.b.ck[q] > key ? 1 : 0;
       if (e < n) {
         S.a.s.sk[rank] = key;
         S.a.s.sm[rank] = zmass_fix(key2f(key_z(key)), Rm);
@@ -518,6 +735,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     if (tid == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
     return;
   }
+  RG_STAMP(6);
   // ---- the decision (waves 0-3; the others leave) and the outputs ----
   if (tid >= FT) return;
   Decision d;
@@ -540,6 +758,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     d.chosen_z = xmax;
   }
   if (greedy) status = 0;
+  RG_STAMP(7);
   int64_t token = status ? -1 : d.token;
   if (P.skip_draw && !greedy) token = -1;
   double lnZ = 0.0;
@@ -572,6 +791,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     if (P.kept_count) P.kept_count[r] = d.kept_n;
     if (P.row_path) P.row_path[r] = 0;
   }
+  RG_STAMP(8);
 }
 
 }  // namespace st
