@@ -79,9 +79,15 @@
       ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = __builtin_amdgcn_s_memrealtime();             \
     }                                                                                             \
   } while (0)
+// a value (not a time) in slot i
+#define RG_STAMP_VAL(i, v)                                                                       \
+  do {                                                                                            \
+    if (threadIdx.x == 0 && blockIdx.x < 8192) ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = (uint64_t)(v); \
+  } while (0)
 #else
 #define RG_STAMP(i) ((void)0)
 #define RG_STAMP_DEP(i, v) ((void)0)
+#define RG_STAMP_VAL(i, v) ((void)0)
 #endif
 
 namespace lps {

@@ -547,6 +547,96 @@ __device__ __forceinline__ void merge_lists_g(RgFinalS& S, int G, int D, int N0,
   else merge_lists<MAXG>(S, G, D, N0, N1, Rm);
 }
 
+// Top-k rows: the merged list 0 without the merge.  Every chunk's list holds
+// its logits from the top down.  If j chunks each hold m entries at or above
+// z = t, and j m >= kc, the row's kc-th largest z is at least t: so for m =
+// kc, kc/2, kc/4, kc/8 (rounded up) the j = ceil(kc / m)-th largest of the
+// chunks' m-th entries bounds it from below, and the largest of the four
+// bounds is kept.  The entries whose z reaches it (all the top-kc set, ties
+// included: typically 1.2-2 kc entries) are compacted into list 1's storage,
+// unused by top-k rows, then rank-sorted into sk[0] / sx[0] / sm[0].
+// Returns their count, or -1 when more than KM are left (the caller merges
+// instead).  FT threads; ends with a barrier.
+__device__ __forceinline__ int select_topk_lists(RgFinalS& S, int G, int kc, int N1, float Rm) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (wv == 0) {
+    // lanes 16 i + q: chunk q's m_i-th entry; a 32-step search per group of
+    // 16 lanes for the j_i-th largest (0 when fewer than j_i chunks hold m_i)
+    const int grp = lane >> 4, q = lane & 15;
+    const int m = (kc + (1 << grp) - 1) >> grp;
+    const uint32_t jn = (uint32_t)((kc + m - 1) / m);
+    uint32_t v = 0u;
+    if (q < G && S.cn[0][q] >= m) v = key_z(S.lk[0][S.cb[0][q] + m - 1]);
+    uint32_t t = 0u;
+#pragma unroll 1
+    for (int b = 31; b >= 0; b--) {
+      const uint32_t c = t | (1u << b);
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(v >= c);
+      const uint32_t cnt = (uint32_t)__builtin_popcount((uint32_t)(bal >> (16 * grp)) & 0xFFFFu);
+      t = cnt >= jn ? c : t;
+    }
+    t = wreduce(t, OpMax{});
+    if (lane == 0) S.mi[26] = (int)t;
+  }
+  __syncthreads();
+  const uint32_t zt = (uint32_t)S.mi[26];
+  // compaction (in any order: the rank sort below fixes it)
+  constexpr int EPT = LKM / FT;
+  uint64_t kk[EPT];
+  uint32_t xx[EPT];
+  uint32_t keep = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; i++) {
+    const int f = i * FT + tid;
+    kk[i] = f < N1 ? S.lk[0][f] : 0ull;
+    xx[i] = f < N1 ? S.lx[0][f] : 0u;
+    keep += (f < N1 && key_z(kk[i]) >= zt) ? 1u : 0u;
+  }
+  uint32_t tot;
+  uint32_t pos = bscan<FW>(keep, &tot, S.u3);
+  const int n = (int)tot;
+  if (n > KM) {
+    __syncthreads();
+    return -1;
+  }
+#pragma unroll
+  for (int i = 0; i < EPT; i++) {
+    const int f = i * FT + tid;
+    if (f < N1 && key_z(kk[i]) >= zt) {
+      S.sk[1][pos] = kk[i];
+      S.sx[1][pos] = xx[i];
+      pos++;
+    }
+  }
+  __syncthreads();
+  // rank sort (keys are distinct: the index is in the low word): each wave
+  // ranks 64 entries at a time, against 64 keys per register load, read back
+  // lane by lane
+  for (int e0 = wv * 64; e0 < n; e0 += FT) {
+    const int e = e0 + lane;
+    const uint64_t key = e < n ? S.sk[1][e] : 0ull;
+    uint32_t rank = 0;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const uint64_t kj = j0 + lane < n ? S.sk[1][j0 + lane] : 0ull;  // 0 ranks below every key
+      const uint32_t hi = (uint32_t)(kj >> 32), lo = (uint32_t)kj;
+#pragma unroll
+      for (int l = 0; l < 64; l++) {
+        const uint64_t a = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, l) << 32) |
+                           (uint64_t)(uint32_t)__builtin_amdgcn_readlane(lo, l);
+        rank += a > key ? 1u : 0u;
+      }
+    }
+    if (e < n) {
+      S.sk[0][rank] = key;
+      S.sx[0][rank] = S.sx[1][e];
+      S.sm[0][rank] = zmass_fix(key2f(key_z(key)), Rm);
+    }
+  }
+  __syncthreads();
+  return n;
+}
+
 // Inclusive prefix of masses m[0, n) into c[0, n) over FT threads (KPT
 // positions per thread, n <= KM).  Ends with a barrier.
 __device__ __forceinline__ void scan_one(const uint64_t* m, uint64_t* c, int n, uint64_t* slot) {
@@ -834,10 +924,18 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   RG_STAMP(26);
   if (greedy) status = 0;
 
-  // ---- merge the chunks' sorted lists ----
+  // ---- merge the chunks' sorted lists (top-k rows: select, then sort) ----
   RG_STAMP(16);
-  merge_lists_g(S, G, D, N1, N2, Rm);
-  __syncthreads();
+  int K = min(N1, KM);  // merged positions of list 0 present
+  int Ntot = N1;
+  const int nsel = (g.kprime > 0 && N2 == 0) ? select_topk_lists(S, G, g.kprime, N1, Rm) : -1;
+  RG_STAMP_VAL(23, nsel + 100000);
+  if (nsel >= 0) {
+    K = Ntot = nsel;
+  } else {
+    merge_lists_g(S, G, D, N1, N2, Rm);
+    __syncthreads();
+  }
   RG_STAMP(27);
 
   int64_t token = -1;
@@ -845,12 +943,11 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   int32_t ties = -1, kept_n = 0;
   int ntop_out = 0;
   const int64_t qtok = g.qtok;
-  const int K = min(N1, KM);  // merged positions of list 0 present
 
   if (status == 0 && g.kprime > 0) {
     // ======================= top-k (and top-N logprobs) =======================
     Decision d;
-    const int rc = topk_decide(g, V, S.sk[0], S.sm[0], S.sc[0], K, N1, u, gam, xmax, S, d);
+    const int rc = topk_decide(g, V, S.sk[0], S.sm[0], S.sc[0], K, Ntot, u, gam, xmax, S, d);
     if (rc) return rc;
     token = d.token; cut = d.cut; qprob = d.qprob; chosen_z = d.chosen_z;
     ties = d.ties; kept_n = d.kept_n; ntop_out = d.ntop_out; status |= d.status;
