@@ -551,8 +551,11 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   // The Leviathan residual reads the general kernel's per-row plans; otherwise
   // both row sets take the fast kernels (rows they cannot finish exactly go
   // to the general kernel after them), with the same results.
+  // Every row shares the temperature and top-p: the row-kind hint that skips
+  // the kernel no row needs (T > 0: nucleus or pure rows; else greedy).
+  const int hint = a->temperature > 0.0f ? LPS_FLAG_ROWS_NUCLEUS : LPS_FLAG_ROWS_TOPK;
   bool vec = vec_ok(a->target_logits, a->dtype, V, k + 1, a->target_stride_b, a->target_stride_k);
-  if ((lev ? dispatch_gen(a->dtype, vec, P, s) : run_sample(P, a->dtype, vec, w.fast, w.fast_bytes, 0, s)) !=
+  if ((lev ? dispatch_gen(a->dtype, vec, P, s) : run_sample(P, a->dtype, vec, w.fast, w.fast_bytes, hint, s)) !=
       hipSuccess)
     return LPS_ELAUNCH;
 
@@ -572,7 +575,7 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   D.plans = w.plans + (size_t)B * (k + 1);
   vec = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
   // (planned for the target rows' count, for which the workspace is sized)
-  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, 0, s, P.R)) !=
+  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, hint, s, P.R)) !=
       hipSuccess)
     return LPS_ELAUNCH;
 

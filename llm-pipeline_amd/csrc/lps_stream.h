@@ -209,16 +209,18 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   // Chunk h's loads (h is clamped to the last chunk, so every call issues the
   // same loads and the compiler's load counters stay exact): four 16-byte
   // vectors per lane, and with masks their legality bytes.
+  // (a tile past the row's end, loaded so that every step issues the same
+  // loads, reads the row's first vector on every lane: one line, not a tile)
   auto load_tile = [&](u32x4 (&d)[SVT], uint32_t (&ab)[SVT], int h) {
-    h = min(h, nch - 1);
+    const bool past = h >= nch;
 #pragma unroll
     for (int i = 0; i < SVT; i++) {
-      const int v = min(h * CV + i * 64 + lane, nvec - 1);
+      const int v = past ? 0 : min(h * CV + i * 64 + lane, nvec - 1);
       d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + (int64_t)v * 16));
     }
 #pragma unroll
     for (int i = 0; i < SVT; i++) {
-      const int v = min(h * CV + i * 64 + lane, nvec - 1);
+      const int v = past ? 0 : min(h * CV + i * 64 + lane, nvec - 1);
       if constexpr (AM) ab[i] = VPE == 8 ? (uint32_t)am[v] : (uint32_t)am[v >> 1];
       else ab[i] = 0xFFu;
     }
