@@ -91,6 +91,7 @@ struct StShared : RgX {
   float segth[SNW];                     // wave thresholds (each wave: >= k' own logits at or above)
   float segjt[SNW];                     // joint shares (each wave: >= ceil(k'/8) own logits at or above)
   int32_t pn;                           // pool count
+  RowCfg cfg;                           // the row's parameters (loaded by wave 0)
 };
 static_assert(sizeof(StShared) <= 80 * 1024, "two workgroups per CU");
 
@@ -206,21 +207,20 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     return b + h * CV * VPE + (s / VPE) * 64 * VPE + (s % VPE);
   };
 
-  // Chunk h's loads (h is clamped to the last chunk, so every call issues the
-  // same loads and the compiler's load counters stay exact): four 16-byte
-  // vectors per lane, and with masks their legality bytes.
+  // Chunk h's loads (every call issues the same loads, so the compiler's load
+  // counters stay exact): four 16-byte vectors per lane, and with masks their
+  // legality bytes.
   // (a tile past the row's end, loaded so that every step issues the same
-  // loads, reads the row's first vector on every lane: one line, not a tile)
+  // loads, reads the row's last vector on every lane: one line, not a tile)
   auto load_tile = [&](u32x4 (&d)[SVT], uint32_t (&ab)[SVT], int h) {
-    const bool past = h >= nch;
 #pragma unroll
     for (int i = 0; i < SVT; i++) {
-      const int v = past ? 0 : min(h * CV + i * 64 + lane, nvec - 1);
+      const int v = min(h * CV + i * 64 + lane, nvec - 1);
       d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + (int64_t)v * 16));
     }
 #pragma unroll
     for (int i = 0; i < SVT; i++) {
-      const int v = past ? 0 : min(h * CV + i * 64 + lane, nvec - 1);
+      const int v = min(h * CV + i * 64 + lane, nvec - 1);
       if constexpr (AM) ab[i] = VPE == 8 ? (uint32_t)am[v] : (uint32_t)am[v >> 1];
       else ab[i] = 0xFFu;
     }
@@ -231,8 +231,11 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   const int32_t* hsrc = hrow0 ? hrow0 : reinterpret_cast<const int32_t*>(row);
   const int hraw0 = hsrc[min((int64_t)tid, max(P.history_stride - 1, (int64_t)0))];
   const int hraw1 = hsrc[min((int64_t)(tid + SNT), max(P.history_stride - 1, (int64_t)0))];
+  // (wave 0 alone loads the parameters, ahead of its chunks; the other waves'
+  // would queue behind the chunks the first waves issued)
   __asm__ volatile("" ::: "memory");
-  const RowCfg g = row_cfg(P, r);
+  RowCfg g0;
+  if (wv == 0) g0 = row_cfg(P, r);
   __asm__ volatile("" ::: "memory");
   // chunks: each wave takes chunks wv, wv + 8, wv + 16, then the next free one
   // (a counter in LDS), so waves that run faster take more of the row
@@ -242,25 +245,11 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   // (in this order: the loop's waits count on b1 being followed by b2's loads)
   load_tile(b0, a0, c0);
   __asm__ volatile("" ::: "memory");
-  load_tile(b1, a1, c1);
-  __asm__ volatile("" ::: "memory");
-  load_tile(b2, a2, c2);
   __asm__ volatile("" ::: "memory");
   const int hid0 = (hrow0 && (int64_t)tid < P.history_stride) ? hraw0 : -1;
   const int hid1 = (hrow0 && (int64_t)(tid + SNT) < P.history_stride) ? hraw1 : -1;
 
-  RG_STAMP_DEP(9, g.T);
-  if (!stream_takes(g)) {
-    // the row-group kernel's rows; deferred when it is not launched
-    if (F.stream_only && tid == 0) F.status[r] = LPS_ROW_DEFERRED | (16 << 8);
-    return;
-  }
-  const bool greedy = g.greedy;
-  const float T = g.T, c = g.c;
-  const int kc = g.kprime;
-  const bool want_lp = P.chosen_logprob || g.ntop > 0;
-  const bool pen = g.pen;
-  const bool kill = pen || am;
+  if (wv == 0 && lane == 0) S.cfg = g0;
 
   // ---- kill-mask table: pattern p (bit e = element e of a vector) -> the
   // bits of the vector's four words that belong to killed elements ----
@@ -275,8 +264,9 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     }
     S.km[tid] = make_uint4(mk[0], mk[1], mk[2], mk[3]);
   }
-  // ---- the history: bitmap of the distinct in-range ids, and their counts ----
-  if (pen) {
+  // ---- the history: bitmap of the distinct in-range ids, and their counts
+  // (cleared before the parameters are known: one barrier for both) ----
+  {
     const int nw = (V + 31) >> 5;
     for (int i = tid; i < nw; i += SNT) S.a.bm[i] = 0u;
     for (int i = tid; i < HASH_CAP; i += SNT) {
@@ -293,6 +283,19 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     S.pn = 0;
   }
   __syncthreads();
+  const RowCfg g = S.cfg;
+  RG_STAMP_DEP(9, g.T);
+  if (!stream_takes(g)) {
+    // the row-group kernel's rows; deferred when it is not launched
+    if (F.stream_only && tid == 0) F.status[r] = LPS_ROW_DEFERRED | (16 << 8);
+    return;
+  }
+  const bool greedy = g.greedy;
+  const float T = g.T, c = g.c;
+  const int kc = g.kprime;
+  const bool want_lp = P.chosen_logprob || g.ntop > 0;
+  const bool pen = g.pen;
+  const bool kill = pen || am;
   RG_STAMP(11);
   // (without a frequency penalty an id's count does not matter: the bitmap
   // decides membership, and the thread whose bit-set finds the bit clear
@@ -301,13 +304,23 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   if (pen) {
     bool full = false;
     uint32_t fresh = 0;  // distinct ids this thread inserted
-    auto insert = [&](int id) {
-      if (id < 0 || id >= V) return;
-      const uint32_t bit = 1u << (id & 31);
-      const uint32_t had = atomicOr(&S.a.bm[id >> 5], bit) & bit;
-      if (!counts) {
-        if (!had) {
-          const int p = atomicAdd(&S.mi[3], 1);
+    // without counts: every lane of the wave calls it (id < 0: none); the
+    // wave's new ids take consecutive list slots, one LDS atomic per wave
+    auto insert_list = [&](int id) {
+      bool nw_id = false;
+      if (id >= 0 && id < V) {
+        const uint32_t bit = 1u << (id & 31);
+        nw_id = !(atomicOr(&S.a.bm[id >> 5], bit) & bit);
+      }
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(nw_id);
+      if (bal) {
+        const int lead = __builtin_ctzll(bal);
+        int base = 0;
+        if (lane == lead) base = atomicAdd(&S.mi[3], __builtin_popcountll(bal));
+        base = __shfl(base, lead);
+        if (nw_id) {
+          const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
           if (p < HASH_CAP) {
             S.hkey[p] = id;
             S.hcnt[p] = 1;
@@ -316,8 +329,11 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
           }
           fresh++;
         }
-        return;
       }
+    };
+    auto insert = [&](int id) {
+      if (id < 0 || id >= V) return;
+      atomicOr(&S.a.bm[id >> 5], 1u << (id & 31));
       uint32_t sl = hash_id(id);
       int p = 0;
       for (; p < HASH_CAP; p++) {
@@ -331,15 +347,28 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
       }
       if (p == HASH_CAP) full = true;
     };
-    if (tid < g.hlen) insert(hid0);
-    if (tid + SNT < g.hlen) insert(hid1);
-    for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) insert(g.hrow[j]);
+    if (!counts) {
+      insert_list(tid < g.hlen ? hid0 : -1);
+      insert_list(tid + SNT < g.hlen ? hid1 : -1);
+      for (int j0 = 2 * SNT; j0 < g.hlen; j0 += SNT) insert_list(j0 + tid < g.hlen ? g.hrow[j0 + tid] : -1);
+    } else {
+      if (tid < g.hlen) insert(hid0);
+      if (tid + SNT < g.hlen) insert(hid1);
+      for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) insert(g.hrow[j]);
+    }
     if (fresh) atomicAdd(&S.mi[1], (int)fresh);
     if (full) S.mi[0] = 1;
   }
   __syncthreads();
   RG_STAMP(10);
   const bool defer_hist = pen && (S.mi[0] != 0 || S.mi[1] > LPS_MAX_HISTORY_DISTINCT);
+  // (the second and third chunks only now: a first flood of every wave's three
+  // chunks would hold the parameters and history ids above back behind it)
+  __asm__ volatile("" ::: "memory");
+  load_tile(b1, a1, c1);
+  __asm__ volatile("" ::: "memory");
+  load_tile(b2, a2, c2);
+  __asm__ volatile("" ::: "memory");
 
   RG_STAMP(1);
   float bx = -INFINITY;             // thread maximum
