@@ -242,9 +242,6 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   int c0 = wv, c1 = wv + SNW, c2 = wv + 2 * SNW;
   u32x4 b0[SVT], b1[SVT], b2[SVT];
   uint32_t a0[SVT], a1[SVT], a2[SVT];
-  // (in this order: the loop's waits count on b1 being followed by b2's loads)
-  load_tile(b0, a0, c0);
-  __asm__ volatile("" ::: "memory");
   __asm__ volatile("" ::: "memory");
   const int hid0 = (hrow0 && (int64_t)tid < P.history_stride) ? hraw0 : -1;
   const int hid1 = (hrow0 && (int64_t)(tid + SNT) < P.history_stride) ? hraw1 : -1;
@@ -362,8 +359,11 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   __syncthreads();
   RG_STAMP(10);
   const bool defer_hist = pen && (S.mi[0] != 0 || S.mi[1] > LPS_MAX_HISTORY_DISTINCT);
-  // (the second and third chunks only now: a first flood of every wave's three
-  // chunks would hold the parameters and history ids above back behind it)
+  // (the chunks only now, in this order: the loop's waits count on b0, b1 and
+  // b2's loads in turn; a first flood of every wave's chunks would hold the
+  // parameters and history ids above back behind it)
+  __asm__ volatile("" ::: "memory");
+  load_tile(b0, a0, c0);
   __asm__ volatile("" ::: "memory");
   load_tile(b1, a1, c1);
   __asm__ volatile("" ::: "memory");
