@@ -779,48 +779,35 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   for (int e = FP1; e < FPT; e++) cv[e] = make_uint4(0u, 0u, 0u, 0u);
 
   // ---- F1: the chunk summaries (wave 0; lane q < G holds chunk q's).  The
-  // chunks are combined with readlanes, field by field, so the combines of
-  // different fields are independent ----
+  // chunks are combined with reductions and prefix sums over the first 16
+  // lanes (G <= 16), all independent of each other; the row mass is summed in
+  // the same order as the chunks' own (wsum) ----
   if (wv == 0) {
     RgSum a{};
     if (lane < G) a = ld_pub(sums + lane);
     RG_STAMP_DEP(19, a.mkey);
-    uint32_t fl = 0, xm = 0, mk = 0, nab = 0, nanb = 0;
-    float R = -INFINITY;
-    int nmax = 0, n1b = 0, n2b = 0, ob = 0, n1t = 0, n2t = 0, ot = 0;
-    for (int q = 0; q < G; q++) {
-      fl |= rdlane(a.flags, q);
-      xm |= 1u << rdlane(a.xcc, q);
-      mk = max(mk, rdlane(a.mkey, q));
-      const float rq = rdlane(a.ref, q);
-      if (rq != INFINITY && rq != -INFINITY) R = fmaxf(R, rq);
-      nab += rdlane(a.nab1, q);
-      nanb = max(nanb, rdlane(a.nanbin, q));
-      const int c1 = (int)rdlane((uint32_t)a.n1, q), c2 = (int)rdlane((uint32_t)a.n2, q);
-      const int co = c1 + c2 > K0 ? c1 + c2 - K0 : 0;
-      nmax = max(nmax, max(c1, c2));
-      // this lane's prefixes (chunks before it)
-      n1b += q < lane ? c1 : 0;
-      n2b += q < lane ? c2 : 0;
-      ob += q < lane ? co : 0;
-      n1t += c1;
-      n2t += c2;
-      ot += co;
-    }
+    const bool in = lane < G;
+    const bool rfin = in && a.ref != INFINITY && a.ref != -INFINITY;
+    const int c1 = in ? (int)a.n1 : 0, c2 = in ? (int)a.n2 : 0;
+    const int co = c1 + c2 > K0 ? c1 + c2 - K0 : 0;
+    uint32_t fl = rreduce16(in ? a.flags : 0u, OpOr{});
+    const uint32_t xm = rreduce16(in ? 1u << a.xcc : 0u, OpOr{});
+    const uint32_t mk = rreduce16(in ? a.mkey : 0u, OpMax{});
+    const float R = rreduce16(rfin ? a.ref : -INFINITY, OpMax{});
+    const uint32_t nab = rreduce16(in ? a.nab1 : 0u, OpAdd{});
+    const uint32_t nanb = rreduce16(in ? a.nanbin : 0u, OpMax{});
+    const int nmax = rreduce16(max(c1, c2), OpMax{});
+    const int i1 = rscan16(c1), i2 = rscan16(c2), io = rscan16(co);
+    // this lane's prefixes (chunks before it) and the totals (lanes >= G add 0)
+    const int n1b = i1 - c1, n2b = i2 - c2, ob = io - co;
+    const int n1t = rdlane(i1, 15), n2t = rdlane(i2, 15), ot = rdlane(io, 15);
     if (__builtin_popcount(xm) > 1) fl |= RF_SPLIT;
     RG_STAMP_DEP(20, fl);
-    int am = 0x7FFFFFFF;
-    double Z = 0.0, A1 = 0.0, A2 = 0.0;
-    for (int q = 0; q < G; q++) {
-      if (rdlane(a.mkey, q) == mk) am = min(am, (int)rdlane((uint32_t)a.amax, q));
-      const float rq = rdlane(a.ref, q);
-      if (rq != INFINITY && rq != -INFINITY) {
-        const double sc = ldexp(1.0, (int)(rq - R));
-        Z += rdlane(a.zsum, q) * sc;
-        A1 += rdlane(a.ab1, q) * sc;
-        A2 += rdlane(a.ab2, q) * sc;
-      }
-    }
+    const int am = rreduce16(in && a.mkey == mk ? (int)a.amax : 0x7FFFFFFF, OpMin{});
+    const double sc = rfin ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
+    const double Z = rreduce16(rfin ? a.zsum * sc : 0.0, OpAdd{});
+    const double A1 = rreduce16(rfin ? a.ab1 * sc : 0.0, OpAdd{});
+    const double A2 = rreduce16(rfin ? a.ab2 * sc : 0.0, OpAdd{});
     if (lane < G) {
       S.cn[0][lane] = (int)a.n1;
       S.cn[1][lane] = (int)a.n2;

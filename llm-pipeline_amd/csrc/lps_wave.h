@@ -93,6 +93,28 @@ __device__ __forceinline__ T wscan_incl(T v) {
   return v;
 }
 
+// Reduction over lanes 0-15 (the first row; the other rows' values do not
+// enter), in every lane.  With the other rows holding the identity it equals
+// wreduce bit for bit (the same steps, then exact combines with the identity).
+template <typename T, typename Op>
+__device__ __forceinline__ T rreduce16(T v, Op op) {
+  v = op(v, dpp_t<0xB1>(v, v));
+  v = op(v, dpp_t<0x4E>(v, v));
+  v = op(v, dpp_t<0x141>(v, v));
+  v = op(v, dpp_t<0x140>(v, v));
+  return rdlane(v, 0);
+}
+// Inclusive prefix sum within each row of 16 lanes.
+template <typename T>
+__device__ __forceinline__ T rscan16(T v) {
+  const T z = (T)0;
+  v += dpp_t<0x111, 0xF, true>(z, v);
+  v += dpp_t<0x112, 0xF, true>(z, v);
+  v += dpp_t<0x114, 0xF, true>(z, v);
+  v += dpp_t<0x118, 0xF, true>(z, v);
+  return v;
+}
+
 __device__ __forceinline__ uint64_t wballot(bool p) { return __ballot(p); }
 // Set lanes of m below this lane.
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
