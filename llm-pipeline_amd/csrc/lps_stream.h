@@ -563,6 +563,21 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     if constexpr (ES == 4) hraw[q] = *reinterpret_cast<const uint32_t*>(row + o);
     else hraw[q] = *reinterpret_cast<const unsigned short*>(row + o);
   }
+  // the wave's final share: its ceil(k'/8)-th largest buffered logit (the
+  // wave has at least that many own logits at or above it, whatever its
+  // threshold was), which raises the joint threshold and so cuts the pool;
+  // computed while the other waves finish their chunks
+  if (kc > 0 && !over) {
+    const int nn = (int)min(nseg, (uint32_t)SEG);
+    uint32_t kv[SEG / 64];
+#pragma unroll
+    for (int q = 0; q < SEG / 64; q++) {
+      const int e = lane + 64 * q;
+      kv[q] = e < nn ? f2key(__uint_as_float(S.b.seg.x[wv][e])) : 0u;
+    }
+    const float share = key_threshold(wave_kth_largest<SEG / 64>(kv, (uint32_t)((kc + SNW - 1) / SNW)), greedy, T);
+    if (lane == 0) S.segjt[wv] = fmaxf(S.segjt[wv], share);
+  }
   // greedy rows: the first index of the thread's maximum, from its first tile holding it
   if (greedy && bt >= 0) {
     load_tile(b0, a0, bt);
