@@ -462,7 +462,11 @@ __device__ __forceinline__ double bin_mass(uint32_t b, unsigned long long acc) {
 // Fixed-point mass (2^44 units) of a scaled logit z against the row
 // reference R: exp2(fma(z, log2 e, -R)), a function of z alone.
 __device__ __forceinline__ uint64_t zmass_fix(float z, float R) {
-  return (uint64_t)__float2ull_rn(ldexpf(__builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, -R)), 44));
+  // (log2(e) as kLog2e + kLog2eLo: for |z| in the hundreds the rounding of
+  // kLog2e alone moves the exponent by ~3e-6)
+  constexpr float kLog2eLo = 1.925963e-08f;
+  const float t = __builtin_fmaf(z, kLog2eLo, __builtin_fmaf(z, kLog2e, -R));
+  return (uint64_t)__float2ull_rn(ldexpf(__builtin_amdgcn_exp2f(t), 44));
 }
 // bin_mass for an accumulator whose low-bit sum fits 32 bits (a chunk bin
 // holds at most NT * 80 < 2^16 masses): 2^(E - 150) (count (128 + t) 2^16 + low).

@@ -927,6 +927,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 
   int64_t token = -1;
   float cut = -INFINITY, qprob = 0.0f, chosen_z = NAN;
+  float chosen_x = NAN;  // the drawn logit (regions' draws): its mass in Z's arithmetic
   int32_t ties = -1, kept_n = 0;
   int ntop_out = 0;
   const int64_t qtok = g.qtok;
@@ -1028,6 +1029,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       const uint64_t dkey = S.sk[1][pd];
       token = (int64_t)key_index(dkey);
       chosen_z = key2f(key_z(dkey));
+      chosen_x = __uint_as_float(S.sx[1][pd]);
       // the drawn id must be kept
       if (nuc && dkey < ckey) return 12;
     }
@@ -1063,7 +1065,14 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   if ((P.chosen_logprob || g.ntop > 0) && wv == 0 && Zfull > 0.0) lnZ = log(Zfull) + (double)Rref * 0.6931471805599453;
   if (P.chosen_logprob && tid == 0) {
     float lp = NAN;
-    if (token >= 0 && Zfull > 0.0 && chosen_z == chosen_z) lp = (float)((double)chosen_z - lnZ);
+    if (token >= 0 && Zfull > 0.0 && chosen_x == chosen_x && chosen_x != INFINITY && chosen_x != -INFINITY) {
+      // the drawn logit's mass computed as Z's are (exp2(x c) against Rref):
+      // the ratio is then exact to rounding even when x c is large, where
+      // z - lnZ is not (the rounding of c moves x c by ~1e-7 of it)
+      lp = (float)((double)__builtin_fmaf(chosen_x, c, -Rref) * 0.6931471805599453 - log(Zfull));
+    } else if (token >= 0 && Zfull > 0.0 && chosen_z == chosen_z) {
+      lp = (float)((double)chosen_z - lnZ);
+    }
     P.chosen_logprob[r] = lp;
   }
   if (g.ntop > 0 && status == 0) {

@@ -149,3 +149,57 @@ def test_large_batch_nonfinite_rows(dev):
     assert st[6] == 0 and tok[6] == 30
     ok = [i for i in range(B) if i not in (3, 4, 5, 6)]
     PY.check_rows(w, out, rows=ok)
+
+
+def _peaked(B, V, dtype, seed, H=48, logprobs=False):
+    """B nucleus rows of heavy-tailed logits (Student-t(3) x 2: a few logits
+    hold almost all of the mass), with penalties over history ids; every fifth
+    row flat (N(0, 0.1^2): its kept set is most of the row)."""
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.standard_t(3, size=(B, V)).astype(np.float32) * 2.0)
+    flat = torch.arange(B) % 5 == 0
+    x[flat] = torch.randn((int(flat.sum()), V), generator=g) * 0.1
+    x = x.to(dtype)
+    T = torch.from_numpy(rng.choice([0.7, 1.0, 1.3], size=B).astype(np.float32))
+    p = torch.from_numpy(rng.choice([0.5, 0.9, 0.95, 0.99], size=B).astype(np.float32))
+    f = lambda v: torch.full((B,), v, dtype=torch.float32)
+    hist = torch.from_numpy(rng.integers(-3, V + 3, size=(B, H)).astype(np.int32))
+    hist[:, : H // 4] = hist[:, H // 4: H // 2]
+    hl = torch.from_numpy(rng.integers(0, H + 1, size=B).astype(np.int32))
+    return W.Workload("peaked", x, T, torch.zeros((B,), dtype=torch.int32), p, f(0.0), f(1.0), f(1.2), f(0.4),
+                      f(0.25), hist, hl, torch.rand((B,), generator=g), logprobs=logprobs, n_top=0)
+
+
+@pytest.mark.parametrize("hint", [0, NUC])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_large_nucleus_batch(dev, dtype, hint):
+    """Nucleus rows of a batch larger than one resident round (the row-group
+    kernel, in rounds): heavy-tailed rows whose scaled logits reach ~100, where
+    the chosen logprob must be computed in the same arithmetic as the row's
+    mass, and flat rows; every row against the oracle, with the chosen
+    logprob."""
+    B, V = 288, 8192
+    w = _peaked(B, V, dtype, seed=53 + int(dtype == torch.bfloat16), logprobs=True)
+    out = PY.run_workload(w, dev, row_kind_hint=hint)
+    rep = PY.check_rows(w, out, lp=True)
+    path = out.row_path.cpu()
+    _print(f"{dtype} hint {hint}: nucleus batch {rep}; general-kernel rows {int(path.sum())}/{B} "
+           f"{_deferral_reasons(out, dev, B)}")
+    assert (path[torch.arange(B) % 5 != 0] == 0).all()
+
+
+def test_large_nucleus_batch_mask(dev):
+    """Heavy-tailed nucleus rows of a large batch: legality bits equal -inf
+    logits bit for bit, and both match the oracle."""
+    B, V = 272, 8192
+    w = _peaked(B, V, torch.bfloat16, seed=61)
+    g = torch.Generator().manual_seed(5)
+    legal = torch.rand((B, V), generator=g) < 0.8
+    legal[:, 0] = True
+    a = PY.run_workload(w, dev, allowed=legal.to(dev))
+    wm = W.Workload(**{**w.__dict__, "logits": w.logits.masked_fill(~legal, float("-inf"))})
+    b = PY.run_workload(wm, dev)
+    assert torch.equal(a.tokens, b.tokens)
+    assert torch.equal(a.kept_count, b.kept_count)
+    PY.check_rows(wm, a)
