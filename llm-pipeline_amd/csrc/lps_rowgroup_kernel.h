@@ -662,6 +662,7 @@ __device__ __forceinline__ void scan_one(const uint64_t* m, uint64_t* c, int n, 
 struct Decision {
   int64_t token = -1;
   float cut = -INFINITY, qprob = 0.0f, chosen_z = NAN;
+  int32_t pos = -1;  // sorted position of the drawn candidate (-1: greedy)
   int32_t ties = -1, kept_n = 0;
   int ntop_out = 0;
   int status = 0;
@@ -731,6 +732,7 @@ __device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_
   const int ps = wave_first_true(0, nf, [&](int p) { return sc[p] > target; });
   d.token = key_index(sk[ps]);
   d.chosen_z = key2f(key_z(sk[ps]));
+  d.pos = ps;
   if (qtok >= 0) {
     if (tid == 0) X.mi[5] = -1;
     __syncthreads();
@@ -938,6 +940,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const int rc = topk_decide(g, V, S.sk[0], S.sm[0], S.sc[0], K, Ntot, u, gam, xmax, S, d);
     if (rc) return rc;
     token = d.token; cut = d.cut; qprob = d.qprob; chosen_z = d.chosen_z;
+    chosen_x = greedy ? xmax : (d.pos >= 0 ? __uint_as_float(S.sx[0][d.pos]) : NAN);
     ties = d.ties; kept_n = d.kept_n; ntop_out = d.ntop_out; status |= d.status;
   } else if (status == 0 && mode == MODE_GREEDY) {
     token = gam;
@@ -1063,13 +1066,14 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   // ln of sum exp(z) over the row: Z is in units of 2^Rref of exp2(x c)
   double lnZ = 0.0;
   if ((P.chosen_logprob || g.ntop > 0) && wv == 0 && Zfull > 0.0) lnZ = log(Zfull) + (double)Rref * 0.6931471805599453;
+  const double lZ = lnZ - (double)Rref * 0.6931471805599453;  // ln Zfull
   if (P.chosen_logprob && tid == 0) {
     float lp = NAN;
     if (token >= 0 && Zfull > 0.0 && chosen_x == chosen_x && chosen_x != INFINITY && chosen_x != -INFINITY) {
       // the drawn logit's mass computed as Z's are (exp2(x c) against Rref):
       // the ratio is then exact to rounding even when x c is large, where
       // z - lnZ is not (the rounding of c moves x c by ~1e-7 of it)
-      lp = (float)((double)__builtin_fmaf(chosen_x, c, -Rref) * 0.6931471805599453 - log(Zfull));
+      lp = (float)((double)__builtin_fmaf(chosen_x, c, -Rref) * 0.6931471805599453 - lZ);
     } else if (token >= 0 && Zfull > 0.0 && chosen_z == chosen_z) {
       lp = (float)((double)chosen_z - lnZ);
     }
@@ -1080,7 +1084,12 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     for (int q = tid; q < P.n_top; q += 64) {
       if (q < ntop_out) {
         const uint64_t kk = S.sk[0][q];
-        P.top_logprobs[(int64_t)r * P.n_top + q] = (float)((double)key2f(key_z(kk)) - lnZ);
+        const float xq = __uint_as_float(S.sx[0][q]);
+        // (as the chosen logprob: the logit's mass in the row mass's arithmetic)
+        P.top_logprobs[(int64_t)r * P.n_top + q] =
+            xq == xq && xq != INFINITY && xq != -INFINITY
+                ? (float)((double)__builtin_fmaf(xq, c, -Rref) * 0.6931471805599453 - lZ)
+                : (float)((double)key2f(key_z(kk)) - lnZ);
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = (int64_t)key_index(kk);
       } else {
         P.top_logprobs[(int64_t)r * P.n_top + q] = -INFINITY;

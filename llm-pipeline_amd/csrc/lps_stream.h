@@ -74,6 +74,7 @@ struct StShared : RgX {
     struct {
       uint64_t sk[KM];                  // sorted keys
       uint64_t sm[KM];                  // their fixed-point masses
+      uint32_t sx[KM];                  // their logits (bits)
     } s;
   } a;
   uint64_t sc[KM];                      // prefix of the masses (topk_decide)
@@ -91,6 +92,7 @@ struct StShared : RgX {
   float segth[SNW];                     // wave thresholds (each wave: >= k' own logits at or above)
   float segjt[SNW];                     // joint shares (each wave: >= ceil(k'/8) own logits at or above)
   int32_t pn;                           // pool count
+  uint32_t cx[POOL];                    // pool logits (bits), beside the pool keys
   RowCfg cfg;                           // the row's parameters (loaded by wave 0)
 };
 static_assert(sizeof(StShared) <= 80 * 1024, "two workgroups per CU");
@@ -704,12 +706,19 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   if (reason == 0 && kc > 0) {
 #pragma unroll
     for (int q = 0; q < PPT; q++)
-      if (pk[q]) S.b.ck[atomicAdd(&S.pn, 1)] = cand_key(__uint_as_float(px[q]), pi[q], greedy, T);
+      if (pk[q]) {
+        const int p = atomicAdd(&S.pn, 1);
+        S.b.ck[p] = cand_key(__uint_as_float(px[q]), pi[q], greedy, T);
+        S.cx[p] = px[q];
+      }
 #pragma unroll
     for (int q = 0; q < HPT_; q++)
       if (hk[q]) {
         const int p = atomicAdd(&S.pn, 1);
-        if (p < POOL) S.b.ck[p] = cand_key(__uint_as_float(hx[q]), hid[q], greedy, T);
+        if (p < POOL) {
+          S.b.ck[p] = cand_key(__uint_as_float(hx[q]), hid[q], greedy, T);
+          S.cx[p] = hx[q];
+        }
       }
     __syncthreads();
     n = S.pn;
@@ -719,12 +728,13 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     // cut the pool again: every wave's slice keeps its kc-th largest z and
     // above, so the largest slice threshold bounds the row's kc-th largest
     uint64_t kk[PPT];
-    uint32_t kz[PPT];
+    uint32_t kz[PPT], kx[PPT];
 #pragma unroll
     for (int q = 0; q < PPT; q++) {
       const int e = wv * 64 * PPT + q * 64 + lane;
       kk[q] = e < n ? S.b.ck[e] : 0ull;
       kz[q] = e < n ? key_z(kk[q]) : 0u;
+      kx[q] = e < n ? S.cx[e] : 0u;
     }
     const uint32_t sth = wave_kth_largest<PPT>(kz, (uint32_t)kc);
     const uint32_t zth = bred<SNW>(sth, S.u2, OpMax{});
@@ -740,7 +750,10 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
 #pragma unroll
     for (int q = 0; q < PPT; q++) {
       const int e = wv * 64 * PPT + q * 64 + lane;
-      if (e < n && kz[q] >= zth) S.b.ck[pos++] = kk[q];
+      if (e < n && kz[q] >= zth) {
+        S.cx[pos] = kx[q];
+        S.b.ck[pos++] = kk[q];
+      }
     }
     __syncthreads();
     n = (int)tot;
@@ -773,6 +786,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
       if (e < n) {
         S.a.s.sk[rank] = key;
         S.a.s.sm[rank] = zmass_fix(key2f(key_z(key)), Rm);
+        S.a.s.sx[rank] = S.cx[e];
       }
     }
   }
@@ -809,16 +823,25 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   if (P.skip_draw && !greedy) token = -1;
   double lnZ = 0.0;
   if (want_lp && Z > 0.0) lnZ = log(Z) + (double)R * 0.6931471805599453;
+  // logprobs from the logits' masses in the row mass's own arithmetic
+  // (exp2(x c) against R): exact to rounding also where x c is large, which
+  // z - lnZ is not (the rounding of c moves x c by ~1e-7 of it)
+  auto lprob = [&](float xv, float zv) -> float {
+    if (xv == xv && xv != INFINITY && xv != -INFINITY)
+      return (float)((double)__builtin_fmaf(xv, c, -R) * 0.6931471805599453 - (lnZ - (double)R * 0.6931471805599453));
+    return (float)((double)zv - lnZ);
+  };
   if (P.chosen_logprob && tid == 0) {
     float lp = NAN;
-    if (token >= 0 && Z > 0.0 && d.chosen_z == d.chosen_z) lp = (float)((double)d.chosen_z - lnZ);
+    const float cx = greedy ? xmax : (d.pos >= 0 ? __uint_as_float(S.a.s.sx[d.pos]) : NAN);
+    if (token >= 0 && Z > 0.0 && d.chosen_z == d.chosen_z) lp = lprob(cx, d.chosen_z);
     P.chosen_logprob[r] = lp;
   }
   if (g.ntop > 0 && status == 0) {
     for (int q = tid; q < P.n_top; q += 64) {  // n_top <= 64: wave 0
       if (q < d.ntop_out) {
         const uint64_t kk = S.a.s.sk[q];
-        P.top_logprobs[(int64_t)r * P.n_top + q] = (float)((double)key2f(key_z(kk)) - lnZ);
+        P.top_logprobs[(int64_t)r * P.n_top + q] = lprob(__uint_as_float(S.a.s.sx[q]), key2f(key_z(kk)));
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + q] = (int64_t)key_index(kk);
       } else {
         P.top_logprobs[(int64_t)r * P.n_top + q] = -INFINITY;

@@ -151,7 +151,7 @@ def test_large_batch_nonfinite_rows(dev):
     PY.check_rows(w, out, rows=ok)
 
 
-def _peaked(B, V, dtype, seed, H=48, logprobs=False):
+def _peaked(B, V, dtype, seed, H=48, logprobs=False, top_k=0):
     """B nucleus rows of heavy-tailed logits (Student-t(3) x 2: a few logits
     hold almost all of the mass), with penalties over history ids; every fifth
     row flat (N(0, 0.1^2): its kept set is most of the row)."""
@@ -167,8 +167,9 @@ def _peaked(B, V, dtype, seed, H=48, logprobs=False):
     hist = torch.from_numpy(rng.integers(-3, V + 3, size=(B, H)).astype(np.int32))
     hist[:, : H // 4] = hist[:, H // 4: H // 2]
     hl = torch.from_numpy(rng.integers(0, H + 1, size=B).astype(np.int32))
-    return W.Workload("peaked", x, T, torch.zeros((B,), dtype=torch.int32), p, f(0.0), f(1.0), f(1.2), f(0.4),
-                      f(0.25), hist, hl, torch.rand((B,), generator=g), logprobs=logprobs, n_top=0)
+    k = torch.full((B,), top_k, dtype=torch.int32)
+    return W.Workload("peaked", x, T, k, p, f(0.0), f(1.0), f(1.2), f(0.4),
+                      f(0.25), hist, hl, torch.rand((B,), generator=g), logprobs=logprobs, n_top=8 if top_k else 0)
 
 
 @pytest.mark.parametrize("hint", [0, NUC])
@@ -203,3 +204,13 @@ def test_large_nucleus_batch_mask(dev):
     assert torch.equal(a.tokens, b.tokens)
     assert torch.equal(a.kept_count, b.kept_count)
     PY.check_rows(wm, a)
+
+
+@pytest.mark.parametrize("B", [24, 288])
+def test_heavy_tailed_topk_logprobs(dev, B):
+    """Top-k rows of heavy-tailed logits with chosen and top-N logprobs: on
+    the row-group kernel (B = 24) and the streaming kernel (B = 288)."""
+    w = _peaked(B, 8192, torch.float32, seed=71, logprobs=True, top_k=20)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out, lp=True)
+    _print(f"heavy-tailed top-k B={B}: {rep}")
