@@ -35,8 +35,10 @@
 // and published sorted; a top-k list stops after its k'-th entry and the
 // entries tied with it.
 // The last workgroup of a row to finish (an arrival count) finalises it: it
-// loads the G sorted lists of each kind, merges them (the rank of an entry is
-// its position in its own list plus a binary search in each other list), and
+// loads the G sorted lists of each kind; a top-k row keeps the entries at or
+// above a bound on its k'-th largest (from the lists' m-th entries) and
+// rank-sorts them, a nucleus row merges its lists (the rank of an entry is its
+// position in its own list plus a binary search in each other list); then it
 // finds the top-k set, the top-p cut and the draw by binary searches over
 // exact fixed-point prefix masses in sorted order.  The draw is an inverse
 // CDF in sorted order: kept ids by scaled logit descending, ties lower index
@@ -79,15 +81,9 @@
       ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = __builtin_amdgcn_s_memrealtime();             \
     }                                                                                             \
   } while (0)
-// a value (not a time) in slot i
-#define RG_STAMP_VAL(i, v)                                                                       \
-  do {                                                                                            \
-    if (threadIdx.x == 0 && blockIdx.x < 8192) ::lps::rg::rg_stamps[blockIdx.x * 32 + (i)] = (uint64_t)(v); \
-  } while (0)
 #else
 #define RG_STAMP(i) ((void)0)
 #define RG_STAMP_DEP(i, v) ((void)0)
-#define RG_STAMP_VAL(i, v) ((void)0)
 #endif
 
 namespace lps {

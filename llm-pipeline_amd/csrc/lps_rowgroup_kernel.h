@@ -918,7 +918,6 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   int K = min(N1, KM);  // merged positions of list 0 present
   int Ntot = N1;
   const int nsel = (g.kprime > 0 && N2 == 0) ? select_topk_lists(S, G, g.kprime, N1, Rm) : -1;
-  RG_STAMP_VAL(23, nsel + 100000);
   if (nsel >= 0) {
     K = Ntot = nsel;
   } else {
