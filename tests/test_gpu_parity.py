@@ -193,25 +193,28 @@ def test_chi_square_one_million_draws(dev):
     assert pval > 1e-4
 
 
-def test_chi_square_draws_across_chunks(dev):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_chi_square_draws_across_chunks(dev, dtype):
     """1e6 draws of one full-vocabulary nucleus row (sampling.py:84-85 draw over
-    the top-p set of :158-185) vs the fp64 kept law.  The kept set is 64 spikes
-    spread over the whole row, so each draw crosses the row-group kernel's
-    chunks: the chunks' candidate lists, the merged regions and the draw's
-    rescan.  Every row must stay on the fast kernel (no deferral)."""
+    the top-p set of :158-185) vs the fp64 kept law, in each input dtype.  The
+    kept set is spikes spread over the whole row (values 12 + k/16, exact in
+    every dtype), so each draw crosses the row-group kernel's chunks: the
+    chunks' candidate lists, the merged regions and the draw's rescan.  Every
+    row must stay on the fast kernel (no deferral)."""
     from scipy.stats import chisquare
     from lps import SamplingParams, sample_rows
     g = torch.Generator().manual_seed(17)
     V, N = 151936, 1_000_000
     row = torch.randn((1, V), generator=g)
     spikes = torch.linspace(97, V - 101, 64).long()
-    row[0, spikes] = 12.0 + 0.04 * torch.arange(64, dtype=torch.float32)
+    row[0, spikes] = 12.0 + torch.arange(64, dtype=torch.float32) / 16
+    row = row.to(dtype)
     params = O.RowParams(temperature=1.0, top_k=0, top_p=0.9)
     r = O.sample_row(row[0], params, [], 0.5)
     kept = r.kept
-    # closed form: the 45 largest spikes hold 0.89992 of the row's mass and 46
-    # hold 0.90691, so top-p keeps the 46 largest (the first past 0.9 kept)
-    assert np.array_equal(np.nonzero(kept)[0], spikes[18:].numpy())
+    # closed form: the 34 largest spikes hold 0.89535 of the row's mass and 35
+    # hold 0.90270, so top-p keeps the 35 largest (the first past 0.9 kept)
+    assert np.array_equal(np.nonzero(kept)[0], spikes[29:].numpy())
     x = row.to(dev).expand(N, V)                          # stride 0 over rows
     p = SamplingParams.build(N, dev, temperature=1.0, top_p=0.9)
     u = torch.rand(N, device=dev, generator=torch.Generator(device=dev).manual_seed(5))
@@ -221,7 +224,7 @@ def test_chi_square_draws_across_chunks(dev):
     counts = torch.bincount(out.tokens, minlength=V).cpu().numpy()
     assert counts[~kept].sum() == 0
     stat, pval = chisquare(counts[kept], r.probs64[kept] * N)
-    _print(f"chi-square 1e6 draws, V={V}: kept={int(kept.sum())} stat={stat:.1f} p={pval:.3g}")
+    _print(f"chi-square 1e6 draws, V={V} {dtype}: kept={int(kept.sum())} stat={stat:.1f} p={pval:.3g}")
     assert pval > 1e-4
 
 
