@@ -216,12 +216,14 @@ def test_heavy_tailed_topk_logprobs(dev, B):
     _print(f"heavy-tailed top-k B={B}: {rep}")
 
 
-def test_chi_square_draws_streaming_kernel(dev):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_chi_square_draws_streaming_kernel(dev, dtype):
     """1e6 draws of one full-vocabulary top-k row (top_k 40, then top-p 0.9 on
     the top-k set: sampling.py:139-185, draw :84-85) on the streaming kernel
     alone (the top-k hint launches no row-group kernel, and no row may fall to
-    the general kernel), against the fp64 kept law.  The kept set is 32 of 64
-    spikes spread over the row, so the candidates come from every wave."""
+    the general kernel), against the fp64 kept law, in each input dtype.  The
+    kept set is 28 of 64 spikes spread over the row (values 12 + k/16, exact in
+    every dtype), so the candidates come from every wave."""
     from scipy.stats import chisquare
     from lps import SamplingParams, sample_rows
     from oracle import reference_semantics as O
@@ -229,12 +231,13 @@ def test_chi_square_draws_streaming_kernel(dev):
     V, N = 151936, 1_000_000
     row = torch.randn((1, V), generator=g)
     spikes = torch.linspace(53, V - 71, 64).long()
-    row[0, spikes] = 12.0 + 0.04 * torch.arange(64, dtype=torch.float32)
+    row[0, spikes] = 12.0 + torch.arange(64, dtype=torch.float32) / 16
+    row = row.to(dtype)
     r = O.sample_row(row[0], O.RowParams(temperature=1.0, top_k=40, top_p=0.9), [], 0.5)
     kept = r.kept
-    # closed form: within the 40 largest spikes, the 31 largest hold 0.89038 of
-    # their mass and 32 hold 0.90460, so top-p keeps the 32 largest
-    assert np.array_equal(np.nonzero(kept)[0], spikes[32:].numpy())
+    # closed form: within the 40 largest spikes, the 27 largest hold 0.88790 of
+    # their mass and 28 hold 0.90011, so top-p keeps the 28 largest
+    assert np.array_equal(np.nonzero(kept)[0], spikes[36:].numpy())
     x = row.to(dev).expand(N, V)                          # stride 0 over rows
     p = SamplingParams.build(N, dev, temperature=1.0, top_k=40, top_p=0.9)
     u = torch.rand(N, device=dev, generator=torch.Generator(device=dev).manual_seed(7))
@@ -244,5 +247,5 @@ def test_chi_square_draws_streaming_kernel(dev):
     counts = torch.bincount(out.tokens, minlength=V).cpu().numpy()
     assert counts[~kept].sum() == 0
     stat, pval = chisquare(counts[kept], r.probs64[kept] * N)
-    _print(f"chi-square 1e6 draws, streaming kernel, V={V}: kept={int(kept.sum())} stat={stat:.1f} p={pval:.3g}")
+    _print(f"chi-square 1e6 draws, streaming kernel, V={V} {dtype}: kept={int(kept.sum())} stat={stat:.1f} p={pval:.3g}")
     assert pval > 1e-4
