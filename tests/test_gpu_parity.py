@@ -419,3 +419,46 @@ def test_query_token_outside_vocab_has_zero_probability(dev):
     assert (a.query_prob.cpu() == 0).all()
     assert torch.equal(a.tokens, ok.tokens)
     assert (a.status.cpu() == 0).all()
+
+
+@pytest.mark.parametrize("residual", ["target", "leviathan"])
+def test_spec_verify_first_token_law(dev, residual):
+    """The law of the first emitted token of one-draft speculative verification
+    (speculative.py:119-174: accept the draft d ~ q with probability
+    min(1, p(d) / q(d)), else resample), 1e6 requests, chi-square against its
+    closed form: with the reference's resample from the target p
+    (speculative.py:150-157) it is min(p, q) + (1 - sum min(p, q)) p; with the
+    residual norm(max(p - q, 0)) it is p itself (the speculative sampling
+    theorem)."""
+    from scipy.stats import chisquare
+    from lps import spec_verify
+    g = torch.Generator().manual_seed(23)
+    V, N = 4000, 1_000_000
+    tgt = torch.randn((1, 2, V), generator=g) * 2.0
+    drf = tgt[:, :1, :] + torch.randn((1, 1, V), generator=g) * 1.0
+    p = torch.softmax(tgt[0, 0].double(), 0).numpy()
+    q = torch.softmax(drf[0, 0].double(), 0).numpy()
+    rng = np.random.default_rng(29)
+    draft_tokens = torch.from_numpy(rng.choice(V, size=(N, 1), p=q))
+    ua = torch.from_numpy(rng.random((N, 1), dtype=np.float32))
+    ur = torch.from_numpy(rng.random((N, 2), dtype=np.float32))
+    out = spec_verify(tgt.to(dev).expand(N, 2, V), drf.to(dev).expand(N, 1, V), draft_tokens.to(dev),
+                      ua.to(dev), ur.to(dev), 1.0, 1.0, residual=residual)
+    torch.cuda.synchronize()
+    assert int(out.status.ne(0).sum().item()) == 0
+    first = out.tokens[:, 0].cpu().numpy()
+    m = np.minimum(p, q)
+    law = p if residual == "leviathan" else m + (1.0 - m.sum()) * p
+    counts = np.bincount(first, minlength=V).astype(np.float64)
+    exp = law * N
+    big = exp >= 20.0                                  # pooled tail below 20 expected draws
+    f_obs = np.append(counts[big], counts[~big].sum())
+    f_exp = np.append(exp[big], exp[~big].sum())
+    stat, pval = chisquare(f_obs, f_exp)
+    # the other residual's law is rejected (the test tells the two rules apart)
+    other = m + (1.0 - m.sum()) * p if residual == "leviathan" else p
+    o_exp = np.append(other[big] * N, other[~big].sum() * N)
+    _, p_other = chisquare(f_obs, o_exp * (f_obs.sum() / o_exp.sum()))
+    _print(f"spec verify first-token law ({residual}): bins={int(big.sum())}+1 stat={stat:.1f} p={pval:.3g}; "
+           f"other law p={p_other:.3g}")
+    assert pval > 1e-4 and p_other < 1e-6
