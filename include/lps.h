@@ -4,10 +4,11 @@
  * Plain C: pointers, sizes and enums only, no torch or HIP types.  The stream
  * argument is a hipStream_t passed as void* (NULL = the null stream).  Every
  * pointer in an args struct is a device pointer unless stated otherwise.  All
- * entry points are stream-ordered and never synchronise.  All but
- * lps_sample_noalloc keep no global mutable state and are safe to call from
- * several host threads at once; lps_sample_noalloc shares one workspace per
- * GPU between its calls (see its declaration).
+ * entry points are stream-ordered and never synchronise.  All are safe to
+ * call from several host threads at once: the library's only process-wide
+ * state is per-device and written once (the device's CU count, and the
+ * address of lps_sample_noalloc's workspace); lps_sample_noalloc shares that
+ * one workspace per GPU between its calls (see its declaration).
  *
  * The entry points replace the logits->token path of DavidAkinpelu/llm-pipeline:
  *
@@ -34,7 +35,12 @@
 extern "C" {
 #endif
 
-#define LPS_ABI_VERSION 1
+/* Version 2: the draw is an inverse CDF over the kept ids in sorted order
+ * (scaled logit descending, ties lower index first); version 1 drew in
+ * vocabulary order, so the same uniforms gave other tokens.  Histories of any
+ * length and any number of distinct ids (LPS_ROW_HISTORY_OVERFLOW is no
+ * longer set). */
+#define LPS_ABI_VERSION 2
 
 /* Return codes.  The reference raises TypeError / ValueError / RuntimeError
  * (sampling.py:106, speculative.py:90-91, torch.multinomial); the Python
@@ -59,12 +65,11 @@ enum {
   LPS_ROW_OK = 0,
   LPS_ROW_NONFINITE = 1,       /* NaN or +inf in the scaled logits of a sampling row */
   LPS_ROW_EMPTY = 2,           /* every logit is -inf on a sampling row               */
-  LPS_ROW_HISTORY_OVERFLOW = 4 /* more distinct history ids than the kernel holds     */
+  LPS_ROW_HISTORY_OVERFLOW = 4 /* never set since ABI version 2 (kept for callers that test it) */
 };
 
-/* Largest top-N logprob count and largest distinct-history size per row. */
+/* Largest top-N logprob count per row. */
 #define LPS_MAX_TOP_LOGPROBS 64
-#define LPS_MAX_HISTORY_DISTINCT 1536
 
 /* lps_sample_args.flags */
 enum {
@@ -122,7 +127,8 @@ typedef struct lps_sample_args {
 
   /* per-row token histories: int32 [R, history_stride], row r holds
    * history_len[r] ids; ids outside [0, V) are ignored (sampling.py:126).
-   * history == NULL: no penalties. */
+   * Any length, any number of distinct ids.  history_stride 0: every row
+   * reads the same history.  history == NULL: no penalties. */
   const int32_t* history;
   int64_t history_stride;
   const int32_t* history_len;

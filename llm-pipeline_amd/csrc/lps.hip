@@ -1,8 +1,11 @@
 // C ABI of the lps token sampler (declarations and reference citations are in
-// include/lps.h).  Launches only; no allocation, no synchronisation, no global
-// mutable state.
+// include/lps.h).  Launches only; no allocation, no synchronisation.  The only
+// process-wide state is per-device and write-once: the CU count of each device
+// (atomic entries) and the no-allocation entry point's workspace address
+// (std::call_once per device).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "lps_rowgroup.h"
@@ -48,9 +51,10 @@ bool dtype_ok(int d) { return d == LPS_DTYPE_F32 || d == LPS_DTYPE_BF16 || d == 
 size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
 // Row-group workspace: per-row counters (a fixed region at offset 0, so a
-// workspace reused for any (rows, vocab) keeps them apart from the data; they
-// are zero between launches: every launch leaves them zero), row status, chunk
-// summaries, histogram exchange and candidates.
+// workspace reused for any (rows, vocab) keeps them apart from the data: the
+// arrival and barrier counts are zero between launches, every launch leaves
+// them zero; the row's launch epoch only grows), row status, chunk summaries,
+// histogram exchange and candidates.
 struct RgWs {
   uint32_t* counters;
   int32_t* status;
@@ -114,15 +118,18 @@ RgWs rg_layout(void* base, int R, int V) {
 
 // CUs of the current device (cached per device): one resident round of
 // row-group workgroups.
+// (threads that race on a device's first call each store the same value)
+std::atomic<int> g_cus[64];
 int device_cus() {
-  static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
+  int c = g_cus[dev].load(std::memory_order_relaxed);
+  if (!c) {
     int n = 0;
-    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+    c = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+    g_cus[dev].store(c, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return c;
 }
 
 template <int DT, int VPE, int NE>

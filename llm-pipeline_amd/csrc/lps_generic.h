@@ -7,6 +7,12 @@
 // (11 + 11 + 10 bits), masses are fixed-point so every decision is
 // deterministic and independent of accumulation order.
 //
+// History counts (penalties) are held for one window of GEN_WIN ids at a
+// time: each pass walks the row window by window, and a window's counts are
+// rebuilt from the row's whole history when the pass enters it.  A history of
+// any length, with any number of distinct ids, is therefore counted exactly
+// (counts are 32-bit).
+//
 // Semantics follow Sampler.sample_token (src/llm_pipeline/inference/
 // sampling.py:51-85): penalties (:108-137 plus presence/frequency), greedy
 // argmax for T <= 0 (:72-75), x / T, top-k with all ties at the k-th value kept
@@ -23,8 +29,8 @@ namespace lps {
 
 constexpr int GEN_NT = 1024;            // threads of the general kernel (the code runs with any multiple of 64 up to it)
 constexpr int GEN_NW = GEN_NT / 64;     // scratch sized for the largest block
-constexpr int HASH_CAP = 2048;     // history hash slots (power of two)
-constexpr int BLOOM_WORDS = 2048;  // 65536-bit bloom filter over token ids
+constexpr int GEN_WIN = 8192;           // ids per history-count window: a multiple of every pass's tile
+                                        // (threads x vector: at most 1024 x 8)
 constexpr int NBINS = 2048;        // radix digit bins (11 bits)
 constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // f2key(-inf)
 
@@ -92,9 +98,7 @@ __device__ __forceinline__ bool id_allowed(const uint8_t* am, int64_t i) {
 constexpr int32_t LPS_ROW_DEFERRED = 8;
 
 struct GenShared {
-  uint32_t bloom[BLOOM_WORDS];
-  int32_t hkey[HASH_CAP];
-  int32_t hcnt[HASH_CAP];
+  alignas(16) uint32_t wcnt[GEN_WIN];  // history counts of the ids [w0, w0 + GEN_WIN) of the loaded window
   union {
     struct {
       uint32_t cnt[NBINS];
@@ -113,28 +117,22 @@ struct GenShared {
   uint64_t misc64[4];
 };
 
-__device__ __forceinline__ uint32_t hash_id(int id) { return ((uint32_t)id * 2654435761u) >> (32 - 11); }
-
+// The row's legality bits and penalties.  The history counts are those of one
+// window of ids (pen_window loads it); apply() takes logits of that window.
 struct PenCtx {
-  bool active;
+  bool active;          // penalties apply (a non-empty history and a non-neutral penalty)
   float rep, pres, freq;
-  const uint32_t* bloom;
-  const int32_t* hkey;
-  const int32_t* hcnt;
-  const uint8_t* am;  // the row's legality bits, or nullptr
+  const uint32_t* wcnt; // counts of the loaded window's ids
+  int64_t w0;           // first id of the window the pass is in
+  int64_t loaded;       // first id of the window whose counts wcnt holds (-1: none)
+  const int32_t* hist;  // the row's history ids (any value; ids outside [0, V) count for nothing)
+  int hlen;
+  int V;
+  const uint8_t* am;    // the row's legality bits, or nullptr
 
-  __device__ __forceinline__ int lookup(int id) const {
-    uint32_t s = hash_id(id);
-    for (int p = 0; p < HASH_CAP; p++) {
-      int k = hkey[s];
-      if (k == id) return hcnt[s];
-      if (k < 0) return 0;
-      s = (s + 1) & (HASH_CAP - 1);
-    }
-    return 0;
-  }
   // Illegal ids to -inf, then the penalties, on the VEC logits of ids
-  // [i0, i0 + VEC) (i0 a multiple of VEC, VEC in {1, 4, 8}).
+  // [i0, i0 + VEC) (i0 a multiple of VEC inside the current window, VEC in
+  // {1, 4, 8}).
   template <int VEC>
   __device__ __forceinline__ void apply(int64_t i0, float (&x)[VEC]) const {
     if (am) {
@@ -144,18 +142,49 @@ struct PenCtx {
         if (!((b >> j) & 1u)) x[j] = -INFINITY;
     }
     if (!active) return;
-    uint32_t w = bloom[(i0 >> 5) & (BLOOM_WORDS - 1)] >> (i0 & 31);
-    if (VEC < 32) w &= (1u << VEC) - 1u;
-    if (!w) return;
+    const uint32_t* c = wcnt + (i0 - w0);
+    uint32_t cw[VEC];
+    if constexpr (VEC % 4 == 0) {
 #pragma unroll
-    for (int j = 0; j < VEC; j++) {
-      if ((w >> j) & 1u) {
-        int c = lookup((int)(i0 + j));
-        if (c) x[j] = penalize(x[j], c, rep, pres, freq);
+      for (int q = 0; q < VEC / 4; q++) {
+        const uint4 a = reinterpret_cast<const uint4*>(c)[q];
+        cw[4 * q] = a.x; cw[4 * q + 1] = a.y; cw[4 * q + 2] = a.z; cw[4 * q + 3] = a.w;
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; j++) cw[j] = c[j];
     }
+    uint32_t any = 0;
+#pragma unroll
+    for (int j = 0; j < VEC; j++) any |= cw[j];
+    if (!any) return;
+#pragma unroll
+    for (int j = 0; j < VEC; j++)
+      if (cw[j]) x[j] = penalize(x[j], (int)cw[j], rep, pres, freq);
   }
 };
+
+// Ids per window of a pass: GEN_WIN with penalties, else the whole row.
+__device__ __forceinline__ int64_t win_size(const PenCtx& pc) { return pc.active ? (int64_t)GEN_WIN : (int64_t)pc.V; }
+
+// Enters the window starting at id w0: its history counts are counted from the
+// row's whole history unless they are loaded already.  Every thread calls it
+// (block-uniform arguments); it ends with a barrier when it loads.
+__device__ __forceinline__ void pen_window(PenCtx& pc, uint32_t* wcnt, int64_t w0) {
+  pc.w0 = w0;
+  if (!pc.active || pc.loaded == w0) return;
+  __syncthreads();  // every reader of the previous window is done with it
+  uint4* c4 = reinterpret_cast<uint4*>(wcnt);
+  for (int i = threadIdx.x; i < GEN_WIN / 4; i += (int)blockDim.x) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  const int64_t w1 = w0 + GEN_WIN < (int64_t)pc.V ? w0 + GEN_WIN : (int64_t)pc.V;
+  for (int j = threadIdx.x; j < pc.hlen; j += (int)blockDim.x) {
+    const int64_t id = pc.hist[j];
+    if (id >= w0 && id < w1) atomicAdd(&wcnt[id - w0], 1u);
+  }
+  __syncthreads();
+  pc.loaded = w0;
+}
 
 // ---------------------------------------------------------------------------
 // Block helpers (blockDim.x threads, a multiple of 64, at most GEN_NT).
@@ -226,14 +255,20 @@ __device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch) {
 // ---------------------------------------------------------------------------
 // Row passes.
 // ---------------------------------------------------------------------------
+// One pass over the row, window by window (every thread calls it).
 template <int DT, int VEC, typename F>
-__device__ __forceinline__ void row_pass(const void* row, int V, const PenCtx& pc, F&& f) {
-  for (int64_t i0 = (int64_t)threadIdx.x * VEC; i0 < V; i0 += (int64_t)(int)blockDim.x * VEC) {
-    float x[VEC];
-    loadv<DT, VEC>(row, i0, x);
-    pc.apply<VEC>(i0, x);
+__device__ __forceinline__ void row_pass(const void* row, int V, PenCtx& pc, GenShared& S, F&& f) {
+  const int64_t W = win_size(pc);
+  for (int64_t w0 = 0; w0 < V; w0 += W) {
+    pen_window(pc, S.wcnt, w0);
+    const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
+    for (int64_t i0 = w0 + (int64_t)threadIdx.x * VEC; i0 < w1; i0 += (int64_t)(int)blockDim.x * VEC) {
+      float x[VEC];
+      loadv<DT, VEC>(row, i0, x);
+      pc.apply<VEC>(i0, x);
 #pragma unroll
-    for (int j = 0; j < VEC; j++) f((int)(i0 + j), x[j]);
+      for (int j = 0; j < VEC; j++) f((int)(i0 + j), x[j]);
+    }
   }
 }
 
@@ -281,7 +316,7 @@ __device__ void clear_hist(GenShared& S) {
 // kk-th largest key (1-based, counting multiplicity) of keyf over the row.
 // Returns the key; *n_above = number of elements with a strictly larger key.
 template <int DT, int VEC, typename KF>
-__device__ __forceinline__ uint32_t select_kth(const void* row, int V, const PenCtx& pc, GenShared& S, uint32_t kk, KF keyf,
+__device__ __forceinline__ uint32_t select_kth(const void* row, int V, PenCtx& pc, GenShared& S, uint32_t kk, KF keyf,
                                uint32_t* n_above) {
   uint32_t prefix = 0;
   uint32_t above = 0;
@@ -289,7 +324,7 @@ __device__ __forceinline__ uint32_t select_kth(const void* row, int V, const Pen
     const int sh = lvl_shift(l), nb = lvl_bins(l);
     const uint32_t hm = lvl_himask(l);
     clear_hist<DT, VEC>(S);
-    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+    row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
       uint32_t k = keyf(x);
       if ((k & hm) == prefix) atomicAdd(&S.u.h.cnt[(k >> sh) & (nb - 1)], 1u);
     });
@@ -316,7 +351,7 @@ struct MassCut {
 
 // Largest key v with mass(active, key >= v) > limit (limit < total active mass).
 template <int DT, int VEC, typename KF, typename AF>
-__device__ __forceinline__ MassCut select_mass(const void* row, int V, const PenCtx& pc, GenShared& S, uint64_t limit, KF keyf,
+__device__ __forceinline__ MassCut select_mass(const void* row, int V, PenCtx& pc, GenShared& S, uint64_t limit, KF keyf,
                                AF massf) {
   uint32_t prefix = 0;
   uint64_t A = 0;
@@ -325,7 +360,7 @@ __device__ __forceinline__ MassCut select_mass(const void* row, int V, const Pen
     const int sh = lvl_shift(l), nb = lvl_bins(l);
     const uint32_t hm = lvl_himask(l);
     clear_hist<DT, VEC>(S);
-    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+    row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
       uint32_t k;
       uint64_t m;
       if (massf(x, &k, &m) && (k & hm) == prefix) {
@@ -377,39 +412,17 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   const bool want_H = P.entropy != nullptr;
   int status = 0;
 
-  // ---- history table (counts of distinct in-range ids) ----
+  // ---- history: its counts are loaded one window of ids at a time by the passes ----
   int hlen = (P.history && P.history_len) ? P.history_len[r] : 0;
   if (P.history_stride > 0 && hlen > P.history_stride) hlen = (int)P.history_stride;  // never past the row
+  if (hlen < 0) hlen = 0;
   const bool pen = hlen > 0 && (rep != 1.0f || pres != 0.0f || freq != 0.0f);
-  for (int i = tid; i < BLOOM_WORDS; i += (int)blockDim.x) S.bloom[i] = 0u;
-  for (int i = tid; i < HASH_CAP; i += (int)blockDim.x) { S.hkey[i] = -1; S.hcnt[i] = 0; }
-  __syncthreads();
-  if (pen) {
-    const int32_t* h = P.history + (int64_t)r * P.history_stride;
-    for (int j = tid; j < hlen; j += (int)blockDim.x) {
-      const int id = h[j];
-      if (id < 0 || id >= V) continue;
-      uint32_t s = hash_id(id);
-      for (int p = 0; p < HASH_CAP; p++) {
-        int old = atomicCAS(&S.hkey[s], -1, id);
-        if (old == -1 || old == id) { atomicAdd(&S.hcnt[s], 1); break; }
-        s = (s + 1) & (HASH_CAP - 1);
-      }
-      atomicOr(&S.bloom[(id >> 5) & (BLOOM_WORDS - 1)], 1u << (id & 31));
-    }
-  }
-  __syncthreads();
-  {
-    uint32_t used = 0;
-    for (int i = tid; i < HASH_CAP; i += (int)blockDim.x) used += S.hkey[i] >= 0 ? 1u : 0u;
-    used = gblock_sum_u32(used, S);
-    if (used > LPS_MAX_HISTORY_DISTINCT) status |= LPS_ROW_HISTORY_OVERFLOW;
-  }
-  PenCtx pc{pen, rep, pres, freq, S.bloom, S.hkey, S.hcnt, row_allowed(P, r)};
+  PenCtx pc{pen, rep, pres, freq, S.wcnt, 0, -1, pen ? P.history + (int64_t)r * P.history_stride : nullptr,
+            hlen, V, row_allowed(P, r)};
 
   // ---- pass 1: max and first argmax of the penalised logits ----
   uint64_t best = 0;
-  row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+  row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
     const uint64_t pk = ((uint64_t)f2key(x) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
     best = pk > best ? pk : best;
   });
@@ -431,19 +444,18 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   } else {
     token = argmax;
   }
-  if (status & LPS_ROW_HISTORY_OVERFLOW) token = -1;
 
   // ---- full-row statistics: Z over all tokens, sum of e * (z - zmax) ----
   const bool stats_ok = !has_nan && Mx != INFINITY && Mx != -INFINITY && zmax != INFINITY;
   uint64_t Zfull = 0;
   double Sed = 0.0;
-  const bool need_full = stats_ok && !(status & LPS_ROW_HISTORY_OVERFLOW) &&
+  const bool need_full = stats_ok &&
                          (want_lp || want_H || (!greedy && status == 0 && topk <= 0 && topp < 1.0f) ||
                           (!greedy && typp < 1.0f));
   if (need_full) {
     uint64_t zs = 0;
     double sd = 0.0;
-    row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+    row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
       const float z = zval(x);
       const float e = mass_f(z, zmax);
       zs += mass_fixed(e);
@@ -482,7 +494,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         Zk = Zfull;
       } else {
         uint64_t zs = 0;
-        row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+        row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
           const float z = zval(x);
           if (f2key(z) >= thk) zs += mass_fixed(mass_f(z, zmax));
         });
@@ -506,7 +518,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     // min-p: keep e >= min_p (the max has e == 1)
     if (minp > 0.0f) {
       uint32_t mk = 0xFFFFFFFFu;
-      row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+      row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
         const float z = zval(x);
         const uint32_t k = f2key(z);
         if (k >= key_lo && mass_f(z, zmax) >= minp) mk = k < mk ? k : mk;
@@ -519,7 +531,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     if (status == 0 && typp < 1.0f) {
       uint32_t ngt = 0, neq = 0, ninf = 0;
       const uint32_t kinf = f2key(-INFINITY);
-      row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+      row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
         const uint32_t k = zkey(x);
         ngt += k > key_lo ? 1u : 0u;
         neq += k == key_lo ? 1u : 0u;
@@ -539,7 +551,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         const float tau = __fmul_rn((float)exp(H), typp);
         const double dmin = lnZ - (double)tau;
         uint32_t mk = 0xFFFFFFFFu;
-        row_pass<DT, VEC>(row, V, pc, [&](int i, float x) {
+        row_pass<DT, VEC>(row, V, pc, S, [&](int i, float x) {
           const float z = zval(x);
           if ((double)__fsub_rn(z, zmax) >= dmin) { const uint32_t k = f2key(z); mk = k < mk ? k : mk; }
         });
@@ -558,12 +570,17 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     uint32_t tie_run = 0, nkept = 0;
     uint64_t qm = 0;
     int qk = 0;
-    for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
+    // (windows of ids, tiles in vocabulary order within each: tie ranks run in vocabulary order)
+    const int64_t W = win_size(pc);
+    for (int64_t w0 = 0; w0 < V; w0 += W) {
+    pen_window(pc, S.wcnt, w0);
+    const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
+    for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       float x[VEC];
       uint32_t k[VEC];
       uint32_t nt_loc = 0;
-      if (i0 < V) {
+      if (i0 < w1) {
         loadv<DT, VEC>(row, i0, x);
         pc.apply<VEC>(i0, x);
 #pragma unroll
@@ -571,7 +588,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       }
       uint32_t tot = 0, ex = 0;
       if (n_tie != kNoTie) ex = gblock_excl_scan<uint32_t>(nt_loc, &tot, S.red32);
-      if (i0 < V) {
+      if (i0 < w1) {
         uint32_t rk = tie_run + ex;
 #pragma unroll
         for (int j = 0; j < VEC; j++) {
@@ -586,6 +603,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         }
       }
       tie_run += tot;
+    }
     }
     Zf = gblock_sum_u64(acc, S);
     kept_n = gblock_sum_u32(nkept, S);
@@ -619,11 +637,16 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     uint32_t run = 0;
     if (tid == 0) S.misc[1] = -1;
     __syncthreads();
-    for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
+    const int64_t W = win_size(pc);
+    bool done = false;
+    for (int64_t w0 = 0; w0 < V && !done; w0 += W) {
+    pen_window(pc, S.wcnt, w0);
+    const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
+    for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       uint32_t k[VEC];
       uint32_t nt_loc = 0;
-      if (i0 < V) {
+      if (i0 < w1) {
         float x[VEC];
         loadv<DT, VEC>(row, i0, x);
         pc.apply<VEC>(i0, x);
@@ -632,7 +655,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       }
       uint32_t ttot;
       const uint32_t tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
-      if (i0 < V && run + tex <= jt && jt < run + tex + nt_loc) {
+      if (i0 < w1 && run + tex <= jt && jt < run + tex + nt_loc) {
         uint32_t rk = run + tex;
 #pragma unroll
         for (int j = 0; j < VEC; j++) {
@@ -645,8 +668,9 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       __syncthreads();
       const int found = S.misc[1];
       __syncthreads();
-      if (found >= 0) { token = found; break; }
+      if (found >= 0) { token = found; done = true; break; }
       run += ttot;
+    }
     }
   } else if (!greedy) {
     token = -1;
@@ -654,14 +678,22 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
 
   // ---- logprobs: chosen id and top-N of log_softmax(penalised z) ----
   if (want_lp) {
-    if (P.chosen_logprob && tid == 0) {
-      float lp = NAN;
-      if (token >= 0 && need_full) {
-        float xa[1] = {load1<DT>(row, token)};
-        pc.apply<1>(token, xa);
-        lp = (float)((double)__fsub_rn(zval(xa[0]), zmax) - lnZ);
+    if (P.chosen_logprob) {
+      // the drawn id's history count (the whole block counts it)
+      uint32_t tc = 0;
+      if (pen && token >= 0)
+        for (int j = tid; j < hlen; j += (int)blockDim.x) tc += pc.hist[j] == token ? 1u : 0u;
+      tc = gblock_sum_u32(tc, S);
+      if (tid == 0) {
+        float lp = NAN;
+        if (token >= 0 && need_full) {
+          float xv = load1<DT>(row, token);
+          if (!id_allowed(pc.am, token)) xv = -INFINITY;
+          if (tc) xv = penalize(xv, (int)tc, rep, pres, freq);
+          lp = (float)((double)__fsub_rn(zval(xv), zmax) - lnZ);
+        }
+        P.chosen_logprob[r] = lp;
       }
-      P.chosen_logprob[r] = lp;
     }
     if (P.n_top > 0 && P.top_logprobs) {
       const int N = P.n_top < V ? P.n_top : V;
@@ -671,19 +703,23 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       if (tid == 0) S.u.lst.n = 0;
       __syncthreads();
       uint32_t tie_run = 0;
-      for (int64_t tile = 0; tile < V; tile += (int64_t)(int)blockDim.x * VEC) {
+      const int64_t W = win_size(pc);
+      for (int64_t w0 = 0; w0 < V; w0 += W) {
+      pen_window(pc, S.wcnt, w0);
+      const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
+      for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
         const int64_t i0 = tile + (int64_t)tid * VEC;
         float x[VEC];
         uint32_t k[VEC];
         uint32_t nt_loc = 0;
-        if (i0 < V) {
+        if (i0 < w1) {
           loadv<DT, VEC>(row, i0, x);
           pc.apply<VEC>(i0, x);
 #pragma unroll
           for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == thn ? 1u : 0u; }
         }
         uint32_t ttot, tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
-        if (i0 < V) {
+        if (i0 < w1) {
           uint32_t rk = tie_run + tex;
 #pragma unroll
           for (int j = 0; j < VEC; j++) {
@@ -696,6 +732,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
           }
         }
         tie_run += ttot;
+      }
       }
       __syncthreads();
       const int n = S.u.lst.n < N ? S.u.lst.n : N;
@@ -721,7 +758,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   }
 
   if (tid == 0) {
-    const bool failed = (status & LPS_ROW_HISTORY_OVERFLOW) || (!greedy && status != 0);
+    const bool failed = !greedy && status != 0;
     P.tokens[r] = failed ? -1 : token;
     append_token(P, r, failed ? -1 : token);
     if (P.row_status) P.row_status[r] = status;

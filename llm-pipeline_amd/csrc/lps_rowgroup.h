@@ -10,8 +10,9 @@
 // chunks of 40960 logits) is 256 workgroups: one resident wave on 256 CUs.
 //
 // Per chunk workgroup, by row mode (row_cfg):
-//   all      penalties from an 8-bit count table of the chunk's history ids
-//            (LDS), legality bits, thread max, workgroup max.
+//   all      penalties from a 16-bit count table of the chunk's history ids
+//            (LDS; any number of distinct ids, a count of 65535 or more
+//            defers the row), legality bits, thread max, workgroup max.
 //   GREEDY   first argmax; with logprobs the chunk mass and top-N candidates.
 //   TOPK     a threshold below the chunk's k'-th largest logit (from the
 //            wave-level k'/8-th largest thread maxima), lowered to the start
@@ -124,19 +125,20 @@ enum { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_PURE = 2, MODE_NUCLEUS = 3, MODE_DEF
 // Chunk flags (RgSum.flags); any of them defers the row.
 enum {
   RF_OVERFLOW = 1,    // more candidates than the lists take
-  RF_HISTORY = 2,     // a history count does not fit 8 bits
-  RF_SPLIT = 4,       // the row's workgroups ran on more than one XCD
+  RF_HISTORY = 2,     // a history count does not fit 16 bits
+  RF_SPLIT = 4,       // a chunk summary is not this launch's, or its chunk ran on another XCD
   RF_REGION = 8,      // no usable cut / draw region, or the barrier timed out
 };
 
 // Per-chunk summary (published for the finaliser).
 struct RgSum {
+  uint64_t tag;       // rg_tag(epoch, row, XCD): which launch, row and XCD wrote it (one 8-byte word,
+                      // read by one load: a current tag vouches for the XCD it names)
   uint32_t mkey;      // max key of the penalised logits (0xFFFFFFFF: NaN present)
   int32_t amax;       // first index of that key (greedy rows)
   float ref;          // mass reference (an integer, log2 units; -inf: no finite logit)
   uint16_t n1, n2;    // published entries of list 1 (top-k / region 1) and list 2 (region 2)
   uint32_t flags;     // RF_*
-  uint32_t xcc;       // XCD that ran the chunk
   uint32_t nab1;      // nucleus: elements above region 1
   uint32_t nanbin;    // nucleus: NaN / +inf masses seen
   double zsum;        // chunk mass: sum of exp2(fma(x, c, -ref))
@@ -144,7 +146,19 @@ struct RgSum {
   double ab2;         // nucleus: exact mass above region 2
   int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row bins; the same in every chunk)
 };
+static_assert(sizeof(RgSum) % 8 == 0 && offsetof(RgSum, tag) == 0, "8-byte words, the tag first");
 __device__ __forceinline__ void store_sum(RgSum* d, const RgSum& a) { *d = a; }
+// Summary tag: the row's launch epoch (a per-row count in the workspace that
+// each launch's finaliser advances, so a record left by an earlier launch
+// carries an older one; zero-filled memory never matches, the epochs start at
+// 1), the row (records of another row or workspace layout never match) and
+// the XCD that ran the chunk.
+__device__ __forceinline__ uint64_t rg_tag(uint32_t epoch, int r, uint32_t xcc) {
+  return ((uint64_t)(epoch + 1u) << 32) | ((uint64_t)(uint32_t)r << 8) | (uint64_t)(xcc & 0xFFu);
+}
+constexpr int CTR_ARRIVE = 0;  // counter words of a row (32 per row): arrivals,
+constexpr int CTR_HIST = 2;    // the histogram barrier,
+constexpr int CTR_EPOCH = 4;   // and the row's launch epoch (never reset)
 
 struct RgParams {
   KParams k;
@@ -156,7 +170,8 @@ struct RgParams {
   int heavy_first;     // dispatch rows without top-k first
   int skip_topk;       // the streaming kernel's rows (stream_takes) ran there: skip them
   int stream_only;     // the row-group kernel is not launched: the streaming kernel defers the others
-  uint32_t* counters;  // [R * 32]: [0] arrivals, [2] histogram barrier; zero between launches
+  uint32_t* counters;  // [R * 32]: arrivals and the histogram barrier (zero between launches), the
+                       // row's launch epoch (CTR_*)
   int32_t* status;     // [R]
   RgSum* sums;         // row r at sums + r * 2 * MAXG
   float* hist;         // row r at hist + r * G * HPUB
@@ -305,7 +320,7 @@ template <int NE>
 struct RgChunkS : RgX {
   union {
     struct {
-      uint32_t hc[NT * NE / 4];             // 8-bit history counts of the chunk's ids
+      uint32_t hc[NT * NE / 2];             // 16-bit history counts of the chunk's ids
       unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
     } a;
     RgLists l;                               // after the counts and the histogram are used
@@ -567,11 +582,13 @@ __device__ __forceinline__ int prefetch_hist(const int32_t* hrow, int hlen) {
   const int j = threadIdx.x;
   return (hrow && j < hlen) ? hrow[j] : -1;
 }
-// 8-bit counts of the history ids that fall in the chunk's ids [lo, lo + n).
-// Returns false when a count reaches 255.  Ends with a barrier.
+// 16-bit counts of the history ids that fall in the chunk's ids [lo, lo + n)
+// (two per word).  Returns false when a count reaches 65534 (the row is then
+// deferred: an increment past 65535 would carry into the next id's count).
+// Ends with a barrier.
 template <int NE>
 __device__ __forceinline__ bool build_counts(RgChunkS<NE>& S, const int32_t* hrow, int hlen, int id0, int lo, int n) {
-  constexpr int WORDS = NT * NE / 4;
+  constexpr int WORDS = NT * NE / 2;
   static_assert(WORDS % 4 == 0, "whole 16-byte stores");
   u32x4* h4 = reinterpret_cast<u32x4*>(S.a.hc);
 #pragma unroll
@@ -582,9 +599,9 @@ __device__ __forceinline__ bool build_counts(RgChunkS<NE>& S, const int32_t* hro
   auto add = [&](int id) {
     if (id >= lo && id < lo + n) {
       const int l = id - lo;
-      const int sh = 8 * (l & 3);
-      const uint32_t old = atomicAdd(&S.a.hc[l >> 2], 1u << sh);
-      if (((old >> sh) & 0xFFu) >= 254u) sat = true;
+      const int sh = 16 * (l & 1);
+      const uint32_t old = atomicAdd(&S.a.hc[l >> 1], 1u << sh);
+      if (((old >> sh) & 0xFFFFu) >= 65533u) sat = true;
     }
   };
   add(id0);
@@ -605,19 +622,23 @@ __device__ __forceinline__ void apply_counts(Chk<DT, VPE, NE>& C, const uint32_t
     const int vl = t + i * NT;
     if (vl >= nv) continue;
     const int l0 = vl * VPE;  // chunk-local id of the vector's first logit
-    uint64_t cw;
+    uint32_t cw[(VPE + 1) / 2];  // the vector's counts, two per word
     if constexpr (VPE == 8) {
-      const uint2 q = *reinterpret_cast<const uint2*>(hc + (l0 >> 2));
-      cw = ((uint64_t)q.y << 32) | q.x;
+      const uint4 q = *reinterpret_cast<const uint4*>(hc + (l0 >> 1));
+      cw[0] = q.x; cw[1] = q.y; cw[2] = q.z; cw[3] = q.w;
     } else if constexpr (VPE == 4) {
-      cw = hc[l0 >> 2];
+      const uint2 q = *reinterpret_cast<const uint2*>(hc + (l0 >> 1));
+      cw[0] = q.x; cw[1] = q.y;
     } else {
-      cw = (hc[l0 >> 2] >> (8 * (l0 & 3))) & 0xFFu;
+      cw[0] = (hc[l0 >> 1] >> (16 * (l0 & 1))) & 0xFFFFu;
     }
-    if (!cw) continue;
+    uint32_t any = 0;
+#pragma unroll
+    for (int q = 0; q < (VPE + 1) / 2; q++) any |= cw[q];
+    if (!any) continue;
 #pragma unroll
     for (int e = 0; e < VPE; e++) {
-      const uint32_t cnt = (uint32_t)(cw >> (8 * e)) & 0xFFu;
+      const uint32_t cnt = VPE == 1 ? cw[0] : (cw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
       if (cnt) C.x[i * VPE + e] = penalize(C.x[i * VPE + e], (int)cnt, rep, pres, freq);
     }
   }
@@ -662,8 +683,8 @@ __device__ __forceinline__ void seg_done(RgLists& L, int l, uint32_t n) {
 // at [0, np0), list 1 at [np0, np0 + np1), entries {z key, index, x bits, 0}.  List 0
 // stops after rank lim0 - 1 and the entries whose z equals that entry's z
 // (lim0 = 0: no limit).  np[l] receives the counts; returns false when a
-// segment overflowed or the lists exceed cap (nothing written then).
-// Every thread calls it; it ends with a barrier.
+// segment overflowed or the lists, list 0 after its limit, exceed cap
+// (nothing written then).  Every thread calls it; it ends with a barrier.
 __device__ __forceinline__ bool sort_publish(RgLists& L, RgX& X, int nl, int lim0, bool greedy, float T, uint4* dst, int cap,
                                              int (&np)[2]) {
   const int tid = threadIdx.x;
@@ -678,7 +699,8 @@ __device__ __forceinline__ bool sort_publish(RgLists& L, RgX& X, int nl, int lim
       pre[l][w] = n[l];
       n[l] += c > SEGCAP ? SEGCAP : c;
     }
-  if (over || n[0] + n[1] > cap) {
+  if (over || (lim0 <= 0 && n[0] + n[1] > cap) || (lim0 > 0 && min(n[0], lim0) + n[1] > cap)) {
+    // (list 0 keeps at least min(n0, lim0) entries: past cap in any case)
     np[0] = np[1] = 0;
     __syncthreads();
     return false;
@@ -749,6 +771,11 @@ __device__ __forceinline__ bool sort_publish(RgLists& L, RgX& X, int nl, int lim
     if (first_out != 0x7FFFFFFF) atomicMin(&X.mi[8], first_out);
     __syncthreads();
     np0 = min(n[0], X.mi[8]);
+  }
+  if (np0 + n[1] > cap) {  // the entries tied with list 0's last kept one pass cap
+    np[0] = np[1] = 0;
+    __syncthreads();
+    return false;
   }
   // write in sorted order
 #pragma unroll

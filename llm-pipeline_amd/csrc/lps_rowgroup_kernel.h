@@ -18,7 +18,7 @@ __device__ __forceinline__ bool wait_count(uint32_t* p, uint32_t n) {
 // ===========================================================================
 template <int DT, int VPE, int NE>
 __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j,
-                                           const RowCfg& g) {
+                                           const RowCfg& g, const uint32_t epoch) {
   using CK = Chk<DT, VPE, NE>;
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -70,7 +70,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   sm.mkey = f2key(M);
   sm.amax = 0x7FFFFFFF;
   sm.ref = ref;
-  sm.xcc = xcc_id();
+  sm.tag = rg_tag(epoch, r, xcc_id());
   sm.reg[0] = sm.reg[1] = sm.reg[2] = sm.reg[3] = 1 << 30;
   // this chunk's published lists
   uint4* cbase = F.cands + (int64_t)r * CAPR + (int64_t)j * F.capw;
@@ -197,8 +197,8 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     __syncthreads();
     if (tid == 0) {
       release_count();
-      add_agent(ctr + 2, 1u);
-      S.mi[6] = wait_count(ctr + 2, (uint32_t)G) ? 0 : 1;
+      add_agent(ctr + CTR_HIST, 1u);
+      S.mi[6] = wait_count(ctr + CTR_HIST, (uint32_t)G) ? 0 : 1;
       acquire_one();
     }
     __syncthreads();
@@ -748,7 +748,8 @@ __device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_
 }
 
 template <int DT, int VPE>
-__device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g) {
+__device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g,
+                                           const uint32_t epoch) {
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = F.G;
@@ -756,9 +757,10 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   const char* row = row_ptr<DT>(P, r);
   const RgSum* sums = F.sums + (int64_t)r * 2 * MAXG + MAXG;
   const uint4* cands = F.cands + (int64_t)r * CAPR;
-  if (tid == 0) {  // the row's counters back to zero for the next launch
-    F.counters[(int64_t)r * 32] = 0u;
-    F.counters[(int64_t)r * 32 + 2] = 0u;
+  if (tid == 0) {  // the row's counters back to zero for the next launch, which has the next epoch
+    F.counters[(int64_t)r * 32 + CTR_ARRIVE] = 0u;
+    F.counters[(int64_t)r * 32 + CTR_HIST] = 0u;
+    F.counters[(int64_t)r * 32 + CTR_EPOCH] = epoch + 1u;
   }
   const int mode = g.mode;
   const bool greedy = g.greedy;
@@ -793,7 +795,9 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const int c1 = in ? (int)a.n1 : 0, c2 = in ? (int)a.n2 : 0;
     const int co = c1 + c2 > K0 ? c1 + c2 - K0 : 0;
     uint32_t fl = rreduce16(in ? a.flags : 0u, OpOr{});
-    const uint32_t xm = rreduce16(in ? 1u << a.xcc : 0u, OpOr{});
+    // every summary is this launch's and was written on this XCD (whose L2
+    // then holds everything the chunk published), else the row is deferred
+    const uint32_t stale = rreduce16((in && a.tag != rg_tag(epoch, r, xcc_id())) ? 1u : 0u, OpOr{});
     const uint32_t mk = rreduce16(in ? a.mkey : 0u, OpMax{});
     const float R = rreduce16(rfin ? a.ref : -INFINITY, OpMax{});
     const uint32_t nab = rreduce16(in ? a.nab1 : 0u, OpAdd{});
@@ -803,7 +807,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     // this lane's prefixes (chunks before it) and the totals (lanes >= G add 0)
     const int n1b = i1 - c1, n2b = i2 - c2, ob = io - co;
     const int n1t = rdlane(i1, 15), n2t = rdlane(i2, 15), ot = rdlane(io, 15);
-    if (__builtin_popcount(xm) > 1) fl |= RF_SPLIT;
+    if (stale) fl |= RF_SPLIT;
     RG_STAMP_DEP(20, fl);
     const int am = rreduce16(in && a.mkey == mk ? (int)a.amax : 0x7FFFFFFF, OpMin{});
     const double sc = rfin ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
@@ -1123,7 +1127,11 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (F.heavy_first) r = heavy_first_row(F.k, r);
   const RowCfg g = row_cfg(F.k, r);
   if (F.skip_topk && stream_takes(g)) return;
-  const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g);
+  // the row's launch epoch: written only by the finalisers of earlier
+  // launches (stream-ordered before this one), read by every chunk of the row
+  // before any of them arrives
+  const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
+  const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g, epoch);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1133,7 +1141,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __syncthreads();
   if (threadIdx.x == 0) {
     release_count();
-    SU.c.mi[7] = add_agent(F.counters + (int64_t)r * 32, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
+    SU.c.mi[7] = add_agent(F.counters + (int64_t)r * 32 + CTR_ARRIVE, 1u) + 1u == (uint32_t)F.G ? 1 : 0;
     if (SU.c.mi[7]) acquire_one();
   }
   __syncthreads();
@@ -1141,7 +1149,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (!SU.c.mi[7] || threadIdx.x >= FT) return;
   acquire_agent();
   RG_STAMP(24);
-  const int reason = final_phase<DT, VPE>(F, SU.f, r, g);
+  const int reason = final_phase<DT, VPE>(F, SU.f, r, g, epoch);
   RG_STAMP(31);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }

@@ -34,6 +34,11 @@
 //     logit of the row's top-k' set (ties included) is at or above the
 //     emission threshold max(own, smallest share) of its wave at any time.
 //     No barrier is taken inside the stream.
+// History ids.  Before the stream the row's in-range history ids set bits of
+// a vocabulary bitmap, and the set bits become a sorted list of the distinct
+// ids (a block scan of the words' bit counts gives each id its rank); with a
+// frequency penalty every history id then adds to its entry's count (found by
+// binary search).  An entry is id | count << 18 (ids < 2^18).
 // After the stream:
 //   - history ids: each distinct id's logit is read, masked, penalised
 //     (penalize: repetition once per distinct id, then frequency and presence)
@@ -46,8 +51,9 @@
 //     decided by the row-group finaliser's top-k code (topk_decide): the same
 //     kept set, cut, draw and outputs as the row-group kernel.
 // Rows the kernel cannot finish exactly (a wave segment overflow, a pool past
-// capacity, more distinct history ids than the table holds) are marked
-// LPS_ROW_DEFERRED for the general kernel.  Nucleus, pure and deferred-mode
+// capacity, more than HLIST distinct history ids or a count past HCMAX) are
+// marked LPS_ROW_DEFERRED for the general kernel, which counts histories of
+// any size.  Nucleus, pure and deferred-mode
 // rows are left to the row-group kernel, or deferred when it is not launched.
 #pragma once
 
@@ -64,6 +70,12 @@ constexpr int SVT = 4;            // 16-byte vectors per thread per tile
 constexpr int SEG = 256;          // candidate entries per wave segment
 constexpr int BMW = STREAM_VMAX / 32;  // history bitmap words
 constexpr int POOL = 2048;        // pool entries (wave candidates and history ids)
+constexpr int HLIST = 4096;       // distinct history ids of a row (sorted list)
+constexpr uint32_t HCMAX = (1u << 14) - 2;  // largest history count of an entry
+constexpr int HPT_ = HLIST / SNT; // list entries per thread after the stream
+constexpr int BMT = BMW / SNT;    // bitmap words per thread (word t + SNT i)
+static_assert(BMW % SNT == 0, "whole bitmap words per thread");
+static_assert(STREAM_VMAX <= (1 << 18), "18-bit ids in the list entries");
 static_assert(POOL == SNW * SEG, "the pool reuses the segments' storage");
 static_assert(KM == 4 * FT && FT == 256, "topk_decide runs on waves 0-3");
 static_assert(STREAM_KMAX <= 128, "first threshold from the lanes' top two");
@@ -78,8 +90,8 @@ struct StShared : RgX {
     } s;
   } a;
   uint64_t sc[KM];                      // prefix of the masses (topk_decide)
-  int32_t hkey[HASH_CAP];               // distinct history ids (open addressing)
-  int32_t hcnt[HASH_CAP];               // their counts
+  uint32_t hl[HLIST];                   // distinct history ids, ascending: id | count << 18
+  uint32_t hwb[SNW][BMT];               // bitmap words' bit counts per wave (list ranks)
   union {
     struct {
       uint32_t x[SNW][SEG];             // candidate logits (bits)
@@ -230,9 +242,11 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   // (the history ids first, then the row's parameters, then the chunks: loads
   // issued behind the whole GPU's first chunks would wait for them)
   const int32_t* hrow0 = P.history ? P.history + (int64_t)r * P.history_stride : nullptr;
-  const int32_t* hsrc = hrow0 ? hrow0 : reinterpret_cast<const int32_t*>(row);
-  const int hraw0 = hsrc[min((int64_t)tid, max(P.history_stride - 1, (int64_t)0))];
-  const int hraw1 = hsrc[min((int64_t)(tid + SNT), max(P.history_stride - 1, (int64_t)0))];
+  // (a row without history reads nothing; a history_stride of 0 shares one
+  // history between the rows, whose first ids are then read at their own offsets)
+  const int64_t hs = P.history_stride > 0 ? P.history_stride : ((int64_t)1 << 31);
+  const int hraw0 = (hrow0 && tid < hs) ? hrow0[tid] : -1;
+  const int hraw1 = (hrow0 && tid + SNT < hs) ? hrow0[tid + SNT] : -1;
   // (wave 0 alone loads the parameters, ahead of its chunks; the other waves'
   // would queue behind the chunks the first waves issued)
   __asm__ volatile("" ::: "memory");
@@ -245,8 +259,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   u32x4 b0[SVT], b1[SVT], b2[SVT];
   uint32_t a0[SVT], a1[SVT], a2[SVT];
   __asm__ volatile("" ::: "memory");
-  const int hid0 = (hrow0 && (int64_t)tid < P.history_stride) ? hraw0 : -1;
-  const int hid1 = (hrow0 && (int64_t)(tid + SNT) < P.history_stride) ? hraw1 : -1;
+  const int hid0 = hraw0, hid1 = hraw1;
 
   if (wv == 0 && lane == 0) S.cfg = g0;
 
@@ -263,22 +276,18 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     }
     S.km[tid] = make_uint4(mk[0], mk[1], mk[2], mk[3]);
   }
-  // ---- the history: bitmap of the distinct in-range ids, and their counts
-  // (cleared before the parameters are known: one barrier for both) ----
+  // ---- the history: bitmap of the distinct in-range ids (cleared before
+  // the parameters are known: one barrier for both) ----
   {
     const int nw = (V + 31) >> 5;
     for (int i = tid; i < nw; i += SNT) S.a.bm[i] = 0u;
-    for (int i = tid; i < HASH_CAP; i += SNT) {
-      S.hkey[i] = -1;
-      S.hcnt[i] = 0;
-    }
   }
   if (lane == 0) S.segjt[wv] = -3.40282347e38f;
   if (tid == 0) {
     S.mi[0] = 0;
     S.mi[1] = 0;
     S.mi[2] = 0;  // chunks taken past the first three of every wave
-    S.mi[3] = 0;  // distinct-id list length (no frequency penalty)
+    S.mi[3] = 0;  // distinct history ids
     S.pn = 0;
   }
   __syncthreads();
@@ -296,71 +305,77 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   const bool pen = g.pen;
   const bool kill = pen || am;
   RG_STAMP(11);
-  // (without a frequency penalty an id's count does not matter: the bitmap
-  // decides membership, and the thread whose bit-set finds the bit clear
-  // appends the id to a list, in place of the hash table)
+  // (without a frequency penalty an id's count does not matter: the list
+  // entries keep count 0)
   const bool counts = g.freq != 0.0f;
   if (pen) {
-    bool full = false;
-    uint32_t fresh = 0;  // distinct ids this thread inserted
-    // without counts: every lane of the wave calls it (id < 0: none); the
-    // wave's new ids take consecutive list slots, one LDS atomic per wave
-    auto insert_list = [&](int id) {
-      bool nw_id = false;
-      if (id >= 0 && id < V) {
-        const uint32_t bit = 1u << (id & 31);
-        nw_id = !(atomicOr(&S.a.bm[id >> 5], bit) & bit);
-      }
-      const uint64_t bal = __builtin_amdgcn_ballot_w64(nw_id);
-      if (bal) {
-        const int lead = __builtin_ctzll(bal);
-        int base = 0;
-        if (lane == lead) base = atomicAdd(&S.mi[3], __builtin_popcountll(bal));
-        base = __shfl(base, lead);
-        if (nw_id) {
-          const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          if (p < HASH_CAP) {
-            S.hkey[p] = id;
-            S.hcnt[p] = 1;
-          } else {
-            full = true;
-          }
-          fresh++;
-        }
-      }
+    auto mark = [&](int id) {
+      if (id >= 0 && id < V) atomicOr(&S.a.bm[id >> 5], 1u << (id & 31));
     };
-    auto insert = [&](int id) {
-      if (id < 0 || id >= V) return;
-      atomicOr(&S.a.bm[id >> 5], 1u << (id & 31));
-      uint32_t sl = hash_id(id);
-      int p = 0;
-      for (; p < HASH_CAP; p++) {
-        const int old = atomicCAS(&S.hkey[sl], -1, id);
-        if (old == -1 || old == id) {
-          atomicAdd(&S.hcnt[sl], 1);
-          fresh += old == -1 ? 1u : 0u;
-          break;
-        }
-        sl = (sl + 1) & (HASH_CAP - 1);
-      }
-      if (p == HASH_CAP) full = true;
-    };
-    if (!counts) {
-      insert_list(tid < g.hlen ? hid0 : -1);
-      insert_list(tid + SNT < g.hlen ? hid1 : -1);
-      for (int j0 = 2 * SNT; j0 < g.hlen; j0 += SNT) insert_list(j0 + tid < g.hlen ? g.hrow[j0 + tid] : -1);
-    } else {
-      if (tid < g.hlen) insert(hid0);
-      if (tid + SNT < g.hlen) insert(hid1);
-      for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) insert(g.hrow[j]);
+    if (tid < g.hlen) mark(hid0);
+    if (tid + SNT < g.hlen) mark(hid1);
+    for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) mark(g.hrow[j]);
+  }
+  __syncthreads();
+  if (pen) {
+    // ranks: word t + SNT i of thread t; words in order i-major.  The bit
+    // counts of each round i are scanned over the block (per wave by DPP,
+    // then across waves), and the rounds follow each other.
+    const int nw = (V + 31) >> 5;
+    uint32_t wd[BMT], pc[BMT], ex[BMT];
+#pragma unroll
+    for (int i = 0; i < BMT; i++) {
+      const int w = tid + SNT * i;
+      wd[i] = w < nw ? S.a.bm[w] : 0u;
+      pc[i] = (uint32_t)__builtin_popcount(wd[i]);
+      const uint32_t inc = wscan_incl(pc[i]);
+      ex[i] = inc - pc[i];
+      if (lane == 63) S.hwb[wv][i] = inc;
     }
-    if (fresh) atomicAdd(&S.mi[1], (int)fresh);
-    if (full) S.mi[0] = 1;
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (int i = 0; i < BMT; i++) {
+      uint32_t before = 0, round = 0;
+#pragma unroll
+      for (int v = 0; v < SNW; v++) {
+        const uint32_t c = S.hwb[v][i];
+        before += v < wv ? c : 0u;
+        round += c;
+      }
+      uint32_t rk = base + before + ex[i];
+      const int w0 = (tid + SNT * i) << 5;
+      for (uint32_t b = wd[i]; b; b &= b - 1u) {
+        if (rk < (uint32_t)HLIST) S.hl[rk] = (uint32_t)(w0 + __builtin_ctz(b));
+        rk++;
+      }
+      base += round;
+    }
+    if (tid == 0) S.mi[3] = (int)base;
+    __syncthreads();
+    const int D = S.mi[3];
+    if (counts && D <= HLIST) {
+      // every history id adds one to its entry (binary search over the sorted ids)
+      int lg = 0;
+      while ((1 << lg) < D) lg++;
+      bool sat = false;
+      auto add = [&](int id) {
+        if (id < 0 || id >= V) return;
+        int p = 0;
+        for (int st = 1 << lg; st > 0; st >>= 1)
+          if (p + st < D && (int)(S.hl[p + st] & 0x3FFFFu) <= id) p += st;
+        const uint32_t old = atomicAdd(&S.hl[p], 1u << 18);
+        if ((old >> 18) >= HCMAX) sat = true;
+      };
+      if (tid < g.hlen) add(hid0);
+      if (tid + SNT < g.hlen) add(hid1);
+      for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) add(g.hrow[j]);
+      if (sat) S.mi[0] = 1;
+    }
   }
   __syncthreads();
   RG_STAMP(10);
-  const bool defer_hist = pen && (S.mi[0] != 0 || S.mi[1] > LPS_MAX_HISTORY_DISTINCT);
+  const bool defer_hist = pen && (S.mi[0] != 0 || S.mi[3] > HLIST);
   // (the chunks only now, in this order: the loop's waits count on b0, b1 and
   // b2's loads in turn; a first flood of every wave's chunks would hold the
   // parameters and history ids above back behind it)
@@ -554,13 +569,17 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   RG_STAMP(2);
   // the history ids' logits (id 0 for empty slots: no divergent loads),
   // loaded before the barrier below
-  constexpr int HPT_ = HASH_CAP / SNT;
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   uint32_t hraw[HPT_];
   int hid[HPT_];
+  uint32_t hct[HPT_];
+  const int nhl = (pen && !defer_hist) ? S.mi[3] : 0;
 #pragma unroll
   for (int q = 0; q < HPT_; q++) {
-    hid[q] = pen ? S.hkey[tid + q * SNT] : -1;
+    const int e = tid + q * SNT;
+    const uint32_t ent = e < nhl ? S.hl[e] : 0u;
+    hid[q] = e < nhl ? (int)(ent & 0x3FFFFu) : -1;
+    hct[q] = ent >> 18;
     const int64_t o = (int64_t)max(hid[q], 0) * ES;
     if constexpr (ES == 4) hraw[q] = *reinterpret_cast<const uint32_t*>(row + o);
     else hraw[q] = *reinterpret_cast<const unsigned short*>(row + o);
@@ -624,7 +643,6 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   bool hk[HPT_];
 #pragma unroll
   for (int q = 0; q < HPT_; q++) {
-    const int s = tid + q * SNT;
     const int id = hid[q];
     hk[q] = false;
     hx[q] = 0u;
@@ -632,7 +650,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
       float xv = ES == 4 ? __uint_as_float(hraw[q])
                          : (DT == LPS_DTYPE_BF16 ? __uint_as_float(hraw[q] << 16) : f16_to_f32(hraw[q]));
       if (!id_allowed(am, id)) xv = -INFINITY;
-      xv = penalize(xv, S.hcnt[s], g.rep, g.pres, g.freq);
+      xv = penalize(xv, (int)hct[q], g.rep, g.pres, g.freq);
       hx[q] = __float_as_uint(xv);
       if (xv != xv) nanidx = min(nanidx, id);
       if (greedy) {

@@ -29,10 +29,10 @@ LPS_DTYPE_F16 = 2
 
 LPS_ROW_NONFINITE = 1
 LPS_ROW_EMPTY = 2
-LPS_ROW_HISTORY_OVERFLOW = 4
+LPS_ROW_HISTORY_OVERFLOW = 4   # never set since ABI version 2 (histories of any size)
+LPS_ABI_VERSION = 2
 
 LPS_MAX_TOP_LOGPROBS = 64
-LPS_MAX_HISTORY_DISTINCT = 1536
 
 LPS_FLAG_GENERIC = 1
 LPS_FLAG_APPEND_HISTORY = 2
@@ -141,7 +141,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = argt
-        if lib.lps_version() != 1:
+        if lib.lps_version() != LPS_ABI_VERSION:
             raise RuntimeError(f"lps ABI version mismatch: {lib.lps_version()}")
         _lib = lib
         return lib

@@ -329,7 +329,4 @@ def raise_on_status(status: torch.Tensor) -> None:
     bad = int(status.ne(0).any().item())
     if not bad:
         return
-    s = int(status.max().item())
-    if s & _lib.LPS_ROW_HISTORY_OVERFLOW:
-        raise ValueError(f"token history holds more than {_lib.LPS_MAX_HISTORY_DISTINCT} distinct ids")
     raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")
