@@ -101,17 +101,22 @@ int rg_max_chunks(int R, int V) {
 // Bytes of the per-row counter region at the workspace's start.
 size_t rg_counter_bytes() { return (size_t)RG_MAX_ROWS * 128; }
 
+// Region `off` of the workspace at base (nullptr when only sizes are wanted).
+template <typename T>
+T* ws_at(void* base, size_t off) {
+  return base ? reinterpret_cast<T*>(reinterpret_cast<char*>(base) + off) : nullptr;
+}
+
 RgWs rg_layout(void* base, int R, int V) {
   RgWs w{};
   if (R > RG_MAX_ROWS) R = RG_MAX_ROWS;
   const int G = rg_max_chunks(R, V);
   size_t off = 0;
-  char* p = reinterpret_cast<char*>(base);
-  w.counters = reinterpret_cast<uint32_t*>(p + off); off = rg_counter_bytes();
-  w.status = reinterpret_cast<int32_t*>(p + off); off = round_up(off + (size_t)R * 4, 256);
-  w.sums = reinterpret_cast<rg::RgSum*>(p + off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
-  w.hist = reinterpret_cast<float*>(p + off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
-  w.cands = reinterpret_cast<uint4*>(p + off); off = round_up(off + (size_t)R * rg::CAPR * 16, 256);
+  w.counters = ws_at<uint32_t>(base, off); off = rg_counter_bytes();
+  w.status = ws_at<int32_t>(base, off); off = round_up(off + (size_t)R * 4, 256);
+  w.sums = ws_at<rg::RgSum>(base, off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
+  w.hist = ws_at<float>(base, off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
+  w.cands = ws_at<uint4>(base, off); off = round_up(off + (size_t)R * rg::CAPR * 16, 256);
   w.bytes = off;
   return w;
 }
@@ -138,7 +143,11 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   // batches of more than one resident round of chunk workgroups: greedy and
   // top-k rows stream through one workgroup each (stream_kernel), the
   // row-group kernel takes the others; the row-kind hints skip a kernel no row
-  // needs (a row the hint misjudges is deferred to the general kernel)
+  // needs (a row the hint misjudges is deferred to the general algorithm).
+  // Rows either kernel cannot finish exactly are sampled by the general
+  // algorithm: when the row-group kernel alone runs one resident round, in
+  // the row's tail workgroup (grid = the chunk grid, then one per row); else
+  // by the general kernel launched after them.
   bool big = false;
   if constexpr (VPE > 1) big = grid > (unsigned)device_cus() && F.k.V <= rg::STREAM_VMAX;
   const bool run_stream = big && !(flags & LPS_FLAG_ROWS_NUCLEUS);
@@ -153,13 +162,17 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
       F.skip_topk = 1;
     }
   }
+  F.main_grid = (int)grid;  // (a multiple of 8: row r's tail runs on the row's XCD)
+  F.tails = (run_rg && !run_stream && grid <= (unsigned)device_cus()) ? 1 : 0;
   if (run_rg) {
-    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
+    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid + (F.tails ? (unsigned)F.k.R : 0u)),
+                       dim3(rg::NT), 0, s, F);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  // rows the row-group kernel deferred: the general algorithm, one 1024-thread
-  // workgroup per row (the others return at once)
+  if (F.tails) return hipSuccess;
+  // the rows the fast kernels deferred: the general algorithm, one
+  // 1024-thread workgroup per row (the others return at once)
   KParams G = F.k;
   G.only_status = F.status;
   G.plans = nullptr;
@@ -283,16 +296,15 @@ struct SpecWs {
 SpecWs spec_layout(void* base, int B, int k, int V) {
   SpecWs w{};
   const size_t Rt = (size_t)B * (k + 1), Rd = (size_t)B * k;
-  char* p = reinterpret_cast<char*>(base);
   w.fast = base;
   w.fast_bytes = rg_layout(nullptr, (int)Rt, V).bytes;
   size_t off = align256(w.fast_bytes);
-  w.draws_t = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rt * 8);
-  w.draws_d = reinterpret_cast<int64_t*>(p + off); off = align256(off + Rd * 8);
-  w.p_t = reinterpret_cast<float*>(p + off); off = align256(off + Rt * 4);
-  w.q_d = reinterpret_cast<float*>(p + off); off = align256(off + Rd * 4);
-  w.first_rej = reinterpret_cast<int32_t*>(p + off); off = align256(off + (size_t)B * 4);
-  w.plans = reinterpret_cast<RowPlan*>(p + off); off = align256(off + (Rt + Rd) * sizeof(RowPlan));
+  w.draws_t = ws_at<int64_t>(base, off); off = align256(off + Rt * 8);
+  w.draws_d = ws_at<int64_t>(base, off); off = align256(off + Rd * 8);
+  w.p_t = ws_at<float>(base, off); off = align256(off + Rt * 4);
+  w.q_d = ws_at<float>(base, off); off = align256(off + Rd * 4);
+  w.first_rej = ws_at<int32_t>(base, off); off = align256(off + (size_t)B * 4);
+  w.plans = ws_at<RowPlan>(base, off); off = align256(off + (Rt + Rd) * sizeof(RowPlan));
   w.bytes = off;
   return w;
 }

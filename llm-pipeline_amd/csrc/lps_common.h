@@ -6,6 +6,13 @@
 
 #include "lps.h"
 
+// Keeps x in a vector register, opaque to the optimiser (an empty asm with a
+// VGPR operand).  A host build of the kernels for the bounds-checking test
+// harness defines its own before this header.
+#ifndef LPS_KEEP_VGPR
+#define LPS_KEEP_VGPR(x) __asm__ volatile("" : "+v"(x))
+#endif
+
 namespace lps {
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -93,9 +93,12 @@ __device__ __forceinline__ const uint8_t* row_allowed(const KParams& P, int r) {
 __device__ __forceinline__ bool id_allowed(const uint8_t* am, int64_t i) {
   return !am || ((am[i >> 3] >> (i & 7)) & 1u);
 }
-// Workspace row status bit (beside the LPS_ROW_* bits): the fast kernels
-// deferred the row to the general kernel.
+// Workspace row status bits (beside the LPS_ROW_* bits): the fast kernels
+// deferred the row to the general kernel's launch (LPS_ROW_DEFERRED), or
+// sampled it with the general algorithm in their own launch (LPS_ROW_GENERAL);
+// the reason code is in bits 8 and up.
 constexpr int32_t LPS_ROW_DEFERRED = 8;
+constexpr int32_t LPS_ROW_GENERAL = 64;
 
 struct GenShared {
   alignas(16) uint32_t wcnt[GEN_WIN];  // history counts of the ids [w0, w0 + GEN_WIN) of the loaded window
@@ -115,7 +118,11 @@ struct GenShared {
   uint32_t red32[GEN_NW];
   int32_t misc[8];
   uint64_t misc64[4];
+  int32_t nth;  // threads running the general algorithm: 0 .. nth - 1 (a multiple of 64, at most GEN_NT;
+                // the block may hold more, which have left)
 };
+// Threads running the general algorithm (set by its entry points).
+__device__ __forceinline__ int gnt(const GenShared& S) { return S.nth; }
 
 // The row's legality bits and penalties.  The history counts are those of one
 // window of ids (pen_window loads it); apply() takes logits of that window.
@@ -170,31 +177,32 @@ __device__ __forceinline__ int64_t win_size(const PenCtx& pc) { return pc.active
 // Enters the window starting at id w0: its history counts are counted from the
 // row's whole history unless they are loaded already.  Every thread calls it
 // (block-uniform arguments); it ends with a barrier when it loads.
-__device__ __forceinline__ void pen_window(PenCtx& pc, uint32_t* wcnt, int64_t w0) {
+__device__ __forceinline__ void pen_window(PenCtx& pc, GenShared& S, int64_t w0) {
   pc.w0 = w0;
   if (!pc.active || pc.loaded == w0) return;
+  const int nt = gnt(S);
   __syncthreads();  // every reader of the previous window is done with it
-  uint4* c4 = reinterpret_cast<uint4*>(wcnt);
-  for (int i = threadIdx.x; i < GEN_WIN / 4; i += (int)blockDim.x) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+  uint4* c4 = reinterpret_cast<uint4*>(S.wcnt);
+  for (int i = threadIdx.x; i < GEN_WIN / 4; i += nt) c4[i] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
   const int64_t w1 = w0 + GEN_WIN < (int64_t)pc.V ? w0 + GEN_WIN : (int64_t)pc.V;
-  for (int j = threadIdx.x; j < pc.hlen; j += (int)blockDim.x) {
+  for (int j = threadIdx.x; j < pc.hlen; j += nt) {
     const int64_t id = pc.hist[j];
-    if (id >= w0 && id < w1) atomicAdd(&wcnt[id - w0], 1u);
+    if (id >= w0 && id < w1) atomicAdd(&S.wcnt[id - w0], 1u);
   }
   __syncthreads();
   pc.loaded = w0;
 }
 
 // ---------------------------------------------------------------------------
-// Block helpers (blockDim.x threads, a multiple of 64, at most GEN_NT).
+// Block helpers (gnt(S) threads, a multiple of 64, at most GEN_NT).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t gblock_max_u64(uint64_t v, GenShared& S) {
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = S.red64[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = S.red64[i] > r ? S.red64[i] : r;
+  for (int i = 1; i < (gnt(S) >> 6); i++) r = S.red64[i] > r ? S.red64[i] : r;
   __syncthreads();
   return r;
 }
@@ -203,7 +211,7 @@ __device__ __forceinline__ uint64_t gblock_sum_u64(uint64_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red64[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.red64[i];
+  for (int i = 0; i < (gnt(S) >> 6); i++) r += S.red64[i];
   __syncthreads();
   return r;
 }
@@ -212,7 +220,7 @@ __device__ __forceinline__ uint32_t gblock_min_u32(uint32_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
   __syncthreads();
   uint32_t r = S.red32[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = S.red32[i] < r ? S.red32[i] : r;
+  for (int i = 1; i < (gnt(S) >> 6); i++) r = S.red32[i] < r ? S.red32[i] : r;
   __syncthreads();
   return r;
 }
@@ -221,7 +229,7 @@ __device__ __forceinline__ uint32_t gblock_sum_u32(uint32_t v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.red32[threadIdx.x >> 6] = v;
   __syncthreads();
   uint32_t r = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.red32[i];
+  for (int i = 0; i < (gnt(S) >> 6); i++) r += S.red32[i];
   __syncthreads();
   return r;
 }
@@ -230,19 +238,19 @@ __device__ __forceinline__ double gblock_sum_f64(double v, GenShared& S) {
   if ((threadIdx.x & 63) == 0) S.redd[threadIdx.x >> 6] = v;
   __syncthreads();
   double r = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); i++) r += S.redd[i];
+  for (int i = 0; i < (gnt(S) >> 6); i++) r += S.redd[i];
   __syncthreads();
   return r;
 }
-// Exclusive scan over the block in thread order; *total = block sum.
+// Exclusive scan over the nt threads in thread order; *total = their sum.
 template <typename T>
-__device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch) {
+__device__ __forceinline__ T gblock_excl_scan(T v, T* total, T* scratch, int nt) {
   T inc = wave_incl_scan(v);
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 63) scratch[w] = inc;
   __syncthreads();
   T off = 0, tot = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); i++) {
+  for (int i = 0; i < (nt >> 6); i++) {
     T s = scratch[i];
     off += (i < w) ? s : (T)0;
     tot += s;
@@ -260,9 +268,9 @@ template <int DT, int VEC, typename F>
 __device__ __forceinline__ void row_pass(const void* row, int V, PenCtx& pc, GenShared& S, F&& f) {
   const int64_t W = win_size(pc);
   for (int64_t w0 = 0; w0 < V; w0 += W) {
-    pen_window(pc, S.wcnt, w0);
+    pen_window(pc, S, w0);
     const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
-    for (int64_t i0 = w0 + (int64_t)threadIdx.x * VEC; i0 < w1; i0 += (int64_t)(int)blockDim.x * VEC) {
+    for (int64_t i0 = w0 + (int64_t)threadIdx.x * VEC; i0 < w1; i0 += (int64_t)gnt(S) * VEC) {
       float x[VEC];
       loadv<DT, VEC>(row, i0, x);
       pc.apply<VEC>(i0, x);
@@ -284,7 +292,7 @@ __device__ __forceinline__ uint32_t lvl_himask(int l) { return l == 0 ? 0u : (l 
 __device__ void find_bin(GenShared& S, int nb, bool by_mass, uint64_t target_or_limit, uint64_t base) {
   if (threadIdx.x == 0) { S.misc[0] = -1; S.misc64[0] = 0; S.misc64[1] = 0; }
   // thread t owns descending positions r = t*per .. t*per+per-1 (bin = nb-1-r)
-  const int per = nb / (int)blockDim.x > 0 ? nb / (int)blockDim.x : 1;
+  const int per = nb / gnt(S) > 0 ? nb / gnt(S) : 1;
   const int r0 = threadIdx.x * per;
   uint64_t v = 0;
   for (int q = 0; q < per; q++) {
@@ -292,7 +300,7 @@ __device__ void find_bin(GenShared& S, int nb, bool by_mass, uint64_t target_or_
     if (rr < nb) v += by_mass ? S.u.h.mass[nb - 1 - rr] : (uint64_t)S.u.h.cnt[nb - 1 - rr];
   }
   uint64_t tot;
-  uint64_t a = gblock_excl_scan<uint64_t>(v, &tot, S.red64);
+  uint64_t a = gblock_excl_scan<uint64_t>(v, &tot, S.red64, gnt(S));
   for (int q = 0; q < per; q++) {
     const int rr = r0 + q;
     if (rr >= nb) break;
@@ -309,7 +317,7 @@ __device__ void find_bin(GenShared& S, int nb, bool by_mass, uint64_t target_or_
 
 template <int DT, int VEC>
 __device__ void clear_hist(GenShared& S) {
-  for (int i = threadIdx.x; i < NBINS; i += (int)blockDim.x) { S.u.h.cnt[i] = 0; S.u.h.mass[i] = 0; }
+  for (int i = threadIdx.x; i < NBINS; i += gnt(S)) { S.u.h.cnt[i] = 0; S.u.h.mass[i] = 0; }
   __syncthreads();
 }
 
@@ -390,9 +398,13 @@ __device__ __forceinline__ MassCut select_mass(const void* row, int V, PenCtx& p
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
+// Samples row r with threads 0 .. nth - 1 of the block (nth a multiple of 64,
+// at most GEN_NT; threads of the block past nth must have left it, and every
+// thread below nth must call this).
 template <int DT, int VEC>
-__device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared& S) {
+__device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared& S, const int nth) {
   const int tid = threadIdx.x;
+  S.nth = nth;  // (every thread stores the same value before its first use)
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   const void* row = reinterpret_cast<const char*>(P.logits) +
                     ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
@@ -573,9 +585,9 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     // (windows of ids, tiles in vocabulary order within each: tie ranks run in vocabulary order)
     const int64_t W = win_size(pc);
     for (int64_t w0 = 0; w0 < V; w0 += W) {
-    pen_window(pc, S.wcnt, w0);
+    pen_window(pc, S, w0);
     const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
-    for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
+    for (int64_t tile = w0; tile < w1; tile += (int64_t)gnt(S) * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       float x[VEC];
       uint32_t k[VEC];
@@ -587,7 +599,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == key_lo ? 1u : 0u; }
       }
       uint32_t tot = 0, ex = 0;
-      if (n_tie != kNoTie) ex = gblock_excl_scan<uint32_t>(nt_loc, &tot, S.red32);
+      if (n_tie != kNoTie) ex = gblock_excl_scan<uint32_t>(nt_loc, &tot, S.red32, gnt(S));
       if (i0 < w1) {
         uint32_t rk = tie_run + ex;
 #pragma unroll
@@ -640,9 +652,9 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
     const int64_t W = win_size(pc);
     bool done = false;
     for (int64_t w0 = 0; w0 < V && !done; w0 += W) {
-    pen_window(pc, S.wcnt, w0);
+    pen_window(pc, S, w0);
     const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
-    for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
+    for (int64_t tile = w0; tile < w1; tile += (int64_t)gnt(S) * VEC) {
       const int64_t i0 = tile + (int64_t)tid * VEC;
       uint32_t k[VEC];
       uint32_t nt_loc = 0;
@@ -654,7 +666,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == vkey ? 1u : 0u; }
       }
       uint32_t ttot;
-      const uint32_t tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
+      const uint32_t tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32, gnt(S));
       if (i0 < w1 && run + tex <= jt && jt < run + tex + nt_loc) {
         uint32_t rk = run + tex;
 #pragma unroll
@@ -682,7 +694,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       // the drawn id's history count (the whole block counts it)
       uint32_t tc = 0;
       if (pen && token >= 0)
-        for (int j = tid; j < hlen; j += (int)blockDim.x) tc += pc.hist[j] == token ? 1u : 0u;
+        for (int j = tid; j < hlen; j += gnt(S)) tc += pc.hist[j] == token ? 1u : 0u;
       tc = gblock_sum_u32(tc, S);
       if (tid == 0) {
         float lp = NAN;
@@ -705,9 +717,9 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
       uint32_t tie_run = 0;
       const int64_t W = win_size(pc);
       for (int64_t w0 = 0; w0 < V; w0 += W) {
-      pen_window(pc, S.wcnt, w0);
+      pen_window(pc, S, w0);
       const int64_t w1 = w0 + W < (int64_t)V ? w0 + W : (int64_t)V;
-      for (int64_t tile = w0; tile < w1; tile += (int64_t)(int)blockDim.x * VEC) {
+      for (int64_t tile = w0; tile < w1; tile += (int64_t)gnt(S) * VEC) {
         const int64_t i0 = tile + (int64_t)tid * VEC;
         float x[VEC];
         uint32_t k[VEC];
@@ -718,7 +730,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
 #pragma unroll
           for (int j = 0; j < VEC; j++) { k[j] = zkey(x[j]); nt_loc += k[j] == thn ? 1u : 0u; }
         }
-        uint32_t ttot, tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32);
+        uint32_t ttot, tex = gblock_excl_scan<uint32_t>(nt_loc, &ttot, S.red32, gnt(S));
         if (i0 < w1) {
           uint32_t rk = tie_run + tex;
 #pragma unroll
@@ -749,7 +761,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
         P.top_logprobs[(int64_t)r * P.n_top + rank] = need_full ? (float)((double)__fsub_rn(z, zmax) - lnZ) : NAN;
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + rank] = ii;
       }
-      for (int j = n + tid; j < P.n_top; j += (int)blockDim.x) {
+      for (int j = n + tid; j < P.n_top; j += gnt(S)) {
         P.top_logprobs[(int64_t)r * P.n_top + j] = -INFINITY;
         if (P.top_ids) P.top_ids[(int64_t)r * P.n_top + j] = -1;
       }
@@ -784,7 +796,7 @@ __global__ __launch_bounds__(GEN_NT) void gen_row_kernel(KParams P) {
   // a copy local to the rows that run: the general path takes the parameters
   // by reference, and a skipped row then never copies them to scratch memory
   KParams Pl = P;
-  gen_row<DT, VEC>(Pl, r, S);
+  gen_row<DT, VEC>(Pl, r, S, GEN_NT);
 }
 
 }  // namespace lps

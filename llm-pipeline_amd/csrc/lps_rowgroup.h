@@ -47,9 +47,13 @@
 //
 // A row the kernel cannot finish exactly (e.g. a flat row whose regions hold
 // more candidates than the lists take, min-p / typical-p without top-k,
-// entropy requested) is marked LPS_ROW_DEFERRED in the workspace status and
-// sampled by the general kernel, launched after this one with that status as
-// its filter.
+// entropy requested) is sampled by the general algorithm.  A launch of one
+// resident round (grid <= CUs) ends with one tail workgroup per row (on the
+// row's XCD), which waits for the row's decision word and runs the general
+// algorithm when the row was deferred (LPS_ROW_GENERAL in the workspace
+// status); a larger launch marks the row LPS_ROW_DEFERRED and is followed by
+// the general kernel with that status as its filter (tail workgroups there
+// would form a round of their own).
 //
 // Cross-workgroup handoffs (the histogram barrier and the arrival count):
 // every thread of the publishing workgroup stores, then waits for its stores
@@ -158,7 +162,9 @@ __device__ __forceinline__ uint64_t rg_tag(uint32_t epoch, int r, uint32_t xcc) 
 }
 constexpr int CTR_ARRIVE = 0;  // counter words of a row (32 per row): arrivals,
 constexpr int CTR_HIST = 2;    // the histogram barrier,
-constexpr int CTR_EPOCH = 4;   // and the row's launch epoch (never reset)
+constexpr int CTR_EPOCH = 4;   // the row's launch epoch (never reset),
+constexpr int CTR_DECIDE = 6;  // and its decision for the tail workgroup (DEC_*; the tail resets it)
+enum { DEC_NONE = 0, DEC_DONE = 1, DEC_GENERAL = 2 };
 
 struct RgParams {
   KParams k;
@@ -169,7 +175,10 @@ struct RgParams {
   int nvec;            // vectors per row
   int heavy_first;     // dispatch rows without top-k first
   int skip_topk;       // the streaming kernel's rows (stream_takes) ran there: skip them
-  int stream_only;     // the row-group kernel is not launched: the streaming kernel defers the others
+  int stream_only;     // the row-group kernel is not launched: the streaming kernel samples the others
+                       // with the general algorithm
+  int main_grid;       // workgroups of the chunk grid; workgroup main_grid + r is row r's tail
+  int tails;           // the grid ends with the tail workgroups (else the general kernel follows)
   uint32_t* counters;  // [R * 32]: arrivals and the histogram barrier (zero between launches), the
                        // row's launch epoch (CTR_*)
   int32_t* status;     // [R]
@@ -338,6 +347,7 @@ template <int NE>
 union RgShared {
   RgChunkS<NE> c;
   RgFinalS f;
+  GenShared g;  // a tail workgroup running the general algorithm
 };
 
 // ---------------------------------------------------------------------------

@@ -1114,12 +1114,59 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   return 0;
 }
 
+// The row's decision for its tail workgroup (one thread; an agent-scope
+// atomic, coherent whichever XCD the tail runs on).
+__device__ __forceinline__ void decide(const RgParams& F, int r, uint32_t d) {
+  __hip_atomic_store(F.counters + (int64_t)r * 32 + CTR_DECIDE, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tail workgroup of row r: waits for the row's decision (a bounded wait; the
+// chunk workgroups it waits for were all dispatched before it), resets the
+// word for the next launch, and samples the row with the general algorithm
+// on all NT threads when the row was deferred.
+template <int DT, int VPE>
+__device__ __forceinline__ void tail_block(const RgParams& F, GenShared& S, const int r) {
+  if (r >= F.k.R) return;
+  if (F.skip_topk && stream_takes(row_cfg(F.k, r))) return;  // the streaming kernel's row
+  uint32_t* dw = F.counters + (int64_t)r * 32 + CTR_DECIDE;
+  if (threadIdx.x == 0) {
+    uint32_t d = DEC_NONE;
+    for (int spins = 0; spins < (1 << 22); spins++) {
+      d = ld_agent(dw);
+      if (d != DEC_NONE) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    __hip_atomic_store(dw, (uint32_t)DEC_NONE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    S.misc[7] = (int)d;
+  }
+  __syncthreads();
+  const int d = S.misc[7];
+  __syncthreads();
+  if (d == DEC_NONE) {  // no decision in time (not reached while chunk groups run to the end)
+    if (threadIdx.x == 0) {
+      F.k.tokens[r] = -1;
+      if (F.k.row_status) F.k.row_status[r] = LPS_ROW_INTERNAL;
+    }
+    return;
+  }
+  if (d != DEC_GENERAL) return;
+  KParams P = F.k;
+  P.plans = nullptr;
+  P.only_status = nullptr;
+  gen_row<DT, VPE>(P, r, S, NT);
+}
+
 // ===========================================================================
-// The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
+// The kernel: grid of ceil(R / 8) * 8 * G chunk workgroups of NT threads,
+// then R tail workgroups.
 // ===========================================================================
 template <int DT, int VPE, int NE>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;
+  if ((int)blockIdx.x >= F.main_grid) {
+    tail_block<DT, VPE>(F, SU.g, (int)blockIdx.x - F.main_grid);
+    return;
+  }
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   int r = (slot / F.G) * 8 + xcd;
   const int j = slot % F.G;
@@ -1133,7 +1180,10 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
   const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g, epoch);
   if (mode == MODE_DEFER) {
-    if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
+    if (j == 0 && threadIdx.x == 0) {
+      F.status[r] = (F.tails ? LPS_ROW_GENERAL : LPS_ROW_DEFERRED) | (1 << 8);
+      if (F.tails) decide(F, r, DEC_GENERAL);
+    }
     return;
   }
   // arrival: the chunk's stores are visible at agent scope before it is counted
@@ -1151,7 +1201,10 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   RG_STAMP(24);
   const int reason = final_phase<DT, VPE>(F, SU.f, r, g, epoch);
   RG_STAMP(31);
-  if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
+  if (threadIdx.x == 0) {
+    if (reason > 0) F.status[r] = (F.tails ? LPS_ROW_GENERAL : LPS_ROW_DEFERRED) | (reason << 8);
+    if (F.tails) decide(F, r, reason > 0 ? DEC_GENERAL : DEC_DONE);
+  }
 }
 
 }  // namespace rg

@@ -81,6 +81,7 @@ __global__ __launch_bounds__(GEN_NT) void residual_kernel(const void* tl, int64_
   const int b = blockIdx.x;
   const int j = first_rej[b];
   if (j >= k) return;
+  S.nth = GEN_NT;  // (every thread stores the same value before its first use)
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
   const void* trow = reinterpret_cast<const char*>(tl) + ES * ((int64_t)b * tsb + (int64_t)j * tsk);
   const void* drow = reinterpret_cast<const char*>(dl) + ES * ((int64_t)b * dsb + (int64_t)j * dsk);
@@ -126,8 +127,8 @@ __global__ __launch_bounds__(GEN_NT) void residual_kernel(const void* tl, int64_
     uint32_t nt = 0, nd = 0;
     if (i0 < V) { nt = ties(i0, trow, pt); nd = ties(i0, drow, pd); }
     uint32_t tt, td;
-    const uint32_t et = gblock_excl_scan<uint32_t>(nt, &tt, S.red32);
-    const uint32_t ed = gblock_excl_scan<uint32_t>(nd, &td, S.red32);
+    const uint32_t et = gblock_excl_scan<uint32_t>(nt, &tt, S.red32, GEN_NT);
+    const uint32_t ed = gblock_excl_scan<uint32_t>(nd, &td, S.red32, GEN_NT);
     if (i0 < V) {
       double rr[VEC];
       tot += tile_res(i0, trun + et, drun + ed, rr);
@@ -153,13 +154,13 @@ __global__ __launch_bounds__(GEN_NT) void residual_kernel(const void* tl, int64_
     uint32_t nt = 0, nd = 0;
     if (i0 < V) { nt = ties(i0, trow, pt); nd = ties(i0, drow, pd); }
     uint32_t tt, td;
-    const uint32_t et = gblock_excl_scan<uint32_t>(nt, &tt, S.red32);
-    const uint32_t ed = gblock_excl_scan<uint32_t>(nd, &td, S.red32);
+    const uint32_t et = gblock_excl_scan<uint32_t>(nt, &tt, S.red32, GEN_NT);
+    const uint32_t ed = gblock_excl_scan<uint32_t>(nd, &td, S.red32, GEN_NT);
     double rr[VEC];
     double s = 0.0;
     if (i0 < V) s = tile_res(i0, trun + et, drun + ed, rr);
     double btot;
-    const double bex = gblock_excl_scan<double>(s, &btot, S.redd);
+    const double bex = gblock_excl_scan<double>(s, &btot, S.redd, GEN_NT);
     if (i0 < V && s > 0.0 && run + bex <= target && target < run + bex + s) {
       double a = run + bex;
 #pragma unroll

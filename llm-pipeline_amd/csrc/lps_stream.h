@@ -53,8 +53,10 @@
 // Rows the kernel cannot finish exactly (a wave segment overflow, a pool past
 // capacity, more than HLIST distinct history ids or a count past HCMAX) are
 // marked LPS_ROW_DEFERRED for the general kernel, which counts histories of
-// any size.  Nucleus, pure and deferred-mode
-// rows are left to the row-group kernel, or deferred when it is not launched.
+// any size.  (Calling the general algorithm from this kernel, even as a
+// separate function, costs the stream ~110 spilled VGPRs under its 128-VGPR
+// budget.)  Nucleus, pure and deferred-mode rows are left to the row-group
+// kernel, or deferred when it is not launched.
 #pragma once
 
 #include "lps_rowgroup.h"
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   // per-slot constants are not hoisted into registers for the whole loop)
   auto vid = [&](int h, int s) {
     int b = lane * VPE;
-    __asm__ volatile("" : "+v"(b));
+    LPS_KEEP_VGPR(b);
     return b + h * CV * VPE + (s / VPE) * 64 * VPE + (s % VPE);
   };
 

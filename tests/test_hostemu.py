@@ -1,0 +1,174 @@
+"""The kernels' index math under host sanitizers (CPU, no GPU).
+
+``tests/hostemu`` compiles the unchanged C ABI and kernels
+(``llm-pipeline_amd/csrc/lps.hip``) for x86 with clang, over a host emulation
+of the HIP subset they use, with AddressSanitizer and UndefinedBehaviorSanitizer
+(array bounds included).  Every LDS array is a bounds-checked array, every
+input and output is its own heap allocation of exactly its size, and the
+workspace is allocated at ``lps_workspace_bytes``.  A run that reads or writes
+out of bounds stops with the sanitizer's report; a run that finishes must also
+match the CPU oracle row by row (the same bar as the GPU parity tests).
+
+The emulation runs a launch's blocks one at a time, so it covers launches
+whose blocks never wait for one another: row-group plans of one chunk per row
+(these include the 16-bit V = 64 rows of ``test_small_vocab_mixed_params``),
+and the general kernel.
+"""
+
+import hashlib
+import os
+import shutil
+import struct
+import subprocess
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from tests import parity as PY
+from tests import workloads as W
+from tests.test_gpu_parity import _small
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+EMU = os.path.join(HERE, "hostemu")
+BUILD = os.path.join(EMU, "_build")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+SOURCES = [os.path.join(EMU, "run_case.cpp"), os.path.join(EMU, "shim", "hip", "hip_runtime.h"),
+           os.path.join(REPO, "include", "lps.h")]
+CSRC = os.path.join(REPO, "llm-pipeline_amd", "csrc")
+
+DT = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def _sources():
+    files = list(SOURCES) + sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".h", ".hip")))
+    h = hashlib.sha256()
+    for p in files:
+        h.update(open(p, "rb").read())
+    return h.hexdigest()[:16]
+
+
+@pytest.fixture(scope="session")
+def run_case():
+    if not os.path.exists(CLANG):
+        pytest.skip("no ROCm clang++ for the host build")
+    os.makedirs(BUILD, exist_ok=True)
+    exe = os.path.join(BUILD, f"run_case_{_sources()}")
+    if not os.path.exists(exe):
+        for old in os.listdir(BUILD):
+            if old.startswith("run_case_"):
+                os.remove(os.path.join(BUILD, old))
+        cmd = [CLANG, "-std=c++20", "-O0", "-g1", "-ffp-contract=off",
+               "-fsanitize=address,undefined", "-fsanitize=bounds", "-fno-sanitize-recover=all",
+               "-I", os.path.join(EMU, "shim"), "-I", os.path.join(REPO, "include"), "-I", CSRC,
+               "-x", "c++", os.path.join(EMU, "run_case.cpp"), "-o", exe + ".tmp", "-lpthread"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-4000:]
+        shutil.move(exe + ".tmp", exe)
+    return exe
+
+
+def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0):
+    """One lps_sample call of workload w under the sanitizers; its outputs as a
+    SampleOutput-like namespace of CPU tensors."""
+    B, V = w.B, w.V
+    H = 0 if w.histories is None else int(w.histories.shape[1])
+    inp, out = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        f.write(struct.pack("<16i", 0x4C505345, DT[w.logits.dtype], B, V, H, n_top, flags, int(workspace),
+                            int(logprobs), 0, 0, 0, 0, 0, 0, 0))
+        f.write(w.logits.contiguous().view(torch.int16 if w.logits.dtype != torch.float32 else torch.int32)
+                .numpy().tobytes())
+        for a, dt in ((w.temperature, np.float32), (w.top_k, np.int32), (w.top_p, np.float32),
+                      (w.min_p, np.float32), (w.typical_p, np.float32), (w.rep, np.float32),
+                      (w.pres, np.float32), (w.freq, np.float32)):
+            f.write(a.numpy().astype(dt).tobytes())
+        if H:
+            f.write(w.histories.numpy().astype(np.int32).tobytes())
+            f.write(w.hist_len.numpy().astype(np.int32).tobytes())
+        f.write(w.uniforms.numpy().astype(np.float32).tobytes())
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    r = subprocess.run([exe, str(inp), str(out)], capture_output=True, text=True, timeout=600, env=env)
+    assert r.returncode == 0, f"host run failed ({r.returncode}):\n{r.stderr[-6000:]}"
+    b = open(out, "rb").read()
+    o = 0
+
+    def take(dt, n):
+        nonlocal o
+        a = np.frombuffer(b, dtype=dt, count=n, offset=o).copy()
+        o += a.nbytes
+        return torch.from_numpy(a)
+
+    res = SimpleNamespace()
+    res.tokens = take(np.int64, B)
+    res.status = take(np.int32, B)
+    res.kept_cut = take(np.float32, B)
+    res.kept_ties = take(np.int32, B)
+    res.kept_count = take(np.int32, B)
+    res.row_path = take(np.int32, B)
+    res.chosen_logprob = take(np.float32, B) if logprobs else None
+    res.top_logprobs = take(np.float32, B * n_top).reshape(B, n_top) if n_top else None
+    res.top_ids = take(np.int64, B * n_top).reshape(B, n_top) if n_top else None
+    assert o == len(b)
+    return res
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_v64_mixed_params(run_case, tmp_path, dtype):
+    """The inputs of test_small_vocab_mixed_params at V = 64 (16-byte vector
+    rows, one chunk): the row-group kernel at G = 1, then the general kernel on
+    the rows it defers (top_k beyond V, top_p <= 0, T < 1e-4 ...).  In bounds,
+    and equal to the oracle."""
+    w = _small(64, 24, dtype, seed=64 + int(dtype == torch.bfloat16) * 7)
+    out = _run(run_case, w, tmp_path)
+    PY.check_rows(w, out)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_v64_general_algorithm_in_the_launch(run_case, tmp_path, dtype):
+    """16-bit V = 64 rows the row-group kernel defers in its chunk phase (min-p
+    and typical-p without top-k, top_k past 256) or finishes itself, in one
+    launch: the deferred rows are sampled by the general algorithm in their
+    tail workgroups (512 threads, 16-byte vector loads)."""
+    w = _small(64, 24, dtype, seed=71)
+    i = torch.arange(24)
+    w.top_k = torch.where(i % 4 == 1, torch.tensor(300, dtype=torch.int32), w.top_k)
+    w.min_p = torch.where(i % 4 == 2, torch.tensor(0.05), w.min_p)
+    w.typical_p = torch.where(i % 4 == 3, torch.tensor(0.8), w.typical_p)
+    w.top_k = torch.where(i % 4 >= 2, torch.tensor(0, dtype=torch.int32), w.top_k)
+    w.temperature = torch.where(i % 4 != 0, torch.tensor(0.9), w.temperature)
+    out = _run(run_case, w, tmp_path)
+    assert (out.row_path[i % 4 != 0] == 1).all() and (out.row_path[i % 4 == 0] == 0).all()
+    PY.check_rows(w, out)
+
+
+@pytest.mark.parametrize("V", [7, 1000, 4099])
+def test_small_vocab_scalar_rows(run_case, tmp_path, V):
+    """Rows read element by element (V % 8 != 0) and a ragged vector row."""
+    w = _small(V, 16, torch.bfloat16, seed=V + 7)
+    PY.check_rows(w, _run(run_case, w, tmp_path))
+
+
+def test_general_kernel_only(run_case, tmp_path):
+    """LPS_FLAG_GENERIC: the general kernel for every row, with penalties over
+    histories that span several count windows (V = 20000 > 8192 ids)."""
+    w = _small(20000, 8, torch.float32, seed=5)
+    rng = np.random.default_rng(5)
+    w.histories = torch.from_numpy(rng.integers(-5, 20005, size=(8, 600)).astype(np.int32))
+    w.hist_len = torch.tensor([0, 1, 17, 600, 599, 300, 600, 5], dtype=torch.int32)
+    out = _run(run_case, w, tmp_path, flags=1, workspace=False)
+    assert (out.row_path == 1).all()
+    PY.check_rows(w, out)
+
+
+def test_logprobs_one_chunk(run_case, tmp_path):
+    """Chosen and top-N logprobs on one-chunk rows (row-group kernel), and on
+    rows it defers (general kernel)."""
+    w = _small(2048, 12, torch.float16, seed=9)
+    w.n_top = 8
+    w.logprobs = True
+    out = _run(run_case, w, tmp_path, logprobs=True, n_top=8)
+    PY.check_rows(w, out, lp=True)
