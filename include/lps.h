@@ -65,9 +65,7 @@ enum {
   LPS_ROW_OK = 0,
   LPS_ROW_NONFINITE = 1,       /* NaN or +inf in the scaled logits of a sampling row */
   LPS_ROW_EMPTY = 2,           /* every logit is -inf on a sampling row               */
-  LPS_ROW_HISTORY_OVERFLOW = 4, /* never set since ABI version 2 (kept for callers that test it) */
-  LPS_ROW_INTERNAL = 16        /* the launch could not finish the row (a bounded in-kernel wait
-                                * ran out; not reached while every workgroup of the launch runs) */
+  LPS_ROW_HISTORY_OVERFLOW = 4 /* never set since ABI version 2 (kept for callers that test it) */
 };
 
 /* Largest top-N logprob count per row. */

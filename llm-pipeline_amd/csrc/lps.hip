@@ -143,11 +143,7 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   // batches of more than one resident round of chunk workgroups: greedy and
   // top-k rows stream through one workgroup each (stream_kernel), the
   // row-group kernel takes the others; the row-kind hints skip a kernel no row
-  // needs (a row the hint misjudges is deferred to the general algorithm).
-  // Rows either kernel cannot finish exactly are sampled by the general
-  // algorithm: when the row-group kernel alone runs one resident round, in
-  // the row's tail workgroup (grid = the chunk grid, then one per row); else
-  // by the general kernel launched after them.
+  // needs (a row the hint misjudges is deferred to the general kernel)
   bool big = false;
   if constexpr (VPE > 1) big = grid > (unsigned)device_cus() && F.k.V <= rg::STREAM_VMAX;
   const bool run_stream = big && !(flags & LPS_FLAG_ROWS_NUCLEUS);
@@ -162,15 +158,11 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
       F.skip_topk = 1;
     }
   }
-  F.main_grid = (int)grid;  // (a multiple of 8: row r's tail runs on the row's XCD)
-  F.tails = (run_rg && !run_stream && grid <= (unsigned)device_cus()) ? 1 : 0;
   if (run_rg) {
-    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid + (F.tails ? (unsigned)F.k.R : 0u)),
-                       dim3(rg::NT), 0, s, F);
+    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (F.tails) return hipSuccess;
   // the rows the fast kernels deferred: the general algorithm, one
   // 1024-thread workgroup per row (the others return at once)
   KParams G = F.k;

@@ -93,12 +93,9 @@ __device__ __forceinline__ const uint8_t* row_allowed(const KParams& P, int r) {
 __device__ __forceinline__ bool id_allowed(const uint8_t* am, int64_t i) {
   return !am || ((am[i >> 3] >> (i & 7)) & 1u);
 }
-// Workspace row status bits (beside the LPS_ROW_* bits): the fast kernels
-// deferred the row to the general kernel's launch (LPS_ROW_DEFERRED), or
-// sampled it with the general algorithm in their own launch (LPS_ROW_GENERAL);
-// the reason code is in bits 8 and up.
+// Workspace row status bit (beside the LPS_ROW_* bits): the fast kernels
+// deferred the row to the general kernel (the reason code in bits 8 and up).
 constexpr int32_t LPS_ROW_DEFERRED = 8;
-constexpr int32_t LPS_ROW_GENERAL = 64;
 
 struct GenShared {
   alignas(16) uint32_t wcnt[GEN_WIN];  // history counts of the ids [w0, w0 + GEN_WIN) of the loaded window

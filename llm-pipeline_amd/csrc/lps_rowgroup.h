@@ -47,13 +47,11 @@
 //
 // A row the kernel cannot finish exactly (e.g. a flat row whose regions hold
 // more candidates than the lists take, min-p / typical-p without top-k,
-// entropy requested) is sampled by the general algorithm.  A launch of one
-// resident round (grid <= CUs) ends with one tail workgroup per row (on the
-// row's XCD), which waits for the row's decision word and runs the general
-// algorithm when the row was deferred (LPS_ROW_GENERAL in the workspace
-// status); a larger launch marks the row LPS_ROW_DEFERRED and is followed by
-// the general kernel with that status as its filter (tail workgroups there
-// would form a round of their own).
+// entropy requested) is marked LPS_ROW_DEFERRED in the workspace status and
+// sampled by the general kernel, launched after this one with that status as
+// its filter.  (Sampling such rows in the same launch, in one tail workgroup
+// per row, was measured: the tail code in the kernel made every launch slower,
+// also those that never ran a tail.)
 //
 // Cross-workgroup handoffs (the histogram barrier and the arrival count):
 // every thread of the publishing workgroup stores, then waits for its stores
@@ -162,9 +160,7 @@ __device__ __forceinline__ uint64_t rg_tag(uint32_t epoch, int r, uint32_t xcc) 
 }
 constexpr int CTR_ARRIVE = 0;  // counter words of a row (32 per row): arrivals,
 constexpr int CTR_HIST = 2;    // the histogram barrier,
-constexpr int CTR_EPOCH = 4;   // the row's launch epoch (never reset),
-constexpr int CTR_DECIDE = 6;  // and its decision for the tail workgroup (DEC_*; the tail resets it)
-enum { DEC_NONE = 0, DEC_DONE = 1, DEC_GENERAL = 2 };
+constexpr int CTR_EPOCH = 4;   // and the row's launch epoch (never reset)
 
 struct RgParams {
   KParams k;
@@ -175,10 +171,7 @@ struct RgParams {
   int nvec;            // vectors per row
   int heavy_first;     // dispatch rows without top-k first
   int skip_topk;       // the streaming kernel's rows (stream_takes) ran there: skip them
-  int stream_only;     // the row-group kernel is not launched: the streaming kernel samples the others
-                       // with the general algorithm
-  int main_grid;       // workgroups of the chunk grid; workgroup main_grid + r is row r's tail
-  int tails;           // the grid ends with the tail workgroups (else the general kernel follows)
+  int stream_only;     // the row-group kernel is not launched: the streaming kernel defers the others
   uint32_t* counters;  // [R * 32]: arrivals and the histogram barrier (zero between launches), the
                        // row's launch epoch (CTR_*)
   int32_t* status;     // [R]
@@ -325,14 +318,21 @@ struct RgLists {
   uint32_t cx[2][CLMAX];
   int32_t scnt[2][NW];               // segment counts (SEGCAP + 1: overflowed)
 };
+// Words of the count table region: the chunk's 16-bit counts, and at least
+// the lists' size, so that the lists (which overlay it) end before the
+// histogram, which is read while the lists fill.
+template <int NE>
+constexpr int hc_words() {
+  return NT * NE / 2 > (int)(sizeof(RgLists) + 3) / 4 ? NT * NE / 2 : (int)((sizeof(RgLists) + 15) / 16 * 4);
+}
 template <int NE>
 struct RgChunkS : RgX {
   union {
     struct {
-      uint32_t hc[NT * NE / 2];             // 16-bit history counts of the chunk's ids
+      uint32_t hc[hc_words<NE>()];          // 16-bit history counts of the chunk's ids
       unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
     } a;
-    RgLists l;                               // after the counts and the histogram are used
+    RgLists l;                               // after the counts are used
   };
 };
 struct RgFinalS : RgX {
@@ -347,7 +347,6 @@ template <int NE>
 union RgShared {
   RgChunkS<NE> c;
   RgFinalS f;
-  GenShared g;  // a tail workgroup running the general algorithm
 };
 
 // ---------------------------------------------------------------------------

@@ -258,11 +258,15 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     double msum = 0.0;
 #pragma unroll
     for (int i = 0; i < HPT; i++) msum += mrg[i];
-    // region bounds are collected with LDS atomics by the few threads whose
-    // bins meet a target (cleared here, before the scan's barrier)
+    // region bounds, and the cumulative mass at each end of region 1, are
+    // collected with LDS atomics by the few threads whose bins meet a target
+    // (cleared here, before the scan's barrier); the masses are non-negative
+    // doubles, whose bit patterns order as they do
     if (tid == 0) {
       S.mi[0] = 1 << 30; S.mi[1] = -1; S.mi[2] = 1 << 30; S.mi[3] = -1;
       S.u3[0] = 0u;
+      S.mq[0] = ~0ull;
+      S.mq[1] = 0ull;
     }
     double stot;
     const double sx = bscan<NW, double>(msum, &stot, S.d2);
@@ -271,39 +275,37 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const bool nuc = mode == MODE_NUCLEUS;
     const double Pm = nuc ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
     if (nuc) {
+      // region 1: its highest bin holds the least prefix a, its lowest the
+      // largest end a + m (cumulative mass at its top and bottom: the kept
+      // mass lies between them, and the draw at u times it)
       int lo = 1 << 30, hi = -1;
+      uint64_t atop = ~0ull, abot = 0ull;
       double a = sx;
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
         const int b = HB - 1 - HPT * tid - i;
-        if (mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) { lo = min(lo, b); hi = max(hi, b); }
+        if (mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) {
+          lo = min(lo, b);
+          hi = max(hi, b);
+          atop = min(atop, __builtin_bit_cast(uint64_t, a));
+          abot = max(abot, __builtin_bit_cast(uint64_t, a + mrg[i]));
+        }
         a += mrg[i];
       }
       if (hi >= 0) {
         atomicMin(&S.mi[0], lo);
         atomicMax(&S.mi[1], hi);
+        atomicMin(reinterpret_cast<unsigned long long*>(&S.mq[0]), (unsigned long long)atop);
+        atomicMax(reinterpret_cast<unsigned long long*>(&S.mq[1]), (unsigned long long)abot);
       }
     }
     __syncthreads();
     const int lo1 = nuc ? S.mi[0] : (1 << 30);
     const int hi1 = nuc ? S.mi[1] : (1 << 30);
-    // cumulative mass at the top of region 1 and at its bottom: the kept mass
-    // lies between them, and the draw at u times it
-    if (nuc && hi1 >= 0) {
-      double a = sx;
-#pragma unroll
-      for (int i = 0; i < HPT; i++) {
-        const int b = HB - 1 - HPT * tid - i;
-        if (b == hi1) S.md[1] = a;
-        if (b == lo1) S.md[2] = a + mrg[i];
-        a += mrg[i];
-      }
-    }
-    __syncthreads();
     if (nuc && hi1 < 0) flags |= RF_REGION;
     const float u = fminf(fmaxf(g.u == g.u ? g.u : 0.0f, 0.0f), 0.99999994f);
-    const double t_lo = (nuc ? (double)u * S.md[1] : (double)u * Z) - eps;
-    const double t_hi = (nuc ? (double)u * S.md[2] : (double)u * Z) + eps;
+    const double t_lo = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[0]) : (double)u * Z) - eps;
+    const double t_hi = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[1]) : (double)u * Z) + eps;
     {
       int lo = 1 << 30, hi = -1;
       uint32_t nest = 0;  // elements in either region (an upper estimate: bin mass / the bin's least mass)
@@ -340,25 +342,25 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const int dl = Mfin && rfin ? (int)(R - ref) : 0;
     auto own = [&](int b) { return b >= (1 << 30) ? b : b + HOCT * dl; };
     const int l1 = own(sm.reg[0]), h1 = own(sm.reg[1]), l2 = own(sm.reg[2]), h2 = own(sm.reg[3]);
-    double ab1 = 0.0, ab2 = 0.0;
-    uint32_t nab = 0;
+    {
+      // (per-wave sums, added up by the publishing thread after the barriers
+      // of the candidate lists; the lists do not overlap the histogram)
+      double ab1 = 0.0, ab2 = 0.0;
+      uint32_t nab = 0;
 #pragma unroll
-    for (int i = 0; i < HLT; i++) {
-      const int b = tid + NT * i;
-      const unsigned long long a = S.a.hist[b];
-      const double m = b == HB_NAN ? 0.0 : bin_mass_u(b, a);
-      if (b > h1 && b != HB_NAN) { ab1 += m; nab += (uint32_t)(a >> 48); }
-      if (b > h2) ab2 += m;
+      for (int i = 0; i < HLT; i++) {
+        const int b = tid + NT * i;
+        const unsigned long long a = S.a.hist[b];
+        const double m = b == HB_NAN ? 0.0 : bin_mass_u(b, a);
+        if (b > h1 && b != HB_NAN) { ab1 += m; nab += (uint32_t)(a >> 48); }
+        if (b > h2) ab2 += m;
+      }
+      RG_STAMP(11);
+      ab1 = wreduce(ab1, OpAdd{});
+      ab2 = wreduce(ab2, OpAdd{});
+      nab = wreduce(nab, OpAdd{});
+      if (lane == 0) { S.d4[wv] = ab1; S.d5[wv] = ab2; S.u4[wv] = nab; }
     }
-    RG_STAMP(11);
-    ab1 = wreduce(ab1, OpAdd{});
-    ab2 = wreduce(ab2, OpAdd{});
-    nab = wreduce(nab, OpAdd{});
-    if (lane == 0) { S.d4[wv] = ab1; S.d5[wv] = ab2; S.u4[wv] = nab; }
-    __syncthreads();
-    sm.ab1 = 0.0; sm.ab2 = 0.0; sm.nab1 = 0;
-#pragma unroll
-    for (int i = 0; i < NW; i++) { sm.ab1 += S.d4[i]; sm.ab2 += S.d5[i]; sm.nab1 += S.u4[i]; }
     // the elements of either region: list 0 (region 1, nucleus rows) and
     // list 1 (region 2, unless the draw is skipped), tested on bin pairs
     static_assert(NE % 2 == 0, "bin pairs");
@@ -387,6 +389,9 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     if (!sort_publish(S.l, S, 2, 0, false, T, cbase, F.capw, np)) flags |= RF_OVERFLOW;
     sm.n1 = (uint16_t)np[0];
     sm.n2 = (uint16_t)np[1];
+    sm.ab1 = 0.0; sm.ab2 = 0.0; sm.nab1 = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) { sm.ab1 += S.d4[i]; sm.ab2 += S.d5[i]; sm.nab1 += S.u4[i]; }
   }
 
   // ---- the chunk's summary, then the arrival count ----
@@ -1114,59 +1119,12 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   return 0;
 }
 
-// The row's decision for its tail workgroup (one thread; an agent-scope
-// atomic, coherent whichever XCD the tail runs on).
-__device__ __forceinline__ void decide(const RgParams& F, int r, uint32_t d) {
-  __hip_atomic_store(F.counters + (int64_t)r * 32 + CTR_DECIDE, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Tail workgroup of row r: waits for the row's decision (a bounded wait; the
-// chunk workgroups it waits for were all dispatched before it), resets the
-// word for the next launch, and samples the row with the general algorithm
-// on all NT threads when the row was deferred.
-template <int DT, int VPE>
-__device__ __forceinline__ void tail_block(const RgParams& F, GenShared& S, const int r) {
-  if (r >= F.k.R) return;
-  if (F.skip_topk && stream_takes(row_cfg(F.k, r))) return;  // the streaming kernel's row
-  uint32_t* dw = F.counters + (int64_t)r * 32 + CTR_DECIDE;
-  if (threadIdx.x == 0) {
-    uint32_t d = DEC_NONE;
-    for (int spins = 0; spins < (1 << 22); spins++) {
-      d = ld_agent(dw);
-      if (d != DEC_NONE) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    __hip_atomic_store(dw, (uint32_t)DEC_NONE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S.misc[7] = (int)d;
-  }
-  __syncthreads();
-  const int d = S.misc[7];
-  __syncthreads();
-  if (d == DEC_NONE) {  // no decision in time (not reached while chunk groups run to the end)
-    if (threadIdx.x == 0) {
-      F.k.tokens[r] = -1;
-      if (F.k.row_status) F.k.row_status[r] = LPS_ROW_INTERNAL;
-    }
-    return;
-  }
-  if (d != DEC_GENERAL) return;
-  KParams P = F.k;
-  P.plans = nullptr;
-  P.only_status = nullptr;
-  gen_row<DT, VPE>(P, r, S, NT);
-}
-
 // ===========================================================================
-// The kernel: grid of ceil(R / 8) * 8 * G chunk workgroups of NT threads,
-// then R tail workgroups.
+// The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
 // ===========================================================================
 template <int DT, int VPE, int NE>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;
-  if ((int)blockIdx.x >= F.main_grid) {
-    tail_block<DT, VPE>(F, SU.g, (int)blockIdx.x - F.main_grid);
-    return;
-  }
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   int r = (slot / F.G) * 8 + xcd;
   const int j = slot % F.G;
@@ -1180,10 +1138,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
   const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g, epoch);
   if (mode == MODE_DEFER) {
-    if (j == 0 && threadIdx.x == 0) {
-      F.status[r] = (F.tails ? LPS_ROW_GENERAL : LPS_ROW_DEFERRED) | (1 << 8);
-      if (F.tails) decide(F, r, DEC_GENERAL);
-    }
+    if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
   }
   // arrival: the chunk's stores are visible at agent scope before it is counted
@@ -1201,10 +1156,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   RG_STAMP(24);
   const int reason = final_phase<DT, VPE>(F, SU.f, r, g, epoch);
   RG_STAMP(31);
-  if (threadIdx.x == 0) {
-    if (reason > 0) F.status[r] = (F.tails ? LPS_ROW_GENERAL : LPS_ROW_DEFERRED) | (reason << 8);
-    if (F.tails) decide(F, r, reason > 0 ? DEC_GENERAL : DEC_DONE);
-  }
+  if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }
 
 }  // namespace rg

@@ -30,7 +30,6 @@ LPS_DTYPE_F16 = 2
 LPS_ROW_NONFINITE = 1
 LPS_ROW_EMPTY = 2
 LPS_ROW_HISTORY_OVERFLOW = 4   # never set since ABI version 2 (histories of any size)
-LPS_ROW_INTERNAL = 16          # the launch could not finish the row
 LPS_ABI_VERSION = 2
 
 LPS_MAX_TOP_LOGPROBS = 64

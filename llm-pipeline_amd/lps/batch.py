@@ -329,6 +329,4 @@ def raise_on_status(status: torch.Tensor) -> None:
     bad = int(status.ne(0).any().item())
     if not bad:
         return
-    if int((status & _lib.LPS_ROW_INTERNAL).ne(0).any().item()):
-        raise RuntimeError("lps: a row was not finished by its launch (in-kernel wait ran out)")
     raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")

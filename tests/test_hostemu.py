@@ -128,11 +128,11 @@ def test_v64_mixed_params(run_case, tmp_path, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_v64_general_algorithm_in_the_launch(run_case, tmp_path, dtype):
+def test_v64_deferred_rows(run_case, tmp_path, dtype):
     """16-bit V = 64 rows the row-group kernel defers in its chunk phase (min-p
-    and typical-p without top-k, top_k past 256) or finishes itself, in one
-    launch: the deferred rows are sampled by the general algorithm in their
-    tail workgroups (512 threads, 16-byte vector loads)."""
+    and typical-p without top-k, top_k past 256) or finishes itself: the
+    deferred rows are sampled by the general kernel launched after it (16-byte
+    vector loads), the others by the row-group kernel."""
     w = _small(64, 24, dtype, seed=71)
     i = torch.arange(24)
     w.top_k = torch.where(i % 4 == 1, torch.tensor(300, dtype=torch.int32), w.top_k)
