@@ -227,6 +227,15 @@ int lps_version(void);
 /* Human-readable name of a return code. */
 const char* lps_status_string(int code);
 
+/* Device self-test (no counterpart in the reference): counts the steps over
+ * every non-NaN fp32 input, in increasing order, where the GPU's hardware
+ * exp2 (v_exp_f32) decreases.  The row-group kernel locates a histogram
+ * region's logits by a search over x that assumes exp2 is non-decreasing
+ * (exp2(fma(x, c, -ref)) is then non-decreasing in x), so *violations must be
+ * 0 on the device it runs on.  Synchronous on the current device (allocates
+ * 8 bytes); a few milliseconds. */
+int lps_selftest_exp2_monotone(unsigned long long* violations);
+
 /* Scratch bytes lps_sample needs for num_rows rows of vocab V. */
 size_t lps_workspace_bytes(int num_rows, int vocab, int flags);
 

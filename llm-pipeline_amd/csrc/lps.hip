@@ -60,6 +60,7 @@ struct RgWs {
   int32_t* status;
   rg::RgSum* sums;
   float* hist;
+  float* fine;
   uint4* cands;
   size_t bytes;
 };
@@ -116,6 +117,7 @@ RgWs rg_layout(void* base, int R, int V) {
   w.status = ws_at<int32_t>(base, off); off = round_up(off + (size_t)R * 4, 256);
   w.sums = ws_at<rg::RgSum>(base, off); off = round_up(off + (size_t)R * 2 * rg::MAXG * sizeof(rg::RgSum), 256);
   w.hist = ws_at<float>(base, off); off = round_up(off + (size_t)R * G * rg::HPUB * 4, 256);
+  w.fine = ws_at<float>(base, off); off = round_up(off + (size_t)R * G * rg::FHN * 4, 256);
   w.cands = ws_at<uint4>(base, off); off = round_up(off + (size_t)R * rg::CAPR * 16, 256);
   w.bytes = off;
   return w;
@@ -248,6 +250,7 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
   F.status = w.status;
   F.sums = w.sums;
   F.hist = w.hist;
+  F.fine = w.fine;
   F.cands = w.cands;
   F.capw = p.capw;
   switch (dtype) {
@@ -352,9 +355,45 @@ hipError_t launch_softmax_reg(const SoftmaxParams& S, const SmPlan& p, hipStream
   return hipGetLastError();
 }
 
+// Monotonicity of the hardware exp2 (v_exp_f32) over every non-NaN input:
+// thread t checks keys [k0 + 1024 t - 1, k0 + 1024 t + 1024) in float-key
+// order (each step against the one before it), counting the steps where the
+// result decreases.
+constexpr uint32_t kKeyNegInf = 0x007FFFFFu, kKeyPosInf = 0xFF800000u;
+__global__ __launch_bounds__(256) void exp2_monotone_kernel(unsigned long long* bad) {
+  const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  const uint64_t k0 = kKeyNegInf + t * 1024u;
+  if (k0 > kKeyPosInf) return;
+  const uint64_t k1 = k0 + 1024u < (uint64_t)kKeyPosInf + 1u ? k0 + 1024u : (uint64_t)kKeyPosInf + 1u;
+  uint32_t n = 0;
+  float prev = __builtin_amdgcn_exp2f(key2f((uint32_t)(k0 > kKeyNegInf ? k0 - 1u : k0)));
+  for (uint64_t k = k0; k < k1; k++) {
+    const float r = __builtin_amdgcn_exp2f(key2f((uint32_t)k));
+    n += r < prev ? 1u : 0u;
+    prev = r;
+  }
+  if (n) atomicAdd(bad, (unsigned long long)n);
+}
+
 }  // namespace
 
 extern "C" {
+
+int lps_selftest_exp2_monotone(unsigned long long* violations) {
+  if (!violations) return LPS_EINVAL;
+  unsigned long long* d = nullptr;
+  if (hipMalloc(&d, sizeof(*d)) != hipSuccess) return LPS_ELAUNCH;
+  hipError_t e = hipMemset(d, 0, sizeof(*d));
+  const uint64_t nkeys = (uint64_t)kKeyPosInf - kKeyNegInf + 1u;
+  const uint32_t blocks = (uint32_t)((nkeys + 256u * 1024u - 1u) / (256u * 1024u));
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(exp2_monotone_kernel, dim3(blocks), dim3(256), 0, 0, d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(violations, d, sizeof(*d), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  return e == hipSuccess ? LPS_OK : LPS_ELAUNCH;
+}
 
 #ifdef LPS_RG_STAMPS
 // Timing builds only: copies the phase stamps of the last launches (8192 x 32

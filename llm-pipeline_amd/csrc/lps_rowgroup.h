@@ -30,7 +30,11 @@
 //            top-p cut (cumulative mass p * Z from the top) and the bins
 //            holding the draw (u times the kept mass).  Elements in either
 //            region are candidates (one list per region), with the exact mass
-//            above each region.
+//            above each region.  Regions too crowded for the lists (flat
+//            rows: thousands of logits in one bin) take a second level: each
+//            chunk bins its elements of the (at most RW) region bins by the
+//            next 8 mantissa bits, exactly as above; after a second barrier
+//            the fine bins are merged and the regions located among them.
 // Candidates are gathered in LDS (per-wave segments filled by ballots), sorted
 // in the chunk by (z = fl(x / T) descending, index ascending) with a rank sort,
 // and published sorted; a top-k list stops after its k'-th entry and the
@@ -45,8 +49,8 @@
 // CDF in sorted order: kept ids by scaled logit descending, ties lower index
 // first.
 //
-// A row the kernel cannot finish exactly (e.g. a flat row whose regions hold
-// more candidates than the lists take, min-p / typical-p without top-k,
+// A row the kernel cannot finish exactly (e.g. a region wider than RW bins
+// holding more candidates than the lists take, min-p / typical-p without top-k,
 // entropy requested) is marked LPS_ROW_DEFERRED in the workspace status and
 // sampled by the general kernel, launched after this one with that status as
 // its filter.  (Sampling such rows in the same launch, in one tail workgroup
@@ -104,6 +108,9 @@ constexpr int HPUB = HB;           // published bins
 constexpr uint32_t BELOW = 0xFFFFu;  // "bin" of masses under the histogram (summed apart)
 constexpr int HE0 = 96;            // float exponent of bin 0: masses from 2^-31
 constexpr int MAXG = 16;           // chunks per row
+constexpr int RW = 2;              // second level: bins of one region it refines
+constexpr int FSUB = 256;          // second level: fine bins per bin (8 more mantissa bits)
+constexpr int FHN = 2 * RW * FSUB; // second level: fine bins of a chunk (region 1, then region 2)
 constexpr int CAPR = 2048;         // published list entries per row (all chunks, both lists)
 constexpr int FT = 256;            // finaliser threads (waves 0-3, one per SIMD; the others leave)
 constexpr int FW = FT / 64;        // finaliser waves
@@ -130,6 +137,7 @@ enum {
   RF_HISTORY = 2,     // a history count does not fit 16 bits
   RF_SPLIT = 4,       // a chunk summary is not this launch's, or its chunk ran on another XCD
   RF_REGION = 8,      // no usable cut / draw region, or the barrier timed out
+  RF_WIDE = 16,       // a crowded region wider than the second level takes (RW bins)
 };
 
 // Per-chunk summary (published for the finaliser).
@@ -146,7 +154,8 @@ struct RgSum {
   double zsum;        // chunk mass: sum of exp2(fma(x, c, -ref))
   double ab1;         // nucleus: exact mass above region 1 (chunk reference)
   double ab2;         // nucleus: exact mass above region 2
-  int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row bins; the same in every chunk)
+  int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row fine bins, efine scale; the same
+                      // in every chunk)
 };
 static_assert(sizeof(RgSum) % 8 == 0 && offsetof(RgSum, tag) == 0, "8-byte words, the tag first");
 __device__ __forceinline__ void store_sum(RgSum* d, const RgSum& a) { *d = a; }
@@ -160,7 +169,8 @@ __device__ __forceinline__ uint64_t rg_tag(uint32_t epoch, int r, uint32_t xcc) 
 }
 constexpr int CTR_ARRIVE = 0;  // counter words of a row (32 per row): arrivals,
 constexpr int CTR_HIST = 2;    // the histogram barrier,
-constexpr int CTR_EPOCH = 4;   // and the row's launch epoch (never reset)
+constexpr int CTR_EPOCH = 4;   // the row's launch epoch (never reset),
+constexpr int CTR_FINE = 6;    // and the second-level barrier
 
 struct RgParams {
   KParams k;
@@ -177,6 +187,7 @@ struct RgParams {
   int32_t* status;     // [R]
   RgSum* sums;         // row r at sums + r * 2 * MAXG
   float* hist;         // row r at hist + r * G * HPUB
+  float* fine;         // second-level bins: row r at fine + r * G * FHN
   uint4* cands;        // row r at cands + r * CAPR: chunk j owns [j * capw, (j + 1) * capw): its
                        // sorted list 1, then its sorted list 2, entries {z key, index, x bits, 0}
   int capw;            // list entries per chunk
@@ -323,6 +334,7 @@ struct RgLists {
 // histogram, which is read while the lists fill.
 template <int NE>
 constexpr int hc_words() {
+  static_assert(sizeof(unsigned long long) * FHN <= sizeof(RgLists), "the fine bins end before the histogram");
   return NT * NE / 2 > (int)(sizeof(RgLists) + 3) / 4 ? NT * NE / 2 : (int)((sizeof(RgLists) + 15) / 16 * 4);
 }
 template <int NE>
@@ -333,6 +345,9 @@ struct RgChunkS : RgX {
       unsigned long long hist[HB + 64];     // count << 48 | sum of low 16 mantissa bits (+ spare slots)
     } a;
     RgLists l;                               // after the counts are used
+    // second level (nucleus rows, after the counts are used and before the
+    // lists fill): count << 48 | sum of low 8 mantissa bits
+    unsigned long long fh[FHN];
   };
 };
 struct RgFinalS : RgX {
@@ -494,6 +509,39 @@ __device__ __forceinline__ double bin_mass_u(int b, unsigned long long acc) {
   const uint32_t cnt = (uint32_t)(acc >> 48), low = (uint32_t)acc;
   const double m = __builtin_fma((double)(cnt * (128u + (uint32_t)(b & 127))), 65536.0, (double)low);
   return ldexp(m, (b >> 7) + HE0 - 150);
+}
+// Fine bin of a mass on the second level's scale: its exponent and top 15
+// mantissa bits, bin ebin(e) << 8 | the next 8 bits (negative under the
+// histogram; from HB_NAN << 8 for NaN / inf).
+__device__ __forceinline__ int efine(float e) { return (int)(__float_as_uint(e) >> 8) - (HE0 << 15); }
+// Exact mass of fine bin f from its accumulator (count << 48 | sum of the low
+// 8 mantissa bits; at most NT * 80 < 2^16 masses): 2^(E - 150) (count (2^15 +
+// top 15 bits) 2^8 + low).  0 for an empty bin, whatever f.
+__device__ __forceinline__ double fine_mass(int f, unsigned long long acc) {
+  const uint32_t cnt = (uint32_t)(acc >> 48), low = (uint32_t)acc;
+  const double m = __builtin_fma((double)(cnt * (uint32_t)(0x8000 + (f & 0x7FFF))), 256.0, (double)low);
+  return cnt ? ldexp(m, (f >> 15) + HE0 - 150) : 0.0;
+}
+// First float key k (in f2key order, over the non-NaN keys) whose logit
+// reaches fine bin thr: efine(emass(key2f(k), c, ref)) >= thr.  The hardware
+// exp2 is non-decreasing over every fp32 input (lps_selftest_exp2_monotone)
+// and fma(x, c, -ref) is non-decreasing in x for c > 0, so the predicate is
+// false then true over the keys; +inf's key satisfies it for thr < 2^22.  One
+// wave searches 64 keys per round (6 rounds); every lane of the wave calls it
+// with the same arguments.
+__device__ __forceinline__ uint32_t first_key_reaching(int thr, float c, float ref) {
+  constexpr uint32_t kNegInfK = 0x007FFFFFu, kPosInfK = 0xFF800000u;
+  const uint64_t l1 = (uint64_t)(threadIdx.x & 63) + 1u;
+  uint32_t lo = kNegInfK, hi = kPosInfK;  // the predicate fails at lo (unless thr is negative), holds at hi
+  while (hi - lo > 1u) {
+    const uint64_t span = hi - lo, step = (span + 63u) >> 6;
+    const uint32_t k = lo + (uint32_t)(l1 * step < span ? l1 * step : span);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(efine(emass(key2f(k), c, ref)) >= thr);
+    const uint64_t j = m ? (uint64_t)__builtin_ctzll(m) : 63u;
+    hi = lo + (uint32_t)((j + 1u) * step < span ? (j + 1u) * step : span);
+    lo = lo + (uint32_t)(j * step);
+  }
+  return hi;
 }
 // The smallest mass of bin b.
 __device__ __forceinline__ double bin_base(int b) {

@@ -62,6 +62,10 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     for (int i = 0; i < HB * 8 / 16 / NT; i++) h4[i * NT + tid] = u32x4{0u, 0u, 0u, 0u};
   }
   const float M = bred(tm, S.f, OpMax{});
+  if (hist_mode) {  // the second level's bins (over the counts, read until that barrier)
+    static_assert(FHN * 8 / 16 == NT, "one store per thread");
+    reinterpret_cast<u32x4*>(S.fh)[tid] = u32x4{0u, 0u, 0u, 0u};
+  }
   const bool Mfin = M != INFINITY && M != -INFINITY;
   const float ref = Mfin ? ceilf(__fmul_rn(M, c)) : (M == INFINITY ? INFINITY : -INFINITY);
 
@@ -235,7 +239,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
         for (int q = 0; q < 2; q++) {
           const int w = w0 + q;
           const float rw = w < G ? S.rf[w] : -INFINITY;
-          const int dl = (rw != -INFINITY) ? (int)(R - rw) : 4096;
+          const int dl = (rw != -INFINITY) ? (int)fminf(R - rw, 4096.0f) : 4096;
           // the chunk's published index of my lowest row bin
           const int src = HPUB - HPT - HPT * tid + HOCT * dl;
           sc[q] = dl < 1024 ? ldexp(1.0, -dl) : 0.0;
@@ -267,6 +271,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       S.u3[0] = 0u;
       S.mq[0] = ~0ull;
       S.mq[1] = 0ull;
+      S.mq[2] = ~0ull;
     }
     double stot;
     const double sx = bscan<NW, double>(msum, &stot, S.d2);
@@ -309,12 +314,17 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     {
       int lo = 1 << 30, hi = -1;
       uint32_t nest = 0;  // elements in either region (an upper estimate: bin mass / the bin's least mass)
+      uint64_t a2 = ~0ull;  // cumulative mass at region 2's top
       double a = sx;
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
         const int b = HB - 1 - HPT * tid - i;
         const bool in2 = mrg[i] > 0.0 && a <= t_hi && a + mrg[i] >= t_lo;
-        if (in2) { lo = min(lo, b); hi = max(hi, b); }
+        if (in2) {
+          lo = min(lo, b);
+          hi = max(hi, b);
+          a2 = min(a2, __builtin_bit_cast(uint64_t, a));
+        }
         if (in2 || (b >= lo1 && b <= hi1))
           nest += (uint32_t)ceilf(__fmul_rn((float)mrg[i], ldexpf(1.0f, 134 - ((b >> 7) + HE0))) /
                                   (float)(128 + (b & 127)));
@@ -323,6 +333,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       if (hi >= 0) {
         atomicMin(&S.mi[2], lo);
         atomicMax(&S.mi[3], hi);
+        atomicMin(reinterpret_cast<unsigned long long*>(&S.mq[2]), (unsigned long long)a2);
       }
       if (nest) atomicAdd(&S.u3[0], nest);
     }
@@ -331,22 +342,203 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const int hi2 = S.mi[3];
     const uint32_t nest = S.u3[0];
     if (hi2 < 0 || !rfin) flags |= RF_REGION;
-    if (nest > (uint32_t)CAPR) flags |= RF_OVERFLOW;
-    sm.reg[0] = nuc ? lo1 : (1 << 30);
-    sm.reg[1] = nuc ? hi1 : (1 << 30);
-    sm.reg[2] = hi2 >= 0 ? lo2 : (1 << 30);
-    sm.reg[3] = hi2 >= 0 ? hi2 : (1 << 30);
+    const bool need2 = !P.skip_draw;
+    // ---- crowded regions take the second level (a row-uniform decision: every
+    // chunk merged the same bins; a chunk whose first barrier timed out is
+    // deferred, and counts itself at the second barrier without waiting) ----
+    // (past 3/4 of the row's lists, so that no chunk's share passes its own
+    // list, or half of what the chunks' wave segments take)
+    const bool crowded = __builtin_expect(nest > (uint32_t)min(CAPR * 3 / 4, G * CLMAX / 2), 0);
+    const bool refine = crowded && !S.mi[6] && rfin && (!nuc || (hi1 >= 0 && hi1 - lo1 < RW)) &&
+                        (!need2 || (hi2 >= 0 && hi2 - lo2 < RW));
+    if (crowded && !refine) flags |= RF_WIDE;
+    if (S.mi[6] && tid == 0) add_agent(ctr + CTR_FINE, 1u);
+    // the regions in row bins (empty: 1 << 30), and in this chunk's bins
+    // (its reference is dl octaves under the row's)
+    constexpr int NOB = 1 << 30;
+    const int cr[4] = {nuc ? lo1 : NOB, nuc ? hi1 : NOB, hi2 >= 0 ? lo2 : NOB, hi2 >= 0 ? hi2 : NOB};
+    const int dl = Mfin && rfin ? (int)fminf(R - ref, 4096.0f) : 0;
+    auto own = [&](int b) { return b >= NOB ? b : b + HOCT * dl; };
+    const int l1 = own(cr[0]), h1 = own(cr[1]), l2 = own(cr[2]), h2 = own(cr[3]);
+    uint32_t L1, C1, L2, C2;
+    region_pair(l1, h1, L1, C1);
+    region_pair(l2, h2, L2, C2);
+    if (!Mfin) C1 = 0u;
+    if (!Mfin || !need2) C2 = 0u;
+    // published regions: row fine bins (whole bins unless refined)
+    int fr[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) fr[q] = cr[q] >= NOB ? NOB : cr[q] * FSUB + ((q & 1) ? FSUB - 1 : 0);
+    // refined rows: this chunk's fine bounds of each region (for the candidate
+    // test) and the exact masses above them inside the region bins
+    int cf[4] = {0, -1, 0, -1};
+    float xr[4] = {0.0f, -1.0f, 0.0f, -1.0f};  // refined rows: the fine regions as ranges of logits
+    double fab1 = 0.0, fab2 = 0.0;
+    uint32_t fnab = 0;
+    if (__builtin_expect(refine, 0)) {
+      // slot p of region q holds the fine bin F0 - p of its top bin (mass descending)
+      const int F0a = cr[1] < NOB ? (h1 + 1) * FSUB - 1 : -1, F0b = need2 ? (h2 + 1) * FSUB - 1 : -1;
+      // (1) this chunk's fine bins of the region bins (the masses recomputed as binned)
+#pragma unroll
+      for (int k = 0; k < NE / 2; k++) {
+        const uint32_t t1 = in_region2(bins[k], L1, C1), t2 = in_region2(bins[k], L2, C2);
+        if (__builtin_amdgcn_ballot_w64((t1 | t2) != 0u) == 0ull) continue;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const bool o1 = (t1 >> (16 * h) & 0xFFFFu) != 0u, o2 = (t2 >> (16 * h) & 0xFFFFu) != 0u;
+          if (o1 || o2) {
+            const float e = emass(C.x[2 * k + h], c, ref);
+            const int f = efine(e);
+            const unsigned long long add = (1ull << 48) | (unsigned long long)(__float_as_uint(e) & 0xFFu);
+            if (o1) atomicAdd(&S.fh[F0a - f], add);
+            if (o2) atomicAdd(&S.fh[RW * FSUB + F0b - f], add);
+          }
+        }
+      }
+      __syncthreads();
+      RG_STAMP(17);
+      // (2) publish them as fp32 masses (thread t: slots 2t, 2t + 1), one
+      // barrier among the row's chunks, merge (rescaled, in chunk order)
+      static_assert(FHN == 2 * NT, "two fine bins per thread");
+      const bool q2 = tid >= NT / 2;
+      const int p0 = 2 * (tid & (NT / 2 - 1));
+      const int f0 = q2 ? F0b : F0a;
+      const unsigned long long acc0 = S.fh[2 * tid], acc1 = S.fh[2 * tid + 1];
+      *reinterpret_cast<float2*>(F.fine + ((int64_t)r * G + j) * FHN + 2 * tid) =
+          make_float2((float)fine_mass(f0 - p0, acc0), (float)fine_mass(f0 - p0 - 1, acc1));
+      release_agent();
+      __syncthreads();
+      if (tid == 0) {
+        release_count();
+        add_agent(ctr + CTR_FINE, 1u);
+        S.mi[6] = wait_count(ctr + CTR_FINE, (uint32_t)G) ? 0 : 1;
+        acquire_one();
+      }
+      __syncthreads();
+      acquire_agent();
+      RG_STAMP(18);
+      if (S.mi[6]) flags |= RF_REGION;
+      double fm[2] = {0.0, 0.0};
+      for (int w0 = 0; w0 < G; w0 += 4) {
+        float2 v[4];
+        double sw[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int w = w0 + q;
+          const float rw = w < G ? S.rf[w] : -INFINITY;
+          const int dw = rw != -INFINITY ? (int)fminf(R - rw, 4096.0f) : 4096;
+          sw[q] = dw < 1024 ? ldexp(1.0, -dw) : 0.0;
+          v[q] = w < G ? ld_pub(reinterpret_cast<const float2*>(F.fine + ((int64_t)r * G + w) * FHN + 2 * tid))
+                       : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          fm[0] += (double)v[q].x * sw[q];
+          fm[1] += (double)v[q].y * sw[q];
+        }
+      }
+      // (3) the fine regions: region 1's fine bins meeting the cut, then region
+      // 2's meeting the draw (u times the kept mass, bounded by region 1's);
+      // cumulative masses from each region's top (exclusive scan per half)
+      const double ms = fm[0] + fm[1];
+      const double inc = wscan_incl(ms);
+      if (lane == 63) S.d3[wv] = inc;
+      if (tid == 0) {
+        S.mi[10] = NOB; S.mi[11] = -1; S.mi[13] = NOB; S.mi[15] = -1;
+        S.mq[3] = ~0ull;
+        S.mq[4] = 0ull;
+      }
+      __syncthreads();
+      double a = inc - ms;
+#pragma unroll
+      for (int i = 0; i < NW; i++) a += (i < wv && (i >= NW / 2) == q2) ? S.d3[i] : 0.0;
+      if (!q2 && nuc) {
+        a += __builtin_bit_cast(double, S.mq[0]);
+        int lo = NOB, hi = -1;
+        uint64_t at = ~0ull, ab = 0ull;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          if (fm[i] > 0.0 && a <= Pm + eps && a + fm[i] >= Pm - eps) {
+            lo = min(lo, p0 + i);
+            hi = max(hi, p0 + i);
+            at = min(at, __builtin_bit_cast(uint64_t, a));
+            ab = max(ab, __builtin_bit_cast(uint64_t, a + fm[i]));
+          }
+          a += fm[i];
+        }
+        if (hi >= 0) {
+          atomicMin(&S.mi[10], lo);
+          atomicMax(&S.mi[11], hi);
+          atomicMin(reinterpret_cast<unsigned long long*>(&S.mq[3]), (unsigned long long)at);
+          atomicMax(reinterpret_cast<unsigned long long*>(&S.mq[4]), (unsigned long long)ab);
+        }
+      }
+      __syncthreads();
+      if (q2 && need2) {
+        a += __builtin_bit_cast(double, S.mq[2]);
+        const double tl = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[3]) : (double)u * Z) - eps;
+        const double th = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[4]) : (double)u * Z) + eps;
+        int lo = NOB, hi = -1;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          if (fm[i] > 0.0 && a <= th && a + fm[i] >= tl) {
+            lo = min(lo, p0 + i);
+            hi = max(hi, p0 + i);
+          }
+          a += fm[i];
+        }
+        if (hi >= 0) {
+          atomicMin(&S.mi[13], lo);
+          atomicMax(&S.mi[15], hi);
+        }
+      }
+      __syncthreads();
+      RG_STAMP(21);
+      const int fp[4] = {S.mi[10], S.mi[11], S.mi[13], S.mi[15]};
+      if ((nuc && fp[1] < 0) || (need2 && fp[3] < 0)) flags |= RF_REGION;
+      if (nuc) {
+        cf[0] = F0a - fp[1]; cf[1] = F0a - fp[0];
+        fr[0] = (cr[1] + 1) * FSUB - 1 - fp[1]; fr[1] = (cr[1] + 1) * FSUB - 1 - fp[0];
+      }
+      if (need2) {
+        cf[2] = F0b - fp[3]; cf[3] = F0b - fp[2];
+        fr[2] = (cr[3] + 1) * FSUB - 1 - fp[3]; fr[3] = (cr[3] + 1) * FSUB - 1 - fp[2];
+      }
+      // (4) this chunk's exact mass (and count) above each fine region inside its region bins
+      const unsigned long long acc[2] = {acc0, acc1};
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int p = p0 + i;
+        if (!q2 && nuc && p < fp[0]) { fab1 += fine_mass(F0a - p, acc[i]); fnab += (uint32_t)(acc[i] >> 48); }
+        if (q2 && need2 && p < fp[2]) fab2 += fine_mass(F0b - p, acc[i]);
+      }
+      // (5) the fine regions as ranges of logits [first key reaching the low
+      // bound, first key past the high bound - 1]: wave w < 4 finds bound w
+      if (wv < 4) {
+        const int thr = wv == 0 ? cf[0] : wv == 1 ? cf[1] + 1 : wv == 2 ? cf[2] : cf[3] + 1;
+        const uint32_t k = first_key_reaching(thr, c, ref);
+        if (lane == 0) S.i3[wv] = (int32_t)k;
+      }
+      __syncthreads();
+      xr[0] = key2f((uint32_t)S.i3[0]);
+      xr[1] = key2f((uint32_t)S.i3[1] - 1u);
+      xr[2] = key2f((uint32_t)S.i3[2]);
+      xr[3] = key2f((uint32_t)S.i3[3] - 1u);
+      if (!nuc || !Mfin) { xr[0] = 0.0f; xr[1] = -1.0f; }
+      if (!need2 || !Mfin) { xr[2] = 0.0f; xr[3] = -1.0f; }
+    }
+    sm.reg[0] = fr[0];
+    sm.reg[1] = fr[1];
+    sm.reg[2] = fr[2];
+    sm.reg[3] = fr[3];
 
     RG_STAMP(6);
     // ---- this chunk: candidates in either region, exact masses above them ----
-    const int dl = Mfin && rfin ? (int)(R - ref) : 0;
-    auto own = [&](int b) { return b >= (1 << 30) ? b : b + HOCT * dl; };
-    const int l1 = own(sm.reg[0]), h1 = own(sm.reg[1]), l2 = own(sm.reg[2]), h2 = own(sm.reg[3]);
     {
       // (per-wave sums, added up by the publishing thread after the barriers
       // of the candidate lists; the lists do not overlap the histogram)
-      double ab1 = 0.0, ab2 = 0.0;
-      uint32_t nab = 0;
+      double ab1 = fab1, ab2 = fab2;
+      uint32_t nab = fnab;
 #pragma unroll
       for (int i = 0; i < HLT; i++) {
         const int b = tid + NT * i;
@@ -363,22 +555,38 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     }
     // the elements of either region: list 0 (region 1, nucleus rows) and
     // list 1 (region 2, unless the draw is skipped), tested on bin pairs
+    // (refined rows: on their ranges of logits)
     static_assert(NE % 2 == 0, "bin pairs");
-    uint32_t L1, C1, L2, C2;
-    region_pair(l1, h1, L1, C1);
-    region_pair(l2, h2, L2, C2);
-    if (!Mfin) C1 = 0u;
-    if (!Mfin || P.skip_draw) C2 = 0u;
     uint32_t n1 = 0, n2 = 0;
+    if (__builtin_expect(refine, 0)) {
 #pragma unroll
-    for (int k = 0; k < NE / 2; k++) {
-      const uint32_t t1 = in_region2(bins[k], L1, C1), t2 = in_region2(bins[k], L2, C2);
-      if (__builtin_amdgcn_ballot_w64((t1 | t2) != 0u) == 0ull) continue;
+      for (int k = 0; k < NE / 2; k++) {
+        bool o[2][2];
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int s2 = 2 * k + h;
-        seg_put(S.l, 0, (t1 >> (16 * h) & 0xFFFFu) != 0u, n1, C.x[s2], CK::index(v0, s2));
-        seg_put(S.l, 1, (t2 >> (16 * h) & 0xFFFFu) != 0u, n2, C.x[s2], CK::index(v0, s2));
+        for (int h = 0; h < 2; h++) {
+          const float x = C.x[2 * k + h];
+          o[h][0] = x >= xr[0] && x <= xr[1];
+          o[h][1] = x >= xr[2] && x <= xr[3];
+        }
+        if (__builtin_amdgcn_ballot_w64(o[0][0] || o[0][1] || o[1][0] || o[1][1]) == 0ull) continue;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int s2 = 2 * k + h;
+          seg_put(S.l, 0, o[h][0], n1, C.x[s2], CK::index(v0, s2));
+          seg_put(S.l, 1, o[h][1], n2, C.x[s2], CK::index(v0, s2));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NE / 2; k++) {
+        const uint32_t t1 = in_region2(bins[k], L1, C1), t2 = in_region2(bins[k], L2, C2);
+        if (__builtin_amdgcn_ballot_w64((t1 | t2) != 0u) == 0ull) continue;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int s2 = 2 * k + h;
+          seg_put(S.l, 0, (t1 >> (16 * h) & 0xFFFFu) != 0u, n1, C.x[s2], CK::index(v0, s2));
+          seg_put(S.l, 1, (t2 >> (16 * h) & 0xFFFFu) != 0u, n2, C.x[s2], CK::index(v0, s2));
+        }
       }
     }
     seg_done(S.l, 0, n1);
@@ -765,6 +973,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   if (tid == 0) {  // the row's counters back to zero for the next launch, which has the next epoch
     F.counters[(int64_t)r * 32 + CTR_ARRIVE] = 0u;
     F.counters[(int64_t)r * 32 + CTR_HIST] = 0u;
+    F.counters[(int64_t)r * 32 + CTR_FINE] = 0u;
     F.counters[(int64_t)r * 32 + CTR_EPOCH] = epoch + 1u;
   }
   const int mode = g.mode;
@@ -968,19 +1177,19 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     uint32_t vkey = 0, n_tie = kNoTie;
     uint64_t Zkept = Zfx;
     int tie_lim = 0x7FFFFFFF;  // kept ids at the cut key: index <= tie_lim
-    // whether every id whose z equals fl(x / T) lies inside row bins [lo, hi]
-    // under the binning of each chunk that can hold it (one wave; lane w
-    // checks chunk w)
+    // whether every id whose z equals fl(x / T) lies inside the row's fine
+    // bins [lo, hi] (a region) under the binning of each chunk that can hold
+    // it (one wave; lane w checks chunk w)
     auto group_inside = [&](float x, int lo, int hi) -> bool {
       const Group gr = collision_group(x, T);
       bool bad = false;
       if (lane < G) {
         const float rw = S.rf[lane], mw = S.rm[lane];
         if (rw != -INFINITY && !(gr.lo > mw)) {  // some id of this chunk may reach the group
-          const int sh = HOCT * (int)(Rref - rw);
-          const uint32_t el = ebin(emass(gr.lo, c, rw)), eh = ebin(emass(fminf(gr.hi, mw), c, rw));
-          const int bl = (el == BELOW ? -(1 << 20) : (int)el) - sh;
-          const int bh = (eh == BELOW ? -(1 << 20) : (int)min(eh, (uint32_t)HB_NAN - 1u)) - sh;
+          const int sh = HOCT * FSUB * (int)fminf(Rref - rw, 4096.0f);
+          const int el = efine(emass(gr.lo, c, rw)), eh = efine(emass(fminf(gr.hi, mw), c, rw));
+          const int bl = (el < 0 ? -(1 << 28) : el) - sh;
+          const int bh = (eh < 0 ? -(1 << 28) : min(eh, HB_NAN * FSUB - 1)) - sh;
           bad = !(bl >= lo && bh <= hi);
         }
       }

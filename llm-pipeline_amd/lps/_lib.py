@@ -120,6 +120,7 @@ SIGNATURES = {
     "lps_softmax": (_i32, [ctypes.c_void_p, _vp]),
     "lps_softmax_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "lps_lm_head": (_i32, [ctypes.c_void_p, _vp]),
+    "lps_selftest_exp2_monotone": (_i32, [ctypes.POINTER(ctypes.c_ulonglong)]),
 }
 
 _lib = None

@@ -22,7 +22,9 @@ namespace {
 //     history i32[R * H], history_len i32[R] (both when H > 0), uniforms f32[R].
 // OUT: tokens i64[R], status i32[R], kept_cut f32[R], kept_ties i32[R],
 //     kept_count i32[R], row_path i32[R], chosen_logprob f32[R] (logprobs),
-//     top_logprobs f32[R * n_top], top_ids i64[R * n_top].
+//     top_logprobs f32[R * n_top], top_ids i64[R * n_top], then the workspace's
+//     row status words i32[R] (LPS_ROW_DEFERRED | reason << 8 for rows the
+//     fast kernels deferred; zeros without a workspace).
 template <typename T>
 std::vector<T> rd(FILE* f, size_t n) {
   std::vector<T> v(n);
@@ -126,6 +128,9 @@ int main(int argc, char** argv) {
   wr(o, clp);
   wr(o, tlp);
   wr(o, tids);
+  std::vector<int32_t> wst(R, 0);
+  if (ws) memcpy(wst.data(), static_cast<char*>(ws) + rg_counter_bytes(), (size_t)R * 4);
+  wr(o, wst);
   fclose(o);
   free(ws);
   free(logits);

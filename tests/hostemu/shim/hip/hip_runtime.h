@@ -274,6 +274,12 @@ inline hipError_t hipDeviceGetAttribute(int* v, int, int) { *v = 256; return hip
 template <typename T>
 inline hipError_t hipGetSymbolAddress(void** p, T* sym) { *p = (void*)sym; return hipSuccess; }
 inline hipError_t hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, n); return hipSuccess; }
+inline hipError_t hipMemset(void* p, int v, size_t n) { memset(p, v, n); return hipSuccess; }
+template <typename T>
+inline hipError_t hipMalloc(T** p, size_t n) { *p = static_cast<T*>(calloc(1, n)); return *p ? hipSuccess : 1; }
+inline hipError_t hipFree(void* p) { free(p); return hipSuccess; }
+enum { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToDevice = 3 };
+inline hipError_t hipMemcpy(void* d, const void* s, size_t n, int) { memcpy(d, s, n); return hipSuccess; }
 template <typename T>
 inline hipError_t hipMemcpyFromSymbol(void* dst, T* sym, size_t n, size_t off, int) {
   memcpy(dst, (const char*)sym + off, n);

@@ -87,7 +87,8 @@ def test_mask_equals_masked_logits(dev, name, path):
 
 
 def test_mask_split_kernels(dev):
-    """A grid above the fused kernel's limit (128 rows x 19 chunks): the split pair."""
+    """128 c2 rows with legality masks: 512 row-group workgroups, more than one
+    resident round on 256 CUs."""
     w = W.c2(B=128)
     m = _mask(w.B, w.V, seed=5)
     wm = _masked(w, m)

@@ -112,6 +112,9 @@ def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0):
     res.chosen_logprob = take(np.float32, B) if logprobs else None
     res.top_logprobs = take(np.float32, B * n_top).reshape(B, n_top) if n_top else None
     res.top_ids = take(np.int64, B * n_top).reshape(B, n_top) if n_top else None
+    # deferral reasons by row (rows the fast kernels deferred)
+    wst = take(np.int32, B)
+    res.reasons = {i: int(wst[i]) >> 8 for i in range(B) if int(res.row_path[i]) != 0}
     assert o == len(b)
     return res
 
@@ -172,3 +175,34 @@ def test_logprobs_one_chunk(run_case, tmp_path):
     w.logprobs = True
     out = _run(run_case, w, tmp_path, logprobs=True, n_top=8)
     PY.check_rows(w, out, lp=True)
+
+
+def _flat(V, B, dtype, sigma, seed):
+    """Flat rows (N(0, sigma^2) logits: thousands in one histogram bin), top_p
+    0.95 and 1 (pure), T 1, no penalties."""
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn((B, V), generator=g) * sigma).to(dtype)
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    p = torch.tensor([0.95, 1.0, 0.6, 0.95])[torch.arange(B) % 4]
+    return W.Workload("flat", x, f(1.0), f(0, torch.int32), p, f(0.0), f(1.0), f(1.0), f(0.0), f(0.0), None,
+                      None, torch.rand((B,), generator=g))
+
+
+def test_flat_rows_second_level(run_case, tmp_path):
+    """Flat fp32 rows of one chunk: the cut and draw bins hold thousands of
+    logits, more than the lists take, so the row-group kernel refines them
+    with its second histogram level (fine bins of the region bins), in
+    bounds; every row finishes there and matches the oracle."""
+    w = _flat(12288, 8, torch.float32, 0.01, seed=11)
+    out = _run(run_case, w, tmp_path)
+    assert (out.row_path == 0).all(), out.reasons
+    PY.check_rows(w, out)
+
+
+def test_flat_rows_second_level_16bit(run_case, tmp_path):
+    """Flat bf16 rows of one chunk (40960 logits, NE = 80): with 8 mantissa
+    bits the logits tie in large groups; rows the second level resolves finish
+    on the row-group kernel, the others are deferred; all match the oracle."""
+    w = _flat(40960, 4, torch.bfloat16, 0.02, seed=12)
+    out = _run(run_case, w, tmp_path)
+    PY.check_rows(w, out)
