@@ -257,7 +257,7 @@ int lps_sample(const lps_sample_args* args, void* stream);
  * array's address up once and clears its counters with a small kernel on
  * `stream`.  Batches whose lps_workspace_bytes(num_rows, vocab, flags)
  * exceeds LPS_NOALLOC_WORKSPACE_BYTES return LPS_ENOALLOC_CAPACITY (for
- * V = 151936: up to 99 rows per call).  Every call on one GPU shares that GPU's
+ * V = 151936: up to 83 rows per call).  Every call on one GPU shares that GPU's
  * array: calls that overlap in time on one GPU (other streams, other host
  * threads) race and must be ordered by the caller.  Results equal
  * lps_sample's on the same inputs. */
