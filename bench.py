@@ -190,14 +190,37 @@ def copy_calibration(nbytes: int = 256 << 20, reps: int = 4):
     print(json.dumps({"copy_calibration_bytes": nbytes, "copies": reps}), flush=True)
 
 
+def host_cpu():
+    """The host CPU the baseline ran on: model name, os.cpu_count(), the
+    cores this process may run on, and the thread share it uses (the box's
+    OMP_NUM_THREADS share when set: the GPU box gives one GPU's jobs 16 of its
+    host's cores, whatever os.cpu_count() reports)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or affinity
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cores": affinity,
+            "threads_used": max(1, min(share, affinity))}
+
+
 def cpu_baseline(w, max_rows=None, repeats=3, dev=None):
     """Reference-as-written sampler (oracle restatement), one call per row with
     that row's parameters and history (continuous_batching.py:394-401)."""
     import torch
     from oracle import reference_semantics as O
     from tests import parity as PY
-    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    threads = max(1, min(share, os.cpu_count() or 1))
+    hc = host_cpu()
+    threads = hc["threads_used"]
     torch.set_num_threads(threads)
     rows = list(range(w.B if max_rows is None else min(w.B, max_rows)))
     x32 = w.logits.float()
@@ -214,7 +237,7 @@ def cpu_baseline(w, max_rows=None, repeats=3, dev=None):
         one_pass()
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    out = {"value": round(len(rows) / t, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+    out = {"value": round(len(rows) / t, 2), "unit": "rows/s", "cores": threads, "kind": "port", "host": hc,
            "sample": f"{len(rows)} rows of the {w.name} batch x {repeats} repeats (median), fp32-upcast logits, "
                      f"torch-CPU restatement of sampling.py:51-85 with torch.multinomial"}
     if dev is not None:
@@ -384,8 +407,7 @@ def softmax_bench(args):
 
     cpu = None
     if not args.no_cpu_baseline:
-        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-        threads = max(1, min(share, os.cpu_count() or 1))
+        threads = host_cpu()["threads_used"]
         torch.set_num_threads(threads)
         n = rows if not causal else 2048
         xc = x0[:n].cpu()
@@ -405,7 +427,7 @@ def softmax_bench(args):
         t = statistics.median(ts)
         cpu_vis = visible if not causal else sum(min(cols, (r % seq_len) + 1) for r in range(n))
         cpu_bytes = cpu_vis * es + n * cols * es
-        cpu = {"value": round(cpu_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(cpu_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port", "host": host_cpu(),
                "sample": f"{n} rows of the workload, torch-CPU restatement of triton_softmax.py:105-113 "
                          f"(masked_fill, softmax in fp32, cast back), median of 10 after one warm-up call"}
 
@@ -477,7 +499,7 @@ def spec_driver_bench(args):
                                                         torch.rand(k + 1, generator=gu)))
         tcpu = time.perf_counter() - t1
         cpu = {"value": round(out.numel() / tcpu, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
-               "kind": "port", "sample": f"one request, {r_cpu} rounds of the oracle's restatement of "
+               "kind": "port", "host": host_cpu(), "sample": f"one request, {r_cpu} rounds of the oracle's restatement of "
                                           f"speculative.py:68-178 (fp32 CPU, same synthetic logits)"}
     print(json.dumps({
         "metric": "batched speculative decoding, generated tokens/s (driver and sampling only)",
@@ -591,7 +613,7 @@ def lm_head_bench(args):
             ts.append(time.perf_counter() - t0)
         t = statistics.median(ts)
         cb = vs * H * 2 + 8 * H * 2 + 8 * vs * 2
-        cpu = {"value": round(cb / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+        cpu = {"value": round(cb / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port", "host": host_cpu(),
                "sample": f"8 rows x {vs} vocabulary rows of the workload, torch-CPU fp32 matmul (the reference's "
                          f"nn.Linear on the CPU), bf16-equivalent bytes, median of 5"}
     print(json.dumps({
@@ -674,8 +696,7 @@ def spec_bench(args):
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import reference_semantics as O
-        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-        threads = max(1, min(share, os.cpu_count() or 1))
+        threads = host_cpu()["threads_used"]
         torch.set_num_threads(threads)
         nr = 8
         args_ref = (sw.target[:nr], sw.draft[:nr], sw.draft_tokens[:nr], sw.u_accept[:nr], sw.u_resample[:nr],
@@ -690,7 +711,7 @@ def spec_bench(args):
         # agreement of the timed launch with the restatement on the sampled requests
         # (an accept test within 1e-5 of its uniform may go either way)
         same = int((n_acc[:nr].cpu() == n_ref).sum())
-        cpu = {"value": round(nr / t, 2), "unit": "requests/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(nr / t, 2), "unit": "requests/s", "cores": threads, "kind": "port", "host": host_cpu(),
                "sample": f"{nr} of the 32 requests x 3 repeats (median): the oracle's torch-CPU restatement of "
                          f"speculative.py:119-174 (top-p, softmax, accept tests, resample) on the same logits",
                "parity": {"requests_checked": nr, "n_accepted_equal": same}}
