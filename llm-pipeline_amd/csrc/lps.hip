@@ -161,7 +161,8 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
     }
   }
   if (run_rg) {
-    hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE>), dim3(grid), dim3(rg::NT), 0, s, F);
+    if (F.k.entropy) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);
+    else hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, false>), dim3(grid), dim3(rg::NT), 0, s, F);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

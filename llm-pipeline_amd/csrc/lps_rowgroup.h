@@ -49,9 +49,11 @@
 // CDF in sorted order: kept ids by scaled logit descending, ties lower index
 // first.
 //
+// With the entropy output (an instantiation of its own), nucleus and pure rows
+// also sum e * log2(e) per chunk, and the finaliser gives H = ln Z - sum(e ln e) / Z.
 // A row the kernel cannot finish exactly (e.g. a region wider than RW bins
 // holding more candidates than the lists take, min-p / typical-p without top-k,
-// entropy requested) is marked LPS_ROW_DEFERRED in the workspace status and
+// entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
 // sampled by the general kernel, launched after this one with that status as
 // its filter.  (Sampling such rows in the same launch, in one tail workgroup
 // per row, was measured: the tail code in the kernel made every launch slower,
@@ -154,6 +156,7 @@ struct RgSum {
   double zsum;        // chunk mass: sum of exp2(fma(x, c, -ref))
   double ab1;         // nucleus: exact mass above region 1 (chunk reference)
   double ab2;         // nucleus: exact mass above region 2
+  double zent;        // entropy rows: sum of e * log2(e), e = exp2(fma(x, c, -ref)) (chunk reference)
   int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row fine bins, efine scale; the same
                       // in every chunk)
 };
@@ -244,7 +247,7 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   else if (g.topk > 0) mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
   else if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
   else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
-  if (P.entropy) mode = MODE_DEFER;
+  if (P.entropy && mode != MODE_NUCLEUS && mode != MODE_PURE) mode = MODE_DEFER;
   if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
   g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
   if (g.kprime > FAST_KMAX) mode = MODE_DEFER;

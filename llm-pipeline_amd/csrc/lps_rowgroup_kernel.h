@@ -16,7 +16,7 @@ __device__ __forceinline__ bool wait_count(uint32_t* p, uint32_t n) {
 // ===========================================================================
 // Chunk phase.  Returns the row's mode (MODE_DEFER: nothing published).
 // ===========================================================================
-template <int DT, int VPE, int NE>
+template <int DT, int VPE, int NE, bool HE>
 __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j,
                                            const RowCfg& g, const uint32_t epoch) {
   using CK = Chk<DT, VPE, NE>;
@@ -193,6 +193,24 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       for (int i = 0; i < NW; i++) { zs += S.d[i]; nanc += S.u[i]; }
       sm.zsum = zs;
       sm.nanbin = nanc;
+    }
+    if constexpr (HE) {
+      // the chunk's sum of e * log2(e), fp32 per vector, fp64 across
+      double zh = 0.0;
+      if (Mfin) {
+#pragma unroll
+        for (int i = 0; i < CK::NV; i++) {
+          float a = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VPE; e++) {
+            const float t = __builtin_fmaf(C.x[i * VPE + e], c, -ref);
+            const float m = __builtin_amdgcn_exp2f(t);
+            a += m > 0.0f ? m * t : 0.0f;
+          }
+          zh += (double)a;
+        }
+      }
+      sm.zent = bred(zh, S.d3, OpAdd{});
     }
     // ---- publish the summary and the bins, one barrier among the row's chunks ----
     if (tid == 0) store_sum(sums + j, sm);
@@ -960,7 +978,7 @@ __device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_
   return 0;
 }
 
-template <int DT, int VPE>
+template <int DT, int VPE, bool HE>
 __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g,
                                            const uint32_t epoch) {
   const KParams& P = F.k;
@@ -1028,6 +1046,9 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const double Z = rreduce16(rfin ? a.zsum * sc : 0.0, OpAdd{});
     const double A1 = rreduce16(rfin ? a.ab1 * sc : 0.0, OpAdd{});
     const double A2 = rreduce16(rfin ? a.ab2 * sc : 0.0, OpAdd{});
+    // entropy rows: sum of e ln e over the row, against the row reference
+    // (a chunk dl octaves under it: e 2^-dl, log2 e - dl), in log2 units
+    const double AH = HE ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
     if (lane < G) {
       S.cn[0][lane] = (int)a.n1;
       S.cn[1][lane] = (int)a.n2;
@@ -1048,7 +1069,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       S.mi[20] = (int)nanb;
       S.mi[21] = a.reg[0]; S.mi[22] = a.reg[1]; S.mi[23] = a.reg[2]; S.mi[24] = a.reg[3];
       S.mi[25] = nmax;
-      S.md[0] = Z; S.md[1] = A1; S.md[2] = A2;
+      S.md[0] = Z; S.md[1] = A1; S.md[2] = A2; S.md[3] = AH;
       S.mf[0] = R;
     }
   }
@@ -1284,6 +1305,11 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   double lnZ = 0.0;
   if ((P.chosen_logprob || g.ntop > 0) && wv == 0 && Zfull > 0.0) lnZ = log(Zfull) + (double)Rref * 0.6931471805599453;
   const double lZ = lnZ - (double)Rref * 0.6931471805599453;  // ln Zfull
+  if (HE && tid == 0) {
+    // H = ln Z - sum(e ln e) / Z (the general kernel's NaN for rows without finite statistics)
+    const bool fin = !has_nan && xmax != INFINITY && xmax != -INFINITY && __fdiv_rn(xmax, T) != INFINITY && Zfull > 0.0;
+    P.entropy[r] = fin ? (float)(log(Zfull) - 0.6931471805599453 * S.md[3] / Zfull) : NAN;
+  }
   if (P.chosen_logprob && tid == 0) {
     float lp = NAN;
     if (token >= 0 && Zfull > 0.0 && chosen_x == chosen_x && chosen_x != INFINITY && chosen_x != -INFINITY) {
@@ -1331,7 +1357,8 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 // ===========================================================================
 // The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
 // ===========================================================================
-template <int DT, int VPE, int NE>
+// HE: the launch asks for the entropy output (its code is absent otherwise).
+template <int DT, int VPE, int NE, bool HE>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -1345,7 +1372,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   // launches (stream-ordered before this one), read by every chunk of the row
   // before any of them arrives
   const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
-  const int mode = chunk_phase<DT, VPE, NE>(F, SU.c, r, j, g, epoch);
+  const int mode = chunk_phase<DT, VPE, NE, HE>(F, SU.c, r, j, g, epoch);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1363,7 +1390,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (!SU.c.mi[7] || threadIdx.x >= FT) return;
   acquire_agent();
   RG_STAMP(24);
-  const int reason = final_phase<DT, VPE>(F, SU.f, r, g, epoch);
+  const int reason = final_phase<DT, VPE, HE>(F, SU.f, r, g, epoch);
   RG_STAMP(31);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }

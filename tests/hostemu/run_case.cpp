@@ -16,13 +16,14 @@
 namespace {
 
 // IN: int32 header[16] = {magic 0x4C505345, dtype, R, V, H, n_top, flags,
-//     use_workspace, logprobs, hint, 0...}, then
+//     use_workspace, logprobs, entropy, skip_draw, 0...}, then
 //     logits [R * V] (dtype), temperature f32[R], top_k i32[R], top_p f32[R],
 //     min_p f32[R], typical_p f32[R], rep f32[R], pres f32[R], freq f32[R],
 //     history i32[R * H], history_len i32[R] (both when H > 0), uniforms f32[R].
 // OUT: tokens i64[R], status i32[R], kept_cut f32[R], kept_ties i32[R],
 //     kept_count i32[R], row_path i32[R], chosen_logprob f32[R] (logprobs),
-//     top_logprobs f32[R * n_top], top_ids i64[R * n_top], then the workspace's
+//     top_logprobs f32[R * n_top], top_ids i64[R * n_top], entropy f32[R] (when
+//     asked), then the workspace's
 //     row status words i32[R] (LPS_ROW_DEFERRED | reason << 8 for rows the
 //     fast kernels deferred; zeros without a workspace).
 template <typename T>
@@ -51,6 +52,7 @@ int main(int argc, char** argv) {
   const std::vector<int32_t> h = rd<int32_t>(f, 16);
   if (h[0] != 0x4C505345) return 2;
   const int dtype = h[1], R = h[2], V = h[3], H = h[4], n_top = h[5], flags = h[6], use_ws = h[7], lp = h[8];
+  const int want_h = h[9], skip_draw = h[10];
   const size_t es = dtype == LPS_DTYPE_F32 ? 4 : 2;
   // the logits exactly sized (an access past the last row is caught)
   std::vector<uint8_t> logits_v = rd<uint8_t>(f, (size_t)R * V * es);
@@ -72,6 +74,7 @@ int main(int argc, char** argv) {
   std::vector<int32_t> status(R, -7), ties(R, -7), count(R, -7), path(R, -7);
   std::vector<float> cut(R, -7.0f), clp(lp ? R : 0, -7.0f), tlp((size_t)R * n_top, -7.0f);
   std::vector<int64_t> tids((size_t)R * n_top, -7);
+  std::vector<float> ent(want_h ? R : 0, -7.0f);
 
   lps_sample_args a{};
   a.logits = logits;
@@ -105,6 +108,8 @@ int main(int argc, char** argv) {
   a.kept_ties = ties.data();
   a.kept_count = count.data();
   a.row_path = path.data();
+  a.entropy = want_h ? ent.data() : nullptr;
+  a.skip_draw = skip_draw;
   a.flags = flags;
   void* ws = nullptr;
   if (use_ws) {
@@ -128,6 +133,7 @@ int main(int argc, char** argv) {
   wr(o, clp);
   wr(o, tlp);
   wr(o, tids);
+  wr(o, ent);
   std::vector<int32_t> wst(R, 0);
   if (ws) memcpy(wst.data(), static_cast<char*>(ws) + rg_counter_bytes(), (size_t)R * 4);
   wr(o, wst);

@@ -266,6 +266,40 @@ def test_mirostat_entropy(dev):
         assert PY.draw_ok(z, kept, u, int(tok)), (u, int(tok), ref_tok, k)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_entropy_on_the_row_group_kernel(dev, dtype):
+    """The entropy output of pure rows with the draw skipped (the first call
+    of sample_mirostat_v2, sampling.py:240-279), and of nucleus rows that
+    draw, at c2's shape (B = 64, V = 151936: four chunks per row, chunk
+    references up to several octaves apart): every row finishes on the
+    row-group kernel, H of softmax(x / T) within 2e-5 of the fp64 value, and
+    the nucleus rows' draws still match the oracle."""
+    from lps import SamplingParams, sample_rows
+    w = W.c2()
+    x = w.logits.to(dtype)
+    B = w.B
+    T = w.temperature.clamp(min=0.3)
+    params = SamplingParams.build(B, dev, temperature=T.to(dev))
+    out = sample_rows(x.to(dev), params, None, entropy=True, skip_draw=True)
+    assert (out.row_path.cpu() == 0).all(), out.row_path.cpu().tolist()
+    H = out.entropy.cpu().double()
+    z = x.double() / T.double().view(-1, 1)
+    href = -(torch.softmax(z, 1) * torch.log_softmax(z, 1)).sum(1)
+    err = (H - href).abs() / href.abs().clamp(min=1.0)
+    assert float(err.max()) <= 2e-5, (int(err.argmax()), float(H[err.argmax()]), float(href[err.argmax()]))
+    # nucleus rows that also draw, with the entropy asked for
+    wn = W.c2()
+    wn.logits = x
+    wn.temperature = T
+    wn.top_k = torch.zeros(B, dtype=torch.int32)
+    wn.histories = wn.hist_len = None   # (the entropy is of the penalised logits: compare unpenalised rows)
+    outn = PY.run_workload(wn, dev, entropy=True)
+    assert (outn.row_path.cpu() == 0).all(), outn.row_path.cpu().tolist()
+    Hn = outn.entropy.cpu().double()
+    assert float(((Hn - href).abs() / href.abs().clamp(min=1.0)).max()) <= 2e-5
+    PY.check_rows(wn, outn)
+
+
 def test_mirostat_long_low_entropy_loop(dev):
     """A peaked row (entropy below tau) makes prev grow every step, so
     k = int(exp(prev)) passes the vocabulary size; the reference's top-k

@@ -70,7 +70,7 @@ def run_case():
     return exe
 
 
-def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0):
+def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0, entropy=False, skip_draw=False):
     """One lps_sample call of workload w under the sanitizers; its outputs as a
     SampleOutput-like namespace of CPU tensors."""
     B, V = w.B, w.V
@@ -78,7 +78,7 @@ def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0):
     inp, out = tmp_path / "in.bin", tmp_path / "out.bin"
     with open(inp, "wb") as f:
         f.write(struct.pack("<16i", 0x4C505345, DT[w.logits.dtype], B, V, H, n_top, flags, int(workspace),
-                            int(logprobs), 0, 0, 0, 0, 0, 0, 0))
+                            int(logprobs), int(entropy), int(skip_draw), 0, 0, 0, 0, 0))
         f.write(w.logits.contiguous().view(torch.int16 if w.logits.dtype != torch.float32 else torch.int32)
                 .numpy().tobytes())
         for a, dt in ((w.temperature, np.float32), (w.top_k, np.int32), (w.top_p, np.float32),
@@ -112,6 +112,7 @@ def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0):
     res.chosen_logprob = take(np.float32, B) if logprobs else None
     res.top_logprobs = take(np.float32, B * n_top).reshape(B, n_top) if n_top else None
     res.top_ids = take(np.int64, B * n_top).reshape(B, n_top) if n_top else None
+    res.entropy = take(np.float32, B) if entropy else None
     # deferral reasons by row (rows the fast kernels deferred)
     wst = take(np.int32, B)
     res.reasons = {i: int(wst[i]) >> 8 for i in range(B) if int(res.row_path[i]) != 0}
@@ -206,3 +207,27 @@ def test_flat_rows_second_level_16bit(run_case, tmp_path):
     w = _flat(40960, 4, torch.bfloat16, 0.02, seed=12)
     out = _run(run_case, w, tmp_path)
     PY.check_rows(w, out)
+
+
+def test_entropy_pure_rows(run_case, tmp_path):
+    """The entropy output (the first call of sample_mirostat_v2: pure rows,
+    draw skipped) on one-chunk rows of the row-group kernel, and on rows with a
+    penalty and non-finite values: H of softmax(x / T) within 2e-5 of the
+    fp64 value; NaN where the row has no finite distribution."""
+    B, V = 6, 12288
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((B, V), generator=g) * torch.tensor([2.0, 0.3, 6.0, 1.0, 2.0, 1.0]).view(-1, 1)
+    x[4, 17] = float("nan")
+    x[5] = float("-inf")
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    T = torch.tensor([1.0, 0.7, 1.3, 1.0, 1.0, 1.0])
+    w = W.Workload("entropy", x, T, f(0, torch.int32), f(1.0), f(0.0), f(1.0), f(1.0), f(0.0), f(0.0), None,
+                   None, torch.rand((B,), generator=g))
+    out = _run(run_case, w, tmp_path, entropy=True, skip_draw=True)
+    assert (out.row_path[:4] == 0).all(), (out.row_path.tolist(), out.reasons)
+    for i in range(4):
+        z = x[i].double() / float(T[i])
+        p = torch.softmax(z, 0)
+        h = float(-(p * torch.log_softmax(z, 0)).sum())
+        assert abs(float(out.entropy[i]) - h) <= 2e-5 * max(1.0, abs(h)), (i, float(out.entropy[i]), h)
+    assert np.isnan(float(out.entropy[4])) and np.isnan(float(out.entropy[5]))
