@@ -280,9 +280,9 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct SpecWs {
   void* fast;         // the fast path's workspace (first, so its counters never move)
   size_t fast_bytes;
-  int64_t* draws_t;   // [B*(k+1)]
+  int64_t* draws_t;   // [B*(k+1)], then draws_d
   int64_t* draws_d;   // [B*k]
-  float* p_t;         // [B*(k+1)]
+  float* p_t;         // [B*(k+1)], then q_d
   float* q_d;         // [B*k]
   int32_t* first_rej; // [B]
   RowPlan* plans;     // [B*(k+1) + B*k]
@@ -293,12 +293,13 @@ SpecWs spec_layout(void* base, int B, int k, int V) {
   SpecWs w{};
   const size_t Rt = (size_t)B * (k + 1), Rd = (size_t)B * k;
   w.fast = base;
-  w.fast_bytes = rg_layout(nullptr, (int)Rt, V).bytes;
+  w.fast_bytes = rg_layout(nullptr, (int)(Rt + Rd), V).bytes;
   size_t off = align256(w.fast_bytes);
-  w.draws_t = ws_at<int64_t>(base, off); off = align256(off + Rt * 8);
-  w.draws_d = ws_at<int64_t>(base, off); off = align256(off + Rd * 8);
-  w.p_t = ws_at<float>(base, off); off = align256(off + Rt * 4);
-  w.q_d = ws_at<float>(base, off); off = align256(off + Rd * 4);
+  // (target then draft entries, contiguous: one launch may write both)
+  w.draws_t = ws_at<int64_t>(base, off);
+  w.draws_d = ws_at<int64_t>(base, off + Rt * 8); off = align256(off + (Rt + Rd) * 8);
+  w.p_t = ws_at<float>(base, off);
+  w.q_d = ws_at<float>(base, off + Rt * 4); off = align256(off + (Rt + Rd) * 4);
   w.first_rej = ws_at<int32_t>(base, off); off = align256(off + (size_t)B * 4);
   w.plans = ws_at<RowPlan>(base, off); off = align256(off + (Rt + Rd) * sizeof(RowPlan));
   w.bytes = off;
@@ -605,7 +606,23 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   // Every row shares the temperature and top-p: the row-kind hint that skips
   // the kernel no row needs (T > 0: nucleus or pure rows; else greedy).
   const int hint = a->temperature > 0.0f ? LPS_FLAG_ROWS_NUCLEUS : LPS_FLAG_ROWS_TOPK;
+  const int Rt = B * (k + 1), Rd = B * k;
   bool vec = vec_ok(a->target_logits, a->dtype, V, k + 1, a->target_stride_b, a->target_stride_k);
+  const bool vec_d = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
+  if (!lev && Rt + Rd <= RG_MAX_ROWS) {
+    // both row sets in one launch: the target rows, then the draft rows as
+    // the second row segment (their own logits and layout, draws skipped);
+    // the outputs of the two sets are contiguous in the workspace
+    KParams J = P;
+    J.R = Rt + Rd;
+    J.R1 = Rt;
+    J.logits2 = a->draft_logits;
+    J.rows_inner2 = k;
+    J.stride_outer2 = a->draft_stride_b;
+    J.stride_inner2 = a->draft_stride_k;
+    J.skip_draw2 = 1;
+    if (run_sample(J, a->dtype, vec && vec_d, w.fast, w.fast_bytes, hint, s) != hipSuccess) return LPS_ELAUNCH;
+  } else {
   if ((lev ? dispatch_gen(a->dtype, vec, P, s) : run_sample(P, a->dtype, vec, w.fast, w.fast_bytes, hint, s)) !=
       hipSuccess)
     return LPS_ELAUNCH;
@@ -624,11 +641,11 @@ int lps_spec_verify(const lps_spec_args* a, void* stream) {
   D.row_status = a->row_status ? a->row_status + (size_t)B * (k + 1) : nullptr;
   D.skip_draw = 1;
   D.plans = w.plans + (size_t)B * (k + 1);
-  vec = vec_ok(a->draft_logits, a->dtype, V, k, a->draft_stride_b, a->draft_stride_k);
-  // (planned for the target rows' count, for which the workspace is sized)
-  if ((lev ? dispatch_gen(a->dtype, vec, D, s) : run_sample(D, a->dtype, vec, w.fast, w.fast_bytes, hint, s, P.R)) !=
+  // (planned for both row sets' count, for which the workspace is sized)
+  if ((lev ? dispatch_gen(a->dtype, vec_d, D, s) : run_sample(D, a->dtype, vec_d, w.fast, w.fast_bytes, hint, s, Rt + Rd)) !=
       hipSuccess)
     return LPS_ELAUNCH;
+  }
 
   hipLaunchKernelGGL(spec_epilogue_kernel, dim3((B + 255) / 256), dim3(256), 0, s, B, k, a->temperature, w.p_t,
                      w.q_d, w.draws_t, a->draft_tokens, a->u_accept, a->n_accepted, a->tokens, a->accept,

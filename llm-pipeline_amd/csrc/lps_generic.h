@@ -48,6 +48,14 @@ struct KParams {
   const void* logits;
   int V, R, rows_inner;
   int64_t stride_outer, stride_inner;
+  // an optional second row segment (rows R1 .. R - 1 when logits2 is set: the
+  // speculative draft rows beside the target rows): its own logits and row
+  // layout, its own skip_draw, no uniforms
+  int R1;
+  const void* logits2;
+  int rows_inner2;
+  int64_t stride_outer2, stride_inner2;
+  int skip_draw2;
   const float* temperature; float temperature_def;
   const int32_t* top_k; int top_k_def;
   const float* top_p; float top_p_def;
@@ -75,6 +83,39 @@ struct KParams {
   int64_t allowed_stride;      // 32-bit words
   int append_history;          // write each sampled token into the row's history
 };
+
+// Row r's segment: its logits base, row within the segment and row layout.
+struct RowSeg {
+  const void* base;
+  int rl, ri;
+  int64_t so, si;
+  bool second;
+};
+__device__ __forceinline__ RowSeg row_seg(const KParams& P, int r) {
+  const bool s2 = P.logits2 != nullptr && r >= P.R1;
+  return RowSeg{s2 ? P.logits2 : P.logits, s2 ? r - P.R1 : r, s2 ? P.rows_inner2 : P.rows_inner,
+                s2 ? P.stride_outer2 : P.stride_outer, s2 ? P.stride_inner2 : P.stride_inner, s2};
+}
+// Row r's logits (ES bytes per element).
+template <int ES>
+__device__ __forceinline__ const char* seg_row_ptr(const KParams& P, int r) {
+  const RowSeg q = row_seg(P, r);
+  return reinterpret_cast<const char*>(q.base) + ES * ((int64_t)(q.rl / q.ri) * q.so + (int64_t)(q.rl % q.ri) * q.si);
+}
+// Row r's draw is skipped.
+__device__ __forceinline__ bool row_skips_draw(const KParams& P, int r) {
+  return (P.logits2 != nullptr && r >= P.R1) ? P.skip_draw2 != 0 : P.skip_draw != 0;
+}
+// Row r's uniform array (the second segment has none).
+__device__ __forceinline__ const float* row_uniforms(const KParams& P, int r) {
+  return (P.logits2 != nullptr && r >= P.R1) ? nullptr : P.uniforms;
+}
+// Index of row r's query token in query_tokens, or -1 when it has none.
+__device__ __forceinline__ int64_t row_query_index(const KParams& P, int r) {
+  const RowSeg q = row_seg(P, r);
+  if (!P.query_tokens || (q.rl % q.ri) >= P.query_inner) return -1;
+  return (int64_t)(q.rl / q.ri) * P.query_inner + (q.rl % q.ri);
+}
 // With append_history: row r's sampled token joins its history for the next
 // step (when the row has room, history_len[r] < history_stride).  One thread.
 __device__ __forceinline__ void append_token(const KParams& P, int r, int64_t token) {
@@ -403,8 +444,7 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   const int tid = threadIdx.x;
   S.nth = nth;  // (every thread stores the same value before its first use)
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
-  const void* row = reinterpret_cast<const char*>(P.logits) +
-                    ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
+  const void* row = seg_row_ptr<ES>(P, r);
   const int V = P.V;
 
   const float T = P.temperature ? P.temperature[r] : P.temperature_def;
@@ -481,9 +521,8 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   uint32_t key_lo = 0, n_tie = kNoTie;
   uint64_t Zk = 0;
   float qprob = 0.0f;
-  const int64_t qtok = (P.query_tokens && (r % P.rows_inner) < P.query_inner)
-                           ? P.query_tokens[(int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner)]
-                           : -1;
+  const int64_t qi = row_query_index(P, r);
+  const int64_t qtok = qi >= 0 ? P.query_tokens[qi] : -1;
   if (greedy) {
     key_lo = mkey;
     n_tie = 1;
@@ -622,8 +661,9 @@ __device__ __forceinline__ void gen_row(const KParams& P, const int r, GenShared
   }
 
   // ---- inverse-CDF draw in sorted order: z descending, ties lower index first ----
-  if (!greedy && status == 0 && !P.skip_draw) {
-    float u = P.uniforms ? P.uniforms[r] : 0.5f;
+  if (!greedy && status == 0 && !row_skips_draw(P, r)) {
+    const float* ur = row_uniforms(P, r);
+    float u = ur ? ur[r] : 0.5f;
     if (!(u >= 0.0f)) u = 0.0f;
     if (u >= 1.0f) u = 0.99999994f;
     uint64_t target = (uint64_t)((double)u * (double)Zf);

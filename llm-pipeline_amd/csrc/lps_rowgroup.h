@@ -230,10 +230,9 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   g.rep = param_or(P.rep, r, P.rep_def);
   g.pres = param_or(P.pres, r, P.pres_def);
   g.freq = param_or(P.freq, r, P.freq_def);
-  g.u = param_or(P.uniforms, r, 0.5f);
-  const bool hasq = P.query_tokens && (r % P.rows_inner) < P.query_inner;
-  g.qtok = param_or(hasq ? P.query_tokens : (const int64_t*)nullptr,
-                    (int64_t)(r / P.rows_inner) * P.query_inner + (r % P.rows_inner), (int64_t)-1);
+  g.u = param_or(row_uniforms(P, r), r, 0.5f);
+  const int64_t qi = row_query_index(P, r);
+  g.qtok = param_or(qi >= 0 ? P.query_tokens : (const int64_t*)nullptr, qi >= 0 ? qi : 0, (int64_t)-1);
   // a query id outside the vocabulary has probability 0 (as verify_drafts_kernel
   // treats it); no logit is read for it
   if (g.qtok >= (int64_t)P.V) g.qtok = -1;
@@ -879,8 +878,7 @@ __device__ __forceinline__ Group collision_group(float x0, float T) {
 template <int DT>
 __device__ __forceinline__ const char* row_ptr(const KParams& P, int r) {
   constexpr int ES = DT == LPS_DTYPE_F32 ? 4 : 2;
-  return reinterpret_cast<const char*>(P.logits) +
-         ES * ((int64_t)(r / P.rows_inner) * P.stride_outer + (int64_t)(r % P.rows_inner) * P.stride_inner);
+  return seg_row_ptr<ES>(P, r);
 }
 
 }  // namespace rg

@@ -360,7 +360,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const int hi2 = S.mi[3];
     const uint32_t nest = S.u3[0];
     if (hi2 < 0 || !rfin) flags |= RF_REGION;
-    const bool need2 = !P.skip_draw;
+    const bool need2 = !row_skips_draw(P, r);
     // ---- crowded regions take the second level (a row-uniform decision: every
     // chunk merged the same bins; a chunk whose first barrier timed out is
     // deferred, and counts itself at the second barrier without waiting) ----
@@ -1190,7 +1190,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   } else if (status == 0 && hmode) {
     // ======================= nucleus / pure =======================
     const bool nuc = mode == MODE_NUCLEUS;
-    const bool want2 = !P.skip_draw;
+    const bool want2 = !row_skips_draw(P, r);
     const int lo1 = S.mi[21], hi1 = S.mi[22], lo2 = S.mi[23], hi2 = S.mi[24];
     const double Z = S.md[0];
     const uint64_t Zfx = (uint64_t)(Z * kFix);
@@ -1298,7 +1298,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       if (kept) qprob = (float)((double)zmass_fix(zq, Rref) / (double)Zkept);
     }
   }
-  if (P.skip_draw && !greedy) token = -1;
+  if (row_skips_draw(P, r) && !greedy) token = -1;
 
   // ---- outputs ----
   // ln of sum exp(z) over the row: Z is in units of 2^Rref of exp2(x c)

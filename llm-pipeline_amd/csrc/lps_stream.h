@@ -840,7 +840,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   if (greedy) status = 0;
   RG_STAMP(7);
   int64_t token = status ? -1 : d.token;
-  if (P.skip_draw && !greedy) token = -1;
+  if (row_skips_draw(P, r) && !greedy) token = -1;
   double lnZ = 0.0;
   if (want_lp && Z > 0.0) lnZ = log(Z) + (double)R * 0.6931471805599453;
   // logprobs from the logits' masses in the row mass's own arithmetic
