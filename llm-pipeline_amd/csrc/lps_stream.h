@@ -36,7 +36,8 @@
 //     No barrier is taken inside the stream.
 // History ids.  Before the stream the row's in-range history ids set bits of
 // a vocabulary bitmap, and the set bits become a sorted list of the distinct
-// ids (a block scan of the words' bit counts gives each id its rank); with a
+// ids (a block scan of the threads' bit counts over their words gives each id
+// its rank); with a
 // frequency penalty every history id then adds to its entry's count (found by
 // binary search).  An entry is id | count << 18 (ids < 2^18).
 // After the stream:
@@ -75,7 +76,7 @@ constexpr int POOL = 2048;        // pool entries (wave candidates and history i
 constexpr int HLIST = 4096;       // distinct history ids of a row (sorted list)
 constexpr uint32_t HCMAX = (1u << 14) - 2;  // largest history count of an entry
 constexpr int HPT_ = HLIST / SNT; // list entries per thread after the stream
-constexpr int BMT = BMW / SNT;    // bitmap words per thread (word t + SNT i)
+constexpr int BMT = BMW / SNT;    // bitmap words per thread (words BMT t .. BMT t + BMT - 1)
 static_assert(BMW % SNT == 0, "whole bitmap words per thread");
 static_assert(STREAM_VMAX <= (1 << 18), "18-bit ids in the list entries");
 static_assert(POOL == SNW * SEG, "the pool reuses the segments' storage");
@@ -93,7 +94,7 @@ struct StShared : RgX {
   } a;
   uint64_t sc[KM];                      // prefix of the masses (topk_decide)
   uint32_t hl[HLIST];                   // distinct history ids, ascending: id | count << 18
-  uint32_t hwb[SNW][BMT];               // bitmap words' bit counts per wave (list ranks)
+  uint32_t hwb[SNW];                    // the waves' bitmap bit counts (list ranks)
   union {
     struct {
       uint32_t x[SNW][SEG];             // candidate logits (bits)
@@ -319,42 +320,42 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
     for (int j = tid + 2 * SNT; j < g.hlen; j += SNT) mark(g.hrow[j]);
   }
   __syncthreads();
+  RG_STAMP(12);
   if (pen) {
-    // ranks: word t + SNT i of thread t; words in order i-major.  The bit
-    // counts of each round i are scanned over the block (per wave by DPP,
-    // then across waves), and the rounds follow each other.
+    // ranks: thread t holds the words [BMT t, BMT t + BMT), so one scan of
+    // the threads' bit counts over the block (per wave by DPP, then across
+    // the waves) ranks every id, in ascending order
     const int nw = (V + 31) >> 5;
-    uint32_t wd[BMT], pc[BMT], ex[BMT];
+    uint32_t wd[BMT];
+    uint32_t pc = 0;
 #pragma unroll
     for (int i = 0; i < BMT; i++) {
-      const int w = tid + SNT * i;
+      const int w = BMT * tid + i;
       wd[i] = w < nw ? S.a.bm[w] : 0u;
-      pc[i] = (uint32_t)__builtin_popcount(wd[i]);
-      const uint32_t inc = wscan_incl(pc[i]);
-      ex[i] = inc - pc[i];
-      if (lane == 63) S.hwb[wv][i] = inc;
+      pc += (uint32_t)__builtin_popcount(wd[i]);
     }
+    const uint32_t inc = wscan_incl(pc);
+    if (lane == 63) S.hwb[wv] = inc;
     __syncthreads();
-    uint32_t base = 0;
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int v = 0; v < SNW; v++) {
+      const uint32_t cv = S.hwb[v];
+      before += v < wv ? cv : 0u;
+      total += cv;
+    }
+    uint32_t rk = before + inc - pc;
 #pragma unroll
     for (int i = 0; i < BMT; i++) {
-      uint32_t before = 0, round = 0;
-#pragma unroll
-      for (int v = 0; v < SNW; v++) {
-        const uint32_t c = S.hwb[v][i];
-        before += v < wv ? c : 0u;
-        round += c;
-      }
-      uint32_t rk = base + before + ex[i];
-      const int w0 = (tid + SNT * i) << 5;
+      const int w0 = (BMT * tid + i) << 5;
       for (uint32_t b = wd[i]; b; b &= b - 1u) {
         if (rk < (uint32_t)HLIST) S.hl[rk] = (uint32_t)(w0 + __builtin_ctz(b));
         rk++;
       }
-      base += round;
     }
-    if (tid == 0) S.mi[3] = (int)base;
+    if (tid == 0) S.mi[3] = (int)total;
     __syncthreads();
+    RG_STAMP(13);
     const int D = S.mi[3];
     if (counts && D <= HLIST) {
       // every history id adds one to its entry (binary search over the sorted ids)
