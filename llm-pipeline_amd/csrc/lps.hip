@@ -161,7 +161,11 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
     }
   }
   if (run_rg) {
-    if (F.k.entropy) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);
+    // the variant with the entropy output and the mass-only path for pure rows
+    // without a draw (top_p >= 1 by default or per row)
+    const bool xf = F.k.entropy || ((F.k.skip_draw || (F.k.logits2 && F.k.skip_draw2)) &&
+                                    (F.k.top_p != nullptr || !(F.k.top_p_def < 1.0f)));
+    if (xf) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);
     else hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, false>), dim3(grid), dim3(rg::NT), 0, s, F);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

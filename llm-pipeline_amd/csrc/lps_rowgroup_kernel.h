@@ -16,7 +16,7 @@ __device__ __forceinline__ bool wait_count(uint32_t* p, uint32_t n) {
 // ===========================================================================
 // Chunk phase.  Returns the row's mode (MODE_DEFER: nothing published).
 // ===========================================================================
-template <int DT, int VPE, int NE, bool HE>
+template <int DT, int VPE, int NE, bool XF>
 __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j,
                                            const RowCfg& g, const uint32_t epoch) {
   using CK = Chk<DT, VPE, NE>;
@@ -55,7 +55,10 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
   float tm = -INFINITY;
 #pragma unroll
   for (int s = 0; s < NE; s++) tm = fmaxf(tm, C.x[s]);
-  const bool hist_mode = mode == MODE_NUCLEUS || mode == MODE_PURE;
+  // pure rows without a draw (query probabilities, entropy) need only the
+  // row mass: no histogram, barrier or candidates
+  const bool zonly = XF && mode == MODE_PURE && row_skips_draw(P, r);
+  const bool hist_mode = (mode == MODE_NUCLEUS || mode == MODE_PURE) && !zonly;
   if (hist_mode) {  // clear the histogram before the barrier of the max
     u32x4* h4 = reinterpret_cast<u32x4*>(S.a.hist);
 #pragma unroll
@@ -145,6 +148,36 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     }
   }
 
+  if (zonly) {
+    // ---- the chunk mass: exp2(fma(x, c, -ref)), fp32 per vector, fp64 across;
+    // a NaN logit is counted as the histogram's NaN bin would ----
+    double zs = 0.0, zh = 0.0;
+    uint32_t nanc = 0;
+    if (Mfin) {
+#pragma unroll
+      for (int i = 0; i < CK::NV; i++) {
+        float a = 0.0f, ah = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VPE; e++) {
+          const float x = C.x[i * VPE + e];
+          const float t = __builtin_fmaf(x, c, -ref);
+          const float m = __builtin_amdgcn_exp2f(t);
+          nanc += x != x ? 1u : 0u;
+          a += x != x ? 0.0f : m;
+          if constexpr (XF) ah += m > 0.0f && x == x ? m * t : 0.0f;
+        }
+        zs += (double)a;
+        zh += (double)ah;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NE; s++) nanc += C.x[s] != C.x[s] ? 1u : 0u;
+    }
+    sm.zsum = bred(zs, S.d, OpAdd{});
+    sm.nanbin = bred(nanc, S.u, OpAdd{});
+    if constexpr (XF) sm.zent = bred(zh, S.d3, OpAdd{});
+  }
+
   if (hist_mode) {
     // ---- exact mass histogram of the chunk ----
     uint32_t bins[NE / 2 + 1];
@@ -194,7 +227,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       sm.zsum = zs;
       sm.nanbin = nanc;
     }
-    if constexpr (HE) {
+    if (XF && P.entropy) {
       // the chunk's sum of e * log2(e), fp32 per vector, fp64 across
       double zh = 0.0;
       if (Mfin) {
@@ -978,7 +1011,7 @@ __device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_
   return 0;
 }
 
-template <int DT, int VPE, bool HE>
+template <int DT, int VPE, bool XF>
 __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g,
                                            const uint32_t epoch) {
   const KParams& P = F.k;
@@ -1048,7 +1081,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const double A2 = rreduce16(rfin ? a.ab2 * sc : 0.0, OpAdd{});
     // entropy rows: sum of e ln e over the row, against the row reference
     // (a chunk dl octaves under it: e 2^-dl, log2 e - dl), in log2 units
-    const double AH = HE ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
+    const double AH = (XF && P.entropy) ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
     if (lane < G) {
       S.cn[0][lane] = (int)a.n1;
       S.cn[1][lane] = (int)a.n2;
@@ -1305,7 +1338,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
   double lnZ = 0.0;
   if ((P.chosen_logprob || g.ntop > 0) && wv == 0 && Zfull > 0.0) lnZ = log(Zfull) + (double)Rref * 0.6931471805599453;
   const double lZ = lnZ - (double)Rref * 0.6931471805599453;  // ln Zfull
-  if (HE && tid == 0) {
+  if (XF && P.entropy && tid == 0) {
     // H = ln Z - sum(e ln e) / Z (the general kernel's NaN for rows without finite statistics)
     const bool fin = !has_nan && xmax != INFINITY && xmax != -INFINITY && __fdiv_rn(xmax, T) != INFINITY && Zfull > 0.0;
     P.entropy[r] = fin ? (float)(log(Zfull) - 0.6931471805599453 * S.md[3] / Zfull) : NAN;
@@ -1357,8 +1390,9 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 // ===========================================================================
 // The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
 // ===========================================================================
-// HE: the launch asks for the entropy output (its code is absent otherwise).
-template <int DT, int VPE, int NE, bool HE>
+// XF: the launch asks for the entropy output or may hold pure rows without a
+// draw (the mass-only path); the code of both is absent otherwise.
+template <int DT, int VPE, int NE, bool XF>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -1372,7 +1406,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   // launches (stream-ordered before this one), read by every chunk of the row
   // before any of them arrives
   const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
-  const int mode = chunk_phase<DT, VPE, NE, HE>(F, SU.c, r, j, g, epoch);
+  const int mode = chunk_phase<DT, VPE, NE, XF>(F, SU.c, r, j, g, epoch);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1390,7 +1424,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (!SU.c.mi[7] || threadIdx.x >= FT) return;
   acquire_agent();
   RG_STAMP(24);
-  const int reason = final_phase<DT, VPE, HE>(F, SU.f, r, g, epoch);
+  const int reason = final_phase<DT, VPE, XF>(F, SU.f, r, g, epoch);
   RG_STAMP(31);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }
