@@ -811,6 +811,17 @@ __device__ __forceinline__ void merge_lists_g(RgFinalS& S, int G, int D, int N0,
   else merge_lists<MAXG>(S, G, D, N0, N1, Rm);
 }
 
+// Counts, over the other 15 lanes of this lane's row of 16, the values greater
+// than v (gt) and at least v (ge): row rotations by 1 .. 15, in either direction
+// every other lane once.
+template <int D>
+__device__ __forceinline__ void row_rank16(uint32_t v, uint32_t& gt, uint32_t& ge) {
+  const uint32_t o = dpp_t<0x120 + D>(v, v);  // row_ror:D
+  gt += o > v ? 1u : 0u;
+  ge += o >= v ? 1u : 0u;
+  if constexpr (D < 15) row_rank16<D + 1>(v, gt, ge);
+}
+
 // Top-k rows: the merged list 0 without the merge.  Every chunk's list holds
 // its logits from the top down.  If j chunks each hold m entries at or above
 // z = t, and j m >= kc, the row's kc-th largest z is at least t: so for m =
@@ -825,25 +836,23 @@ __device__ __forceinline__ int select_topk_lists(RgFinalS& S, int G, int kc, int
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (wv == 0) {
-    // lanes 16 i + q: chunk q's m_i-th entry; a 32-step search per group of
-    // 16 lanes for the j_i-th largest (0 when fewer than j_i chunks hold m_i)
+    // lanes 16 i + q: chunk q's m_i-th entry (0 when chunk q holds fewer than
+    // m_i entries); the j_i-th largest of each row of 16 lanes is the value of
+    // the lanes with fewer than j_i values above theirs and at least j_i at or
+    // above
     const int grp = lane >> 4, q = lane & 15;
     const int m = (kc + (1 << grp) - 1) >> grp;
     const uint32_t jn = (uint32_t)((kc + m - 1) / m);
     uint32_t v = 0u;
     if (q < G && S.cn[0][q] >= m) v = key_z(S.lk[0][S.cb[0][q] + m - 1]);
-    uint32_t t = 0u;
-#pragma unroll 1
-    for (int b = 31; b >= 0; b--) {
-      const uint32_t c = t | (1u << b);
-      const uint64_t bal = __builtin_amdgcn_ballot_w64(v >= c);
-      const uint32_t cnt = (uint32_t)__builtin_popcount((uint32_t)(bal >> (16 * grp)) & 0xFFFFu);
-      t = cnt >= jn ? c : t;
-    }
+    uint32_t gt = 0u, ge = 1u;
+    row_rank16<1>(v, gt, ge);
+    uint32_t t = (gt < jn && jn <= ge) ? v : 0u;
     t = wreduce(t, OpMax{});
     if (lane == 0) S.mi[26] = (int)t;
   }
   __syncthreads();
+  RG_STAMP(22);
   const uint32_t zt = (uint32_t)S.mi[26];
   // compaction (in any order: the rank sort below fixes it)
   constexpr int EPT = LKM / FT;
@@ -874,6 +883,7 @@ __device__ __forceinline__ int select_topk_lists(RgFinalS& S, int G, int kc, int
     }
   }
   __syncthreads();
+  RG_STAMP(23);
   // rank sort (keys are distinct: the index is in the low word): each wave
   // ranks 64 entries at a time, against 64 keys per register load, read back
   // lane by lane

@@ -250,6 +250,7 @@ inline int dpp_src(int l, int ctrl) {
     const int n = ctrl - 0x110;
     return in - n >= 0 ? l - n : -1;
   }
+  if (ctrl >= 0x121 && ctrl <= 0x12F) return row + ((in - (ctrl - 0x120)) & 15);  // row_ror:n
   if (ctrl == 0x140) return row + 15 - in;
   if (ctrl == 0x141) return (l & ~7) + 7 - (l & 7);
   if (ctrl == 0x142) return row >= 16 ? row - 1 : -1;
