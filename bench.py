@@ -736,7 +736,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c3", "c3f", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c2m", "c3", "c3f", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
@@ -786,7 +786,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(),
+    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(), "c2m": lambda: W.c2_minp(),
             "c3": lambda: W.c3(), "c3f": lambda: W.c3(flat=True), "c5": lambda: W.c5()}[args.config]
     w = make()
     lib = _lib.load()
@@ -814,7 +814,8 @@ def main():
     # row-kind hint from the host-side parameters (as Sampler.sample_token
     # passes it): a large batch launches only the kernels its rows need
     from lps import row_kind_flags
-    io["flags"] = _lib.LPS_FLAG_GENERIC if args.generic else row_kind_flags(w.temperature, w.top_k)
+    io["flags"] = (_lib.LPS_FLAG_GENERIC if args.generic
+                   else row_kind_flags(w.temperature, w.top_k, w.min_p, w.typical_p))
     if args.allowed_frac is not None:
         from lps import pack_allowed
         gm = torch.Generator().manual_seed(11)
@@ -861,6 +862,8 @@ def main():
                         "c1g": "c1 greedy: B=1, V=151936 fp32, rep 1.1, T=0",
                         "c2": "c2: B=64, V=151936 bf16 N(0,3^2)+3 spikes, T~U[0.3,1.2], top_k in {0,20,50,100}, "
                               "top_p~U[0.8,1], presence 0.5, frequency 0.3 over 512 Zipf(1.1) ids/row",
+                        "c2m": "c2 with min-p: c2's rows and penalties, top_k 0, T>=0.3, min_p in "
+                               "{1e-3,0.02,0.05,0.1,0.2,0.3,1}, top_p in {1,0.9,0.5,0.95}, typical_p 0.6 on 1 row in 9",
                         "c3": "c3: B=256, V=151936 fp32 Student-t(3)*2, top_p 0.95, T 1",
                         "c3f": "c3 flat: B=256, V=151936 fp32 N(0,0.1^2), top_p 0.95, T 1",
                         "c5": "c5: B=512, V=151936 fp16, half greedy, half T 0.9/k 40/p 0.92, rep 1.05 over "

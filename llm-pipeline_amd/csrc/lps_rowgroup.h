@@ -51,9 +51,13 @@
 //
 // With the entropy output (an instantiation of its own), nucleus and pure rows
 // also sum e * log2(e) per chunk, and the finaliser gives H = ln Z - sum(e ln e) / Z.
+// The same instantiation takes min-p rows without top-k as nucleus rows (region
+// 1 also covers the bins that can hold the min-p boundary, and the finaliser
+// applies the exact test to the sorted candidates) and typical-p rows that top-p
+// or min-p cut (only the argmax is kept).
 // A row the kernel cannot finish exactly (e.g. a region wider than RW bins
-// holding more candidates than the lists take, min-p / typical-p without top-k,
-// entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
+// holding more candidates than the lists take, typical-p on a row no other
+// filter cut, entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
 // sampled by the general kernel, launched after this one with that status as
 // its filter.  (Sampling such rows in the same launch, in one tail workgroup
 // per row, was measured: the tail code in the kernel made every launch slower,
@@ -220,6 +224,9 @@ __device__ __forceinline__ T param_or(const T* p, int64_t i, T def) {
   const T v = *q;
   return p ? v : def;
 }
+// MT: the kernel takes min-p and typical-p rows without top-k (else they are
+// deferred).
+template <bool MT = true>
 __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   RowCfg g;
   g.T = param_or(P.temperature, r, P.temperature_def);
@@ -244,8 +251,14 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   if (g.greedy) mode = MODE_GREEDY;
   else if (!(g.T >= 1e-4f)) mode = MODE_DEFER;
   else if (g.topk > 0) mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
-  else if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
-  else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
+  else if (!MT) {
+    if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
+    else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
+  } else if (g.ntop > 0 || g.minp > 1.0f) mode = MODE_DEFER;
+  // (typical-p after a filter that removed ids keeps the argmax, which the
+  // finaliser takes; typical-p proper, on a full row, is deferred)
+  else if (g.typp < 1.0f && !(g.topp < 1.0f || g.minp > 0.0f)) mode = MODE_DEFER;
+  else mode = (g.topp < 1.0f || g.minp > 0.0f) ? MODE_NUCLEUS : MODE_PURE;
   if (P.entropy && mode != MODE_NUCLEUS && mode != MODE_PURE) mode = MODE_DEFER;
   if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
   g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
@@ -548,6 +561,27 @@ __device__ __forceinline__ uint32_t first_key_reaching(int thr, float c, float r
 // The smallest mass of bin b.
 __device__ __forceinline__ double bin_base(int b) {
   return ldexp(8388608.0 + (double)(b & 127) * 65536.0, (b >> 7) + HE0 - 150);
+}
+// Row bins [lo, hi] that can hold the min-p boundary (sampling.py:187-205: the
+// general kernel keeps z iff mass_f(z, zmax) >= min_p, for 0 < min_p <= 1).
+// The boundary's mass against the row reference R is min_p times the row
+// maximum's; every id the general rule keeps has its binned mass (emass against
+// its chunk's reference, rescaled) above that mass times 2^-E and every id it
+// drops has it under that mass times 2^E.  E bounds the rounding of both
+// computations, in log2 units: each step rounds a value of magnitude at most
+// W = |xmax c| + |log2 min_p| + 4 (the scaled logits near the boundary, the
+// references, their differences) by 2^-24 relative, and the two exp2 add a
+// few ulps; 2^-19 W is several times their sum.  False when the range leaves
+// the histogram (min_p under about 2^-30).
+__device__ __forceinline__ bool minp_bins(float minp, float xmax, float c, float R, int& lo, int& hi) {
+  const float W = fabsf(__fmul_rn(xmax, c)) + fabsf(log2f(minp)) + 4.0f;
+  const float E = ldexpf(W, -19);
+  const float tm = __fmul_rn(emass(xmax, c, R), minp);
+  const uint32_t bl = ebin(__fmul_rn(tm, __builtin_amdgcn_exp2f(-E)));
+  const uint32_t bh = ebin(__fmul_rn(tm, __builtin_amdgcn_exp2f(E)));
+  lo = (int)bl;
+  hi = (int)bh;
+  return bl != BELOW && bh < (uint32_t)HB_NAN && !(xmax != xmax);
 }
 
 // ---------------------------------------------------------------------------

@@ -245,6 +245,18 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       }
       sm.zent = bred(zh, S.d3, OpAdd{});
     }
+    if (XF && __builtin_expect(g.typp < 1.0f, 0) && Mfin) {
+      // typical-p rows (kept: the argmax, when a filter removed ids): the
+      // chunk's first id whose z equals its maximum's, fl(x / T) == fl(M / T)
+      const float xlo = collision_lo(M, T);
+      int best = 0x7FFFFFFF;
+      if (tm >= xlo) {
+#pragma unroll
+        for (int s = 0; s < NE; s++)
+          if (C.x[s] >= xlo) best = min(best, CK::index(v0, s));
+      }
+      sm.amax = bred(best, S.i1, OpMin{});
+    }
     // ---- publish the summary and the bins, one barrier among the row's chunks ----
     if (tid == 0) store_sum(sums + j, sm);
     RG_STAMP(4);
@@ -269,8 +281,13 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       const float R = wmax(af ? a.ref : -INFINITY);
       const double sc = af ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
       const double Z = wsum(af ? a.zsum * sc : 0.0);
+      const uint32_t mk = XF ? wmax(lane < G ? a.mkey : 0u) : 0u;
       if (lane < G) { S.rf[lane] = af ? a.ref : -INFINITY; }
-      if (lane == 0) { S.md[0] = Z; S.mf[0] = R; }
+      if (lane == 0) {
+        S.md[0] = Z;
+        S.mf[0] = R;
+        if constexpr (XF) S.mi[8] = (int)mk;
+      }
     }
     __syncthreads();
     const float R = S.mf[0];
@@ -329,7 +346,24 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     // ---- regions: bins whose cumulative interval meets the targets ----
     const double eps = 1e-6 * Z;
     const bool nuc = mode == MODE_NUCLEUS;
-    const double Pm = nuc ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
+    const bool topp_on = nuc && (!XF || g.topp < 1.0f);  // (without XF every nucleus row has top-p)
+    const double Pm = topp_on ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
+    // min-p rows: the bins that can hold the boundary [lom, him], and up to the
+    // lowest non-empty bin above them (which holds the least kept id when every
+    // id of [lom, him] is dropped): hm
+    const bool mp = XF && nuc && g.minp > 0.0f && rfin;
+    int lom = 0, him = -1, hm = -1;
+    if (__builtin_expect(mp, 0)) {
+      if (!minp_bins(g.minp, key2f((uint32_t)S.mi[8]), c, R, lom, him)) flags |= RF_REGION;
+      int bp = 1 << 30;
+#pragma unroll
+      for (int i = 0; i < HPT; i++) {
+        const int b = HB - 1 - HPT * tid - i;
+        if (b > him && b < HB_NAN && mrg[i] > 0.0) bp = min(bp, b);
+      }
+      bp = bred(bp, S.i2, OpMin{});
+      hm = bp < (1 << 30) ? bp : him;
+    }
     if (nuc) {
       // region 1: its highest bin holds the least prefix a, its lowest the
       // largest end a + m (cumulative mass at its top and bottom: the kept
@@ -340,12 +374,15 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
         const int b = HB - 1 - HPT * tid - i;
-        if (mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) {
+        if (topp_on && mrg[i] > 0.0 && a <= Pm + eps && a + mrg[i] >= Pm - eps) {
           lo = min(lo, b);
           hi = max(hi, b);
           atop = min(atop, __builtin_bit_cast(uint64_t, a));
           abot = max(abot, __builtin_bit_cast(uint64_t, a + mrg[i]));
         }
+        // (min-p rows: the cumulative mass at the top of bin hm and the bottom of bin lom)
+        if (mp && b == hm) S.mq[5] = __builtin_bit_cast(uint64_t, a);
+        if (mp && b == lom) S.mq[6] = __builtin_bit_cast(uint64_t, a + mrg[i]);
         a += mrg[i];
       }
       if (hi >= 0) {
@@ -356,12 +393,25 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       }
     }
     __syncthreads();
-    const int lo1 = nuc ? S.mi[0] : (1 << 30);
-    const int hi1 = nuc ? S.mi[1] : (1 << 30);
-    if (nuc && hi1 < 0) flags |= RF_REGION;
+    int lo1 = nuc ? S.mi[0] : (1 << 30);
+    int hi1 = nuc ? S.mi[1] : (1 << 30);
+    uint64_t q1t = S.mq[0], q1b = S.mq[1];
+    if (topp_on && hi1 < 0) flags |= RF_REGION;
+    if (__builtin_expect(mp, 0)) {
+      // the top-p cut entirely above [lom, hm]: top-p alone decides (every id
+      // it keeps passes min-p); entirely under it (or no top-p): min-p alone;
+      // else region 1 covers both
+      const double mt = __builtin_bit_cast(double, S.mq[5]), mb = __builtin_bit_cast(double, S.mq[6]);
+      if (!topp_on || mb < Pm - eps) {
+        lo1 = lom; hi1 = hm; q1t = S.mq[5]; q1b = S.mq[6];
+      } else if (!(mt > Pm + eps) && hi1 >= 0) {
+        lo1 = min(lo1, lom); hi1 = max(hi1, hm);
+        q1t = min(q1t, S.mq[5]); q1b = max(q1b, S.mq[6]);
+      }
+    }
     const float u = fminf(fmaxf(g.u == g.u ? g.u : 0.0f, 0.0f), 0.99999994f);
-    const double t_lo = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[0]) : (double)u * Z) - eps;
-    const double t_hi = (nuc ? (double)u * __builtin_bit_cast(double, S.mq[1]) : (double)u * Z) + eps;
+    const double t_lo = (nuc ? (double)u * __builtin_bit_cast(double, q1t) : (double)u * Z) - eps;
+    const double t_hi = (nuc ? (double)u * __builtin_bit_cast(double, q1b) : (double)u * Z) + eps;
     {
       int lo = 1 << 30, hi = -1;
       uint32_t nest = 0;  // elements in either region (an upper estimate: bin mass / the bin's least mass)
@@ -400,7 +450,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     // (past 3/4 of the row's lists, so that no chunk's share passes its own
     // list, or half of what the chunks' wave segments take)
     const bool crowded = __builtin_expect(nest > (uint32_t)min(CAPR * 3 / 4, G * CLMAX / 2), 0);
-    const bool refine = crowded && !S.mi[6] && rfin && (!nuc || (hi1 >= 0 && hi1 - lo1 < RW)) &&
+    const bool refine = crowded && !mp && !S.mi[6] && rfin && (!nuc || (hi1 >= 0 && hi1 - lo1 < RW)) &&
                         (!need2 || (hi2 >= 0 && hi2 - lo2 < RW));
     if (crowded && !refine) flags |= RF_WIDE;
     if (S.mi[6] && tid == 0) add_agent(ctr + CTR_FINE, 1u);
@@ -1084,7 +1134,12 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const int n1t = rdlane(i1, 15), n2t = rdlane(i2, 15), ot = rdlane(io, 15);
     if (stale) fl |= RF_SPLIT;
     RG_STAMP_DEP(20, fl);
-    const int am = rreduce16(in && a.mkey == mk ? (int)a.amax : 0x7FFFFFFF, OpMin{});
+    // (typical-p nucleus rows: the first id at the row's maximum z, over the
+    // chunks whose maximum has that z)
+    const bool tz = XF && mode == MODE_NUCLEUS && g.typp < 1.0f;
+    const float zr = tz ? __fdiv_rn(key2f(mk), T) : 0.0f;
+    const bool amc = tz ? __fdiv_rn(key2f(a.mkey), T) == zr : a.mkey == mk;
+    const int am = rreduce16(in && amc ? (int)a.amax : 0x7FFFFFFF, OpMin{});
     const double sc = rfin ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
     const double Z = rreduce16(rfin ? a.zsum * sc : 0.0, OpAdd{});
     const double A1 = rreduce16(rfin ? a.ab1 * sc : 0.0, OpAdd{});
@@ -1263,6 +1318,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     RG_STAMP(28);
     uint64_t ckey = 0;  // the last kept id's sort key
     int qc = -1, pd = -1;
+    bool targ = false;  // typical-p row keeping only its argmax
     if (nuc) {
       // sorted position p of the row is kept iff its exclusive prefix <= limit
       const uint64_t A1 = (uint64_t)(S.md[1] * kFix);
@@ -1270,9 +1326,26 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       uint64_t limit = (uint64_t)pl;
       if (limit >= Zfx) limit = Zfx - 1;
       // the first dropped position
-      const int lo = wave_first_true(0, N1, [&](int p) { return A1 + (p > 0 ? S.sc[0][p - 1] : 0ull) > limit; });
-      // the cut must fall inside the list: something kept, something dropped
-      if (lo == 0 || A1 + S.sc[0][N1 - 1] <= limit) return 6;
+      const bool tp = !XF || g.topp < 1.0f;
+      int lo = tp ? wave_first_true(0, N1, [&](int p) { return A1 + (p > 0 ? S.sc[0][p - 1] : 0ull) > limit; }) : N1;
+      bool mcut = false;  // region 1 holds the whole min-p boundary range
+      if (XF && __builtin_expect(g.minp > 0.0f, 0)) {
+        // min-p after top-p (sampling.py:187-205): keep z with mass_f(z, zmax)
+        // >= min_p, a prefix of the sorted order (exp2 is non-decreasing)
+        const float zmax = __fdiv_rn(xmax, T);
+        const int lm = wave_first_true(0, N1, [&](int p) {
+          return !(mass_f(key2f(key_z(S.sk[0][p])), zmax) >= g.minp);
+        });
+        int bl, bh;
+        mcut = minp_bins(g.minp, xmax, c, Rref, bl, bh) && lo1 <= bl * FSUB && hi1 >= bh * FSUB + FSUB - 1;
+        lo = min(lo, lm);
+      }
+      // the cut must fall inside the list: something kept, and the id after
+      // the list dropped (min-p drops every id under region 1 when it holds
+      // the boundary range)
+      if (XF ? (lo == 0 || (lo == N1 && !mcut && (!tp || A1 + S.sc[0][N1 - 1] <= limit)))
+             : (lo == 0 || A1 + S.sc[0][N1 - 1] <= limit))
+        return 6;
       qc = lo - 1;
       ckey = S.sk[0][qc];
       vkey = key_z(ckey);
@@ -1286,10 +1359,17 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)lo);
       ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
       cut = key2f(vkey);
+      if (XF && __builtin_expect(g.typp < 1.0f, 0)) {
+        // typical-p after top-p / min-p (sampling.py:207-238): a row that lost
+        // ids holds -inf, its entropy is NaN and only the argmax is kept; a
+        // row that kept every id takes the typical filter proper
+        if (kept_n >= V) return 14;
+        targ = true;
+      }
     } else {
       kept_n = -1;  // filled below when asked
     }
-    if (want2) {
+    if (want2 && !targ) {
       const uint64_t A2 = (uint64_t)(S.md[2] * kFix);
       uint64_t target = (uint64_t)((double)u * (double)Zkept);
       if (target >= Zkept) target = Zkept - 1;
@@ -1302,13 +1382,29 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       const bool ok = group_inside(__uint_as_float(S.sx[0][qc]), lo1, hi1);
       if (lane == 0) S.mi[12] = ok ? 1 : 0;
     }
-    if (wv == 1 && want2) {  // the drawn id's group inside region 2
+    if (wv == 1 && want2 && !targ) {  // the drawn id's group inside region 2
       const bool ok = group_inside(__uint_as_float(S.sx[1][pd]), lo2, hi2);
       if (lane == 0) S.mi[14] = ok ? 1 : 0;
     }
     __syncthreads();
     if (nuc && !S.mi[12]) return 8;
-    if (want2) {
+    if (XF && __builtin_expect(targ, 0)) {
+      // the argmax: the first id at the row's maximum z
+      if (gam == 0x7FFFFFFF) return 14;
+      const float zr = __fdiv_rn(xmax, T);
+      vkey = f2key(zr);
+      n_tie = 1;
+      tie_lim = gam;
+      Zkept = zmass_fix(zr, Rref);
+      cut = zr;
+      ties = 1;
+      kept_n = 1;
+      if (want2) {
+        token = gam;
+        chosen_z = zr;
+        chosen_x = P.chosen_logprob ? penal_logit<DT>(P, g, row, r, gam, S) : NAN;
+      }
+    } else if (want2) {
       if (!S.mi[14]) return 11;
       const uint64_t dkey = S.sk[1][pd];
       token = (int64_t)key_index(dkey);
@@ -1400,8 +1496,9 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 // ===========================================================================
 // The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
 // ===========================================================================
-// XF: the launch asks for the entropy output or may hold pure rows without a
-// draw (the mass-only path); the code of both is absent otherwise.
+// XF: the launch asks for the entropy output, may hold pure rows without a
+// draw (the mass-only path), or may hold min-p / typical-p rows without top-k;
+// the code of all three is absent otherwise (such rows are then deferred).
 template <int DT, int VPE, int NE, bool XF>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;
@@ -1410,7 +1507,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   const int j = slot % F.G;
   if (r >= F.k.R) return;
   if (F.heavy_first) r = heavy_first_row(F.k, r);
-  const RowCfg g = row_cfg(F.k, r);
+  const RowCfg g = row_cfg<XF>(F.k, r);
   if (F.skip_topk && stream_takes(g)) return;
   // the row's launch epoch: written only by the finalisers of earlier
   // launches (stream-ordered before this one), read by every chunk of the row

@@ -254,7 +254,7 @@ __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   // would queue behind the chunks the first waves issued)
   __asm__ volatile("" ::: "memory");
   RowCfg g0;
-  if (wv == 0) g0 = row_cfg(P, r);
+  if (wv == 0) g0 = row_cfg<false>(P, r);  // (the rows it takes: greedy and top-k)
   __asm__ volatile("" ::: "memory");
   // chunks: each wave takes chunks wv, wv + 8, wv + 16, then the next free one
   // (a counter in LDS), so waves that run faster take more of the row

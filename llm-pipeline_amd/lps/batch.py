@@ -98,34 +98,42 @@ class SampleOutput:
     row_path: Optional[torch.Tensor] = None         # int32 [B]: 0 fast kernel, 1 general kernel
 
 
-def row_kind_flags(temperature, top_k) -> int:
+def row_kind_flags(temperature, top_k, min_p=None, typical_p=None) -> int:
     """Row-kind hint flags for ``lps_sample`` from host-side per-row
-    temperatures and top-k values (scalars, sequences or CPU tensors):
-    ``LPS_FLAG_ROWS_TOPK`` when every row is greedy (temperature <= 0) or has
-    top_k > 0, ``LPS_FLAG_ROWS_NUCLEUS`` when none is, else 0 (also for device
-    tensors, whose values the host does not hold).  The hints only choose which
-    kernels a large batch launches; a row that breaks one is still sampled
-    exactly, by the general kernel."""
+    parameters (scalars, sequences or CPU tensors): ``LPS_FLAG_ROWS_TOPK`` when
+    every row is greedy (temperature <= 0) or has top_k > 0,
+    ``LPS_FLAG_ROWS_NUCLEUS`` when none is; ``LPS_FLAG_ROWS_NO_MINP_TYPICAL``
+    when ``min_p`` and ``typical_p`` are given and no row has min_p > 0 or
+    typical_p < 1.  Nothing is hinted from device tensors, whose values the
+    host does not hold.  The hints only choose which kernels (and which build
+    of the row-group kernel) a launch runs; a row that breaks one is still
+    sampled exactly, by the general kernel."""
     def host(v):
         if isinstance(v, torch.Tensor):
             return v.reshape(-1) if v.device.type == "cpu" else None
         return torch.as_tensor(v).reshape(-1)
+    flags = 0
+    if min_p is not None and typical_p is not None:
+        mp, tp = host(min_p), host(typical_p)
+        if mp is not None and tp is not None and not bool((mp.float() > 0).any()) \
+                and not bool((tp.float() < 1).any()):
+            flags |= _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
     T, k = host(temperature), host(top_k)
     if T is None or k is None:
-        return 0
+        return flags
     n = max(T.numel(), k.numel())
     if n == 0:
-        return 0
+        return flags
     T = T.float().expand(n) if T.numel() == 1 else T.float()
     k = k.long().expand(n) if k.numel() == 1 else k.long()
     if T.numel() != n or k.numel() != n:
-        return 0
+        return flags
     topk_row = ~(T > 0) | (k > 0)
     if bool(topk_row.all()):
-        return _lib.LPS_FLAG_ROWS_TOPK
+        return flags | _lib.LPS_FLAG_ROWS_TOPK
     if not bool(topk_row.any()):
-        return _lib.LPS_FLAG_ROWS_NUCLEUS
-    return 0
+        return flags | _lib.LPS_FLAG_ROWS_NUCLEUS
+    return flags
 
 
 def pad_histories(histories: Iterable[Sequence[int]], device) -> tuple:
@@ -302,8 +310,10 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_ties = D.ptr(out.kept_ties)
     a.kept_count = D.ptr(out.kept_count)
     a.row_path = D.ptr(out.row_path)
-    if row_kind_hint & ~(_lib.LPS_FLAG_ROWS_TOPK | _lib.LPS_FLAG_ROWS_NUCLEUS):
-        raise ValueError("row_kind_hint takes LPS_FLAG_ROWS_TOPK / LPS_FLAG_ROWS_NUCLEUS only")
+    hints = _lib.LPS_FLAG_ROWS_TOPK | _lib.LPS_FLAG_ROWS_NUCLEUS | _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
+    if row_kind_hint & ~hints:
+        raise ValueError("row_kind_hint takes LPS_FLAG_ROWS_TOPK / LPS_FLAG_ROWS_NUCLEUS / "
+                         "LPS_FLAG_ROWS_NO_MINP_TYPICAL only")
     a.flags = ((0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
                | row_kind_hint)
     if noalloc:

@@ -93,7 +93,7 @@ class Sampler:
         dev = logits.device
         hint = 0
         if params is None:
-            hint = row_kind_flags(config.temperature, config.top_k)
+            hint = row_kind_flags(config.temperature, config.top_k, config.min_p, config.typical_p)
             params = SamplingParams.build(
                 B, dev, temperature=config.temperature, top_k=config.top_k, top_p=config.top_p,
                 min_p=config.min_p, typical_p=config.typical_p, repetition_penalty=config.repetition_penalty,
@@ -142,7 +142,8 @@ class Sampler:
         k = max(1, int(math.exp(previous_entropy))) if previous_entropy > 0 else 0
         # the reference's _apply_top_k clamps k to the vocabulary (sampling.py:151)
         k = min(k, logits.shape[-1])
-        out = sample_rows(logits, SamplingParams.build(B, dev, temperature=T, top_k=k), uniforms)
+        out = sample_rows(logits, SamplingParams.build(B, dev, temperature=T, top_k=k), uniforms,
+                          row_kind_hint=row_kind_flags(T, k, 0.0, 1.0))
         raise_on_status(out.status)
         return out.tokens, previous_entropy
 

@@ -39,7 +39,7 @@ from typing import Callable, List, Optional, Sequence, Tuple, Union
 import torch
 
 from . import _device as D
-from .batch import SamplingParams, sample_rows
+from .batch import SamplingParams, row_kind_flags, sample_rows
 from .speculative import SpecDecStats, spec_verify
 
 Prompts = Union[torch.Tensor, Sequence[torch.Tensor]]
@@ -80,6 +80,11 @@ def _plain_params(n: int, temperature: float, dev) -> SamplingParams:
     """``softmax(logits / T)`` with nothing filtered (``speculative.py:50-57``);
     ``T <= 0`` samples the argmax."""
     return SamplingParams.build(n, dev, temperature=max(float(temperature), 0.0), top_k=0, top_p=1.0)
+
+
+def _plain_hint(temperature: float) -> int:
+    """The row-kind hint of ``_plain_params`` rows (every row alike)."""
+    return row_kind_flags(max(float(temperature), 0.0), 0, 0.0, 1.0)
 
 
 def _round_uniforms(uniforms, generator, rnd: int, rows: List[int], width: int, dev) -> torch.Tensor:
@@ -149,6 +154,7 @@ def speculative_decode_batched(target_forward: Callable[[torch.Tensor], torch.Te
         x = torch.where(torch.arange(L + k, device=dev).unsqueeze(0) < ld.unsqueeze(1), x, pad_token_id)
         ar = torch.arange(A, device=dev)
         params = _plain_params(A, temperature, dev)
+        hint = _plain_hint(temperature)
         d_all = None                                                          # [A, k, V] draft rows
         d_tok = torch.empty((A, k), dtype=torch.int64, device=dev)
         for s in range(k):
@@ -156,7 +162,7 @@ def speculative_decode_batched(target_forward: Callable[[torch.Tensor], torch.Te
             if d_all is None:
                 d_all = torch.empty((A, k, logits.shape[-1]), dtype=logits.dtype, device=dev)
             d_all[:, s] = logits[ar, ld - 1 + s]
-            d_tok[:, s] = sample_rows(d_all[:, s], params, u[:, s].contiguous()).tokens
+            d_tok[:, s] = sample_rows(d_all[:, s], params, u[:, s].contiguous(), row_kind_hint=hint).tokens
             x[ar, ld + s] = d_tok[:, s]
         t_logits = _logits_on(target_forward(x), dev)
         t_rows = t_logits[ar.unsqueeze(1), (ld - 1).unsqueeze(1) + kk.unsqueeze(0)]   # [A, k+1, V]
@@ -235,12 +241,13 @@ def mtp_speculative_decode_batched(main_forward_with_hidden: Callable[[torch.Ten
         x, lens = _padded([seqs[i] for i in rows], 2, pad_token_id)   # room for x_next and the draft
         ar = torch.arange(A, device=dev)
         params = _plain_params(A, temperature, dev)
+        hint = _plain_hint(temperature)
         logits, hidden = main_forward_with_hidden(x[:, : int(lens.max())])
         logits = _logits_on(logits, dev)
-        x_next = sample_rows(logits[ar, lens - 1], params, u[:, 0].contiguous()).tokens
+        x_next = sample_rows(logits[ar, lens - 1], params, u[:, 0].contiguous(), row_kind_hint=hint).tokens
         h_last = hidden[ar.to(hidden.device), (lens - 1).to(hidden.device)].unsqueeze(1)
         mtp_logits = _logits_on(mtp_head(h_last, x_next.to(hidden.device).unsqueeze(-1)), dev)     # [A, 1, V]
-        x_draft = sample_rows(mtp_logits[:, 0], params, u[:, 1].contiguous()).tokens
+        x_draft = sample_rows(mtp_logits[:, 0], params, u[:, 1].contiguous(), row_kind_hint=hint).tokens
         x[ar, lens] = x_next
         nxt = x_next.cpu().tolist()
         verify = []

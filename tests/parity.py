@@ -128,7 +128,7 @@ def check_rows(w, out, rows=None, report: RowReport = None, lp=False) -> RowRepo
 
 def run_workload(w, dev, path="auto", **kw):
     from lps import SamplingParams, row_kind_flags, sample_rows
-    kw.setdefault("row_kind_hint", row_kind_flags(w.temperature, w.top_k))
+    kw.setdefault("row_kind_hint", row_kind_flags(w.temperature, w.top_k, w.min_p, w.typical_p))
     p = SamplingParams(w.temperature.to(dev), w.top_k.to(dev), w.top_p.to(dev), w.min_p.to(dev),
                        w.typical_p.to(dev), w.rep.to(dev), w.pres.to(dev), w.freq.to(dev))
     hist = w.histories.to(dev) if w.histories is not None else None

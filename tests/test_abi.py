@@ -182,6 +182,22 @@ def test_sampling_params_and_histories_host():
     assert h.shape == (3, 3) and n.tolist() == [3, 0, 1] and h[2, 0].item() == 7
 
 
+def test_row_kind_flags():
+    """Row-kind hints from host-side parameters; nothing is hinted from values
+    the host does not hold, and no min-p / typical-p hint without both."""
+    from lps import _lib, row_kind_flags
+    TOPK, NUC, NMT = _lib.LPS_FLAG_ROWS_TOPK, _lib.LPS_FLAG_ROWS_NUCLEUS, _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
+    assert row_kind_flags([0.0, 1.0], [0, 5]) == TOPK
+    assert row_kind_flags(1.0, 0) == NUC
+    assert row_kind_flags([0.0, 1.0], [0, 0]) == 0
+    assert row_kind_flags(1.0, 0, 0.0, 1.0) == NUC | NMT
+    assert row_kind_flags(torch.tensor([0.0, 0.7]), torch.tensor([0, 9]), [0.0, 0.0], [1.0, 1.0]) == TOPK | NMT
+    assert row_kind_flags(1.0, 0, [0.0, 0.05], 1.0) == NUC
+    assert row_kind_flags(1.0, 0, 0.0, [1.0, 0.9]) == NUC
+    assert row_kind_flags(1.0, 0, 0.0) == NUC
+    assert _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL == 16
+
+
 def test_lm_head_argument_errors(lib):
     """Argument checks of lps_lm_head happen before any launch (no GPU)."""
     from lps import _lib

@@ -300,6 +300,27 @@ def test_entropy_on_the_row_group_kernel(dev, dtype):
     PY.check_rows(wn, outn)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_min_p_on_the_row_group_kernel(dev, dtype):
+    """min-p without top-k (sampling.py:187-205) at c2's shape (B = 64, V =
+    151936: four chunks per row, with c2's penalties), alone and after top-p,
+    min_p from 1e-3 to 1; and typical-p after top-p / min-p, which keeps the
+    argmax (sampling.py:231-234).  The row-group kernel takes these rows
+    (region 1 covers the bins that can hold the min-p boundary and the
+    finaliser applies the general kernel's test to the sorted candidates):
+    at most 2 of the 64 are deferred, and every kept set and draw equals the
+    oracle's."""
+    from tests.test_gpu_stream import _deferral_reasons
+    w = W.c2_minp(dtype)
+    B = w.B
+    out = PY.run_workload(w, dev)
+    off = (out.row_path.cpu() != 0).nonzero().flatten().tolist()
+    print(f"min-p rows {dtype}: off the row-group kernel {off}, reasons {_deferral_reasons(out, dev, B)}", flush=True)
+    assert len(off) <= 2
+    rep = PY.check_rows(w, out)
+    print(f"min-p rows {dtype}: {rep}", flush=True)
+
+
 def test_mirostat_long_low_entropy_loop(dev):
     """A peaked row (entropy below tau) makes prev grow every step, so
     k = int(exp(prev)) passes the vocabulary size; the reference's top-k

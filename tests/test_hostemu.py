@@ -120,23 +120,29 @@ def _run(exe, w, tmp_path, flags=0, workspace=True, logprobs=False, n_top=0, ent
     return res
 
 
+@pytest.mark.parametrize("hint", [0, 16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_v64_mixed_params(run_case, tmp_path, dtype):
+def test_v64_mixed_params(run_case, tmp_path, dtype, hint):
     """The inputs of test_small_vocab_mixed_params at V = 64 (16-byte vector
     rows, one chunk): the row-group kernel at G = 1, then the general kernel on
-    the rows it defers (top_k beyond V, top_p <= 0, T < 1e-4 ...).  In bounds,
-    and equal to the oracle."""
+    the rows it defers (top_k beyond V, top_p <= 0, T < 1e-4 ...); both builds
+    of the row-group kernel (hint 16, LPS_FLAG_ROWS_NO_MINP_TYPICAL: the one
+    without the min-p / typical-p code).  In bounds, and equal to the oracle."""
     w = _small(64, 24, dtype, seed=64 + int(dtype == torch.bfloat16) * 7)
-    out = _run(run_case, w, tmp_path)
+    out = _run(run_case, w, tmp_path, flags=hint)
     PY.check_rows(w, out)
 
 
+@pytest.mark.parametrize("hint", [0, 16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_v64_deferred_rows(run_case, tmp_path, dtype):
-    """16-bit V = 64 rows the row-group kernel defers in its chunk phase (min-p
-    and typical-p without top-k, top_k past 256) or finishes itself: the
-    deferred rows are sampled by the general kernel launched after it (16-byte
-    vector loads), the others by the row-group kernel."""
+def test_v64_deferred_rows(run_case, tmp_path, dtype, hint):
+    """16-bit V = 64 rows the row-group kernel defers in its chunk phase (top_k
+    past 256, typical-p on a row no other filter cut) or finishes itself
+    (min-p without top-k, typical-p after top-p): the deferred rows are sampled
+    by the general kernel launched after it (16-byte vector loads), the others
+    by the row-group kernel.  With hint 16 (LPS_FLAG_ROWS_NO_MINP_TYPICAL, wrong
+    for these rows) the row-group kernel runs without the min-p / typical-p
+    code and defers those rows too: still sampled exactly."""
     w = _small(64, 24, dtype, seed=71)
     i = torch.arange(24)
     w.top_k = torch.where(i % 4 == 1, torch.tensor(300, dtype=torch.int32), w.top_k)
@@ -144,8 +150,12 @@ def test_v64_deferred_rows(run_case, tmp_path, dtype):
     w.typical_p = torch.where(i % 4 == 3, torch.tensor(0.8), w.typical_p)
     w.top_k = torch.where(i % 4 >= 2, torch.tensor(0, dtype=torch.int32), w.top_k)
     w.temperature = torch.where(i % 4 != 0, torch.tensor(0.9), w.temperature)
-    out = _run(run_case, w, tmp_path)
-    assert (out.row_path[i % 4 != 0] == 1).all() and (out.row_path[i % 4 == 0] == 0).all()
+    out = _run(run_case, w, tmp_path, flags=hint)
+    print("paths", out.row_path.tolist(), out.reasons)
+    assert (out.row_path[i % 4 == 1] == 1).all() and (out.row_path[i % 4 == 0] == 0).all()
+    assert (out.row_path[(i % 4 == 3) & (w.top_p >= 1)] == 1).all()
+    if hint:
+        assert (out.row_path[i % 4 != 0] == 1).all()
     PY.check_rows(w, out)
 
 
@@ -231,3 +241,37 @@ def test_entropy_pure_rows(run_case, tmp_path):
         h = float(-(p * torch.log_softmax(z, 0)).sum())
         assert abs(float(out.entropy[i]) - h) <= 2e-5 * max(1.0, abs(h)), (i, float(out.entropy[i]), h)
     assert np.isnan(float(out.entropy[4])) and np.isnan(float(out.entropy[5]))
+
+
+def _minp_rows(V, dtype, seed):
+    """Rows without top-k that the row-group kernel takes with min-p: N(0,
+    sigma^2) logits (sigma 1, 2.5, 4: flatter to peaked), min_p from 1e-3 to
+    1, alone (top_p 1) and after top_p 0.9 / 0.5 / 0, T 0.7 to 1.3; and
+    typical-p after top-p / min-p (the argmax)."""
+    B = 24
+    g = torch.Generator().manual_seed(seed)
+    i = torch.arange(B)
+    sig = torch.tensor([1.0, 2.5, 4.0])[i % 3]
+    x = (torch.randn((B, V), generator=g) * sig.view(-1, 1)).to(dtype)
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    T = torch.tensor([0.7, 1.0, 1.3, 1.0])[i % 4]
+    mp = torch.tensor([0.001, 0.02, 0.1, 0.5, 1.0, 0.05])[i % 6]
+    p = torch.tensor([1.0, 0.9, 1.0, 0.5, 0.0, 1.0, 0.9, 1.0])[i % 8]
+    typ = torch.where(i % 7 == 3, torch.tensor(0.7), torch.tensor(1.0))
+    return W.Workload("minp", x, T, f(0, torch.int32), p, mp, typ, f(1.0), f(0.0), f(0.0), None, None,
+                      torch.rand((B,), generator=g))
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960), (torch.float16, 40960)])
+def test_min_p_rows(run_case, tmp_path, dtype, V):
+    """min-p without top-k on one-chunk rows of the row-group kernel (region 1
+    covers the bins that can hold the min-p boundary; the finaliser applies the
+    general kernel's test exactly), with and without top-p, and typical-p after
+    them (the argmax): in bounds, and the kept sets and draws equal the
+    oracle's.  Rows whose region is crowded are deferred (reason 2 + RF_WIDE)."""
+    w = _minp_rows(V, dtype, seed=31 + V)
+    out = _run(run_case, w, tmp_path)
+    off = [i for i in range(w.B) if int(out.row_path[i]) != 0]
+    print("rows off the row-group kernel:", off, out.reasons)
+    assert len(off) <= 4, (off, out.reasons)
+    PY.check_rows(w, out)

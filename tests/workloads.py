@@ -88,6 +88,24 @@ def c2(B=64, V=V_QWEN3, seed=2, H=512) -> Workload:
                     _full(B, 0.3), hist, _full(B, H, torch.int32), torch.rand((B,), generator=g))
 
 
+def c2_minp(dtype=torch.bfloat16) -> Workload:
+    """c2's rows and penalties with min-p instead of top-k: top_k 0, T clamped to
+    >= 0.3, min_p cycling 1e-3 / 0.02 / 0.05 / 0.1 / 0.3 / 1 / 0.05 / 0.2, top_p
+    cycling 1 / 0.9 / 1 / 0.5 / 0.95, typical_p 0.6 on every ninth row (after
+    top-p / min-p: the argmax)."""
+    w = c2()
+    w.name = "c2_minp"
+    w.logits = w.logits.to(dtype)
+    B = w.B
+    i = torch.arange(B)
+    w.top_k = torch.zeros(B, dtype=torch.int32)
+    w.temperature = w.temperature.clamp(min=0.3)
+    w.min_p = torch.tensor([0.001, 0.02, 0.05, 0.1, 0.3, 1.0, 0.05, 0.2])[i % 8]
+    w.top_p = torch.tensor([1.0, 0.9, 1.0, 0.5, 0.95])[i % 5]
+    w.typical_p = torch.where(i % 9 == 4, torch.tensor(0.6), torch.tensor(1.0))
+    return w
+
+
 def c3(B=256, V=V_QWEN3, seed=3, flat=False) -> Workload:
     """B=256 fp32 Student-t(3)*2 (or flat N(0, 0.1^2)); top_p 0.95, T 1, no penalties."""
     g = torch.Generator().manual_seed(seed)
