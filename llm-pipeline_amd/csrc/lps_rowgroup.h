@@ -53,11 +53,13 @@
 // also sum e * log2(e) per chunk, and the finaliser gives H = ln Z - sum(e ln e) / Z.
 // The same instantiation takes min-p rows without top-k as nucleus rows (region
 // 1 also covers the bins that can hold the min-p boundary, and the finaliser
-// applies the exact test to the sorted candidates) and typical-p rows that top-p
-// or min-p cut (only the argmax is kept).
+// applies the exact test to the sorted candidates), typical-p rows that top-p or
+// min-p cut (only the argmax is kept), and typical-p rows without other filters
+// (the cut from the row's entropy: the argmax, every logit, a threshold cut
+// like min-p's, or a cut under the histogram that the chunks count).
 // A row the kernel cannot finish exactly (e.g. a region wider than RW bins
-// holding more candidates than the lists take, typical-p on a row no other
-// filter cut, entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
+// holding more candidates than the lists take, typical-p after a top-p / min-p
+// that removed nothing, entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
 // sampled by the general kernel, launched after this one with that status as
 // its filter.  (Sampling such rows in the same launch, in one tail workgroup
 // per row, was measured: the tail code in the kernel made every launch slower,
@@ -158,7 +160,10 @@ struct RgSum {
   uint32_t nab1;      // nucleus: elements above region 1
   uint32_t nanbin;    // nucleus: NaN / +inf masses seen
   double zsum;        // chunk mass: sum of exp2(fma(x, c, -ref))
-  double ab1;         // nucleus: exact mass above region 1 (chunk reference)
+  double ab1;         // nucleus: exact mass above region 1 (chunk reference).  Typical-p rows
+                      // without other filters (tw_pack): at the barrier, the chunk's -inf
+                      // logits and its least logit's key; at arrival, for a cut under the
+                      // histogram (no region 1), the logits it drops and the least kept key
   double ab2;         // nucleus: exact mass above region 2
   double zent;        // entropy rows: sum of e * log2(e), e = exp2(fma(x, c, -ref)) (chunk reference)
   int32_t reg[4];     // nucleus: the regions lo1, hi1, lo2, hi2 (row fine bins, efine scale; the same
@@ -166,6 +171,11 @@ struct RgSum {
 };
 static_assert(sizeof(RgSum) % 8 == 0 && offsetof(RgSum, tag) == 0, "8-byte words, the tag first");
 __device__ __forceinline__ void store_sum(RgSum* d, const RgSum& a) { *d = a; }
+__device__ __forceinline__ double tw_pack(uint32_t n, uint32_t key) {
+  return __builtin_bit_cast(double, ((uint64_t)key << 32) | n);
+}
+__device__ __forceinline__ uint32_t tw_n(double v) { return (uint32_t)__builtin_bit_cast(uint64_t, v); }
+__device__ __forceinline__ uint32_t tw_key(double v) { return (uint32_t)(__builtin_bit_cast(uint64_t, v) >> 32); }
 // Summary tag: the row's launch epoch (a per-row count in the workspace that
 // each launch's finaliser advances, so a record left by an earlier launch
 // carries an older one; zero-filled memory never matches, the epochs start at
@@ -255,10 +265,9 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
     if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
     else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;
   } else if (g.ntop > 0 || g.minp > 1.0f) mode = MODE_DEFER;
-  // (typical-p after a filter that removed ids keeps the argmax, which the
-  // finaliser takes; typical-p proper, on a full row, is deferred)
-  else if (g.typp < 1.0f && !(g.topp < 1.0f || g.minp > 0.0f)) mode = MODE_DEFER;
-  else mode = (g.topp < 1.0f || g.minp > 0.0f) ? MODE_NUCLEUS : MODE_PURE;
+  // (typical-p after a filter that removed ids keeps the argmax; on a full row
+  // it is a threshold cut like min-p's)
+  else mode = (g.topp < 1.0f || g.minp > 0.0f || g.typp < 1.0f) ? MODE_NUCLEUS : MODE_PURE;
   if (P.entropy && mode != MODE_NUCLEUS && mode != MODE_PURE) mode = MODE_DEFER;
   if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
   g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
@@ -537,51 +546,90 @@ __device__ __forceinline__ double fine_mass(int f, unsigned long long acc) {
   const double m = __builtin_fma((double)(cnt * (uint32_t)(0x8000 + (f & 0x7FFF))), 256.0, (double)low);
   return cnt ? ldexp(m, (f >> 15) + HE0 - 150) : 0.0;
 }
-// First float key k (in f2key order, over the non-NaN keys) whose logit
-// reaches fine bin thr: efine(emass(key2f(k), c, ref)) >= thr.  The hardware
-// exp2 is non-decreasing over every fp32 input (lps_selftest_exp2_monotone)
-// and fma(x, c, -ref) is non-decreasing in x for c > 0, so the predicate is
-// false then true over the keys; +inf's key satisfies it for thr < 2^22.  One
-// wave searches 64 keys per round (6 rounds); every lane of the wave calls it
-// with the same arguments.
-__device__ __forceinline__ uint32_t first_key_reaching(int thr, float c, float ref) {
+// First float key k (in f2key order, over the non-NaN keys, from -inf's
+// exclusive to +inf's) where a predicate of the logit, false then true over
+// the keys, holds.  One wave searches 64 keys per round (6 rounds); every lane
+// of the wave calls it with the same arguments.
+// first_key_reaching: the first whose logit reaches fine bin thr,
+// efine(emass(key2f(k), c, ref)) >= thr.  The hardware exp2 is non-decreasing
+// over every fp32 input (lps_selftest_exp2_monotone) and fma(x, c, -ref) is
+// non-decreasing in x for c > 0; +inf's key satisfies it for thr < 2^22.
+template <class Pr>
+__device__ __forceinline__ uint32_t first_key_where(Pr pred) {
   constexpr uint32_t kNegInfK = 0x007FFFFFu, kPosInfK = 0xFF800000u;
   const uint64_t l1 = (uint64_t)(threadIdx.x & 63) + 1u;
-  uint32_t lo = kNegInfK, hi = kPosInfK;  // the predicate fails at lo (unless thr is negative), holds at hi
+  uint32_t lo = kNegInfK, hi = kPosInfK;  // the predicate is taken to fail at lo and to hold at hi
   while (hi - lo > 1u) {
     const uint64_t span = hi - lo, step = (span + 63u) >> 6;
     const uint32_t k = lo + (uint32_t)(l1 * step < span ? l1 * step : span);
-    const uint64_t m = __builtin_amdgcn_ballot_w64(efine(emass(key2f(k), c, ref)) >= thr);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pred(key2f(k)));
     const uint64_t j = m ? (uint64_t)__builtin_ctzll(m) : 63u;
     hi = lo + (uint32_t)((j + 1u) * step < span ? (j + 1u) * step : span);
     lo = lo + (uint32_t)(j * step);
   }
   return hi;
 }
+__device__ __forceinline__ uint32_t first_key_reaching(int thr, float c, float ref) {
+  return first_key_where([&](float x) { return efine(emass(x, c, ref)) >= thr; });
+}
 // The smallest mass of bin b.
 __device__ __forceinline__ double bin_base(int b) {
   return ldexp(8388608.0 + (double)(b & 127) * 65536.0, (b >> 7) + HE0 - 150);
 }
-// Row bins [lo, hi] that can hold the min-p boundary (sampling.py:187-205: the
-// general kernel keeps z iff mass_f(z, zmax) >= min_p, for 0 < min_p <= 1).
-// The boundary's mass against the row reference R is min_p times the row
-// maximum's; every id the general rule keeps has its binned mass (emass against
-// its chunk's reference, rescaled) above that mass times 2^-E and every id it
-// drops has it under that mass times 2^E.  E bounds the rounding of both
-// computations, in log2 units: each step rounds a value of magnitude at most
-// W = |xmax c| + |log2 min_p| + 4 (the scaled logits near the boundary, the
-// references, their differences) by 2^-24 relative, and the two exp2 add a
-// few ulps; 2^-19 W is several times their sum.  False when the range leaves
-// the histogram (min_p under about 2^-30).
-__device__ __forceinline__ bool minp_bins(float minp, float xmax, float c, float R, int& lo, int& hi) {
-  const float W = fabsf(__fmul_rn(xmax, c)) + fabsf(log2f(minp)) + 4.0f;
+// Row bins [lo, hi] that can hold a threshold cut "mass relative to the row
+// maximum >= ratio": the general kernel's min-p rule (keep z iff mass_f(z,
+// zmax) >= min_p, ratio = min_p, 0 < min_p <= 1; sampling.py:187-205) and its
+// typical-p rule on a full row (keep z iff z - zmax >= dmin, ratio =
+// exp(dmin); sampling.py:207-238).  The boundary's mass against the row
+// reference R is ratio times the row maximum's; every id the rule keeps has its
+// binned mass (emass against its chunk's reference, rescaled) above that mass
+// times 2^-E and every id it drops has it under that mass times 2^E.  E bounds
+// the rounding of both computations, in log2 units: each step rounds a value of
+// magnitude at most W = |xmax c| + |log2 ratio| + 4 (the scaled logits near
+// the boundary, the references, their differences) by 2^-24 relative, and the
+// two exp2 add a few ulps; 2^-19 W is several times their sum.  False when the
+// range leaves the histogram (a ratio under about 2^-30, or 0).
+__device__ __forceinline__ bool cut_bins(float ratio, float xmax, float c, float R, int& lo, int& hi) {
+  const float W = fabsf(__fmul_rn(xmax, c)) + fabsf(log2f(ratio)) + 4.0f;
   const float E = ldexpf(W, -19);
-  const float tm = __fmul_rn(emass(xmax, c, R), minp);
+  const float tm = __fmul_rn(emass(xmax, c, R), ratio);
   const uint32_t bl = ebin(__fmul_rn(tm, __builtin_amdgcn_exp2f(-E)));
   const uint32_t bh = ebin(__fmul_rn(tm, __builtin_amdgcn_exp2f(E)));
   lo = (int)bl;
   hi = (int)bh;
   return bl != BELOW && bh < (uint32_t)HB_NAN && !(xmax != xmax);
+}
+// Typical-p rows without other filters, by what their cut keeps (decided
+// alike in every chunk and in the finaliser, from the same summaries):
+enum {
+  TYP_ARGMAX = 0,  // the row holds -inf (NaN entropy) or the cut keeps nothing: only the argmax
+  TYP_ALL = 1,     // the cut keeps the least logit, so every logit: a pure row
+  TYP_CUT = 2,     // the boundary lies in the histogram, in bins [lo, hi]: a threshold cut
+  TYP_LOW = 3,     // the boundary lies under the histogram: every binned logit is kept, a pure
+                   // draw; the chunks count the few logits it drops
+  TYP_WIDE = 4     // the boundary's range straddles the histogram's bottom: deferred
+};
+__device__ __forceinline__ int typical_case(uint32_t ninf, double dmin, float xmin, float xmax, float T, float c,
+                                            float R, int& lo, int& hi) {
+  if (ninf > 0u || !(dmin <= 0.0)) return TYP_ARGMAX;
+  if ((double)__fsub_rn(__fdiv_rn(xmin, T), __fdiv_rn(xmax, T)) >= dmin) return TYP_ALL;
+  const float ratio = (float)exp(dmin);
+  if (!(ratio > 0.0f)) return TYP_LOW;
+  if (cut_bins(ratio, xmax, c, R, lo, hi)) return TYP_CUT;
+  return (uint32_t)hi == BELOW ? TYP_LOW : TYP_WIDE;
+}
+// Typical-p on a full row in the general kernel's terms (no id removed, no
+// -inf): lnZ = ln sum exp(z - zmax), H = lnZ - sum e (z - zmax) / Z, tau =
+// fl(exp(H)) typical_p, and z is kept iff z - zmax >= dmin = lnZ - tau.  From
+// the row mass Z and AH = sum e log2 e, both against 2^R (e = exp2(fma(x, c,
+// -R))): sum exp(z - zmax) is Z over the maximum's mass exp2(fma(xmax, c, -R)),
+// and H is invariant to the reference.
+__device__ __forceinline__ double typical_dmin(double Z, double AH, float R, float xmax, float c, float typp) {
+  const double lZ = log(Z);
+  const double lnZ = lZ - 0.6931471805599453 * (double)__builtin_fmaf(xmax, c, -R);
+  const double H = lZ - 0.6931471805599453 * AH / Z;
+  const float tau = __fmul_rn((float)exp(H), typp);
+  return lnZ - (double)tau;
 }
 
 // ---------------------------------------------------------------------------

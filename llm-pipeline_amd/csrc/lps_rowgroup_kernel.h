@@ -18,7 +18,7 @@ __device__ __forceinline__ bool wait_count(uint32_t* p, uint32_t n) {
 // ===========================================================================
 template <int DT, int VPE, int NE, bool XF>
 __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, const int r, const int j,
-                                           const RowCfg& g, const uint32_t epoch) {
+                                           const RowCfg& g, const uint32_t epoch, int& tcase) {
   using CK = Chk<DT, VPE, NE>;
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -227,7 +227,10 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       sm.zsum = zs;
       sm.nanbin = nanc;
     }
-    if (XF && P.entropy) {
+    // typical-p without top-p / min-p: the typical filter proper (a threshold
+    // cut from the row's entropy), unless the row holds -inf
+    const bool tpl = XF && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    if (XF && (P.entropy || tpl)) {
       // the chunk's sum of e * log2(e), fp32 per vector, fp64 across
       double zh = 0.0;
       if (Mfin) {
@@ -257,6 +260,19 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       }
       sm.amax = bred(best, S.i1, OpMin{});
     }
+    if (__builtin_expect(tpl, 0)) {
+      // (over the chunk's nv vectors: its slots past them hold -inf too)
+      uint32_t ni = 0;
+      float mn = INFINITY;
+#pragma unroll
+      for (int s = 0; s < NE; s++) {
+        const bool inr = tid + (s / VPE) * NT < nv;
+        ni += inr && C.x[s] == -INFINITY ? 1u : 0u;
+        mn = inr ? fminf(mn, C.x[s]) : mn;
+      }
+      const uint32_t nis = bred(ni, S.u2, OpAdd{});
+      sm.ab1 = tw_pack(nis, f2key(bred(mn, S.f, OpMin{})));
+    }
     // ---- publish the summary and the bins, one barrier among the row's chunks ----
     if (tid == 0) store_sum(sums + j, sm);
     RG_STAMP(4);
@@ -282,11 +298,20 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       const double sc = af ? ldexp(1.0, (int)(a.ref - R)) : 0.0;
       const double Z = wsum(af ? a.zsum * sc : 0.0);
       const uint32_t mk = XF ? wmax(lane < G ? a.mkey : 0u) : 0u;
+      // (typical rows: sum e log2 e against R, summed as the finaliser does; -inf count)
+      const double ah = tpl ? wsum(af ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0) : 0.0;
+      const uint32_t ni = tpl ? wsum(lane < G ? tw_n(a.ab1) : 0u) : 0u;
+      const uint32_t mn = tpl ? wmin(lane < G ? tw_key(a.ab1) : 0xFFFFFFFFu) : 0u;
       if (lane < G) { S.rf[lane] = af ? a.ref : -INFINITY; }
       if (lane == 0) {
         S.md[0] = Z;
         S.mf[0] = R;
-        if constexpr (XF) S.mi[8] = (int)mk;
+        if constexpr (XF) {
+          S.mi[8] = (int)mk;
+          S.md[1] = ah;
+          S.mi[9] = (int)ni;
+          S.mi[4] = (int)mn;
+        }
       }
     }
     __syncthreads();
@@ -345,16 +370,46 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const double sx = bscan<NW, double>(msum, &stot, S.d2);
     // ---- regions: bins whose cumulative interval meets the targets ----
     const double eps = 1e-6 * Z;
-    const bool nuc = mode == MODE_NUCLEUS;
+    // threshold cuts (min-p; typical-p on a full row): the bins that can hold
+    // the boundary [lom, him], and up to the lowest non-empty bin above them
+    // (which holds the least kept id when every id of [lom, him] is dropped):
+    // hm.  A typical row holding -inf, or whose cut keeps nothing, keeps only
+    // the argmax (targ: no regions, no candidates); one whose cut keeps its
+    // least logit keeps every logit, a pure row (tall)
+    bool tc = XF && mode == MODE_NUCLEUS && g.minp > 0.0f && rfin;
+    bool targ = false, tall = false;
+    int lom = 0, him = -1, hm = -1;
+    double lowtw = 0.0;  // (a typical cut under the histogram: the chunk's dropped logits, least kept key)
+    if (XF && __builtin_expect(tpl && rfin, 0)) {
+      const float xmx = key2f((uint32_t)S.mi[8]);
+      const double dmin = typical_dmin(Z, S.md[1], R, xmx, c, g.typp);
+      tcase = typical_case((uint32_t)S.mi[9], dmin, key2f((uint32_t)S.mi[4]), xmx, T, c, R, lom, him);
+      targ = tcase == TYP_ARGMAX;
+      tall = tcase == TYP_ALL || tcase == TYP_LOW;
+      tc = tcase == TYP_CUT;
+      if (tcase == TYP_WIDE) flags |= RF_REGION;
+      if (tcase == TYP_LOW) {
+        // the least logit the cut keeps (first_key_where: z - zmax >= dmin is
+        // non-decreasing in x), then this chunk's dropped logits and least kept one
+        const float zmx = __fdiv_rn(xmx, T);
+        const float xt = key2f(first_key_where([&](float x) { return (double)__fsub_rn(__fdiv_rn(x, T), zmx) >= dmin; }));
+        uint32_t nd = 0;
+        float mk = INFINITY;
+#pragma unroll
+        for (int s = 0; s < NE; s++) {
+          const bool inr = tid + (s / VPE) * NT < nv;
+          nd += inr && C.x[s] < xt ? 1u : 0u;
+          mk = inr && C.x[s] >= xt ? fminf(mk, C.x[s]) : mk;
+        }
+        const uint32_t nds = bred(nd, S.u2, OpAdd{});
+        lowtw = tw_pack(nds, f2key(bred(mk, S.f, OpMin{})));
+      }
+    }
+    const bool nuc = mode == MODE_NUCLEUS && !tall;
     const bool topp_on = nuc && (!XF || g.topp < 1.0f);  // (without XF every nucleus row has top-p)
     const double Pm = topp_on ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
-    // min-p rows: the bins that can hold the boundary [lom, him], and up to the
-    // lowest non-empty bin above them (which holds the least kept id when every
-    // id of [lom, him] is dropped): hm
-    const bool mp = XF && nuc && g.minp > 0.0f && rfin;
-    int lom = 0, him = -1, hm = -1;
-    if (__builtin_expect(mp, 0)) {
-      if (!minp_bins(g.minp, key2f((uint32_t)S.mi[8]), c, R, lom, him)) flags |= RF_REGION;
+    if (__builtin_expect(tc, 0)) {
+      if (!tpl && !cut_bins(g.minp, key2f((uint32_t)S.mi[8]), c, R, lom, him)) flags |= RF_REGION;
       int bp = 1 << 30;
 #pragma unroll
       for (int i = 0; i < HPT; i++) {
@@ -380,9 +435,9 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
           atop = min(atop, __builtin_bit_cast(uint64_t, a));
           abot = max(abot, __builtin_bit_cast(uint64_t, a + mrg[i]));
         }
-        // (min-p rows: the cumulative mass at the top of bin hm and the bottom of bin lom)
-        if (mp && b == hm) S.mq[5] = __builtin_bit_cast(uint64_t, a);
-        if (mp && b == lom) S.mq[6] = __builtin_bit_cast(uint64_t, a + mrg[i]);
+        // (threshold cuts: the cumulative mass at the top of bin hm and the bottom of bin lom)
+        if (tc && b == hm) S.mq[5] = __builtin_bit_cast(uint64_t, a);
+        if (tc && b == lom) S.mq[6] = __builtin_bit_cast(uint64_t, a + mrg[i]);
         a += mrg[i];
       }
       if (hi >= 0) {
@@ -397,10 +452,10 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     int hi1 = nuc ? S.mi[1] : (1 << 30);
     uint64_t q1t = S.mq[0], q1b = S.mq[1];
     if (topp_on && hi1 < 0) flags |= RF_REGION;
-    if (__builtin_expect(mp, 0)) {
+    if (__builtin_expect(tc, 0)) {
       // the top-p cut entirely above [lom, hm]: top-p alone decides (every id
-      // it keeps passes min-p); entirely under it (or no top-p): min-p alone;
-      // else region 1 covers both
+      // it keeps passes min-p); entirely under it (or no top-p): the threshold
+      // alone; else region 1 covers both
       const double mt = __builtin_bit_cast(double, S.mq[5]), mb = __builtin_bit_cast(double, S.mq[6]);
       if (!topp_on || mb < Pm - eps) {
         lo1 = lom; hi1 = hm; q1t = S.mq[5]; q1b = S.mq[6];
@@ -409,9 +464,11 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
         q1t = min(q1t, S.mq[5]); q1b = max(q1b, S.mq[6]);
       }
     }
+    if (XF && targ) lo1 = hi1 = 1 << 30;
     const float u = fminf(fmaxf(g.u == g.u ? g.u : 0.0f, 0.0f), 0.99999994f);
-    const double t_lo = (nuc ? (double)u * __builtin_bit_cast(double, q1t) : (double)u * Z) - eps;
-    const double t_hi = (nuc ? (double)u * __builtin_bit_cast(double, q1b) : (double)u * Z) + eps;
+    double t_lo = (nuc ? (double)u * __builtin_bit_cast(double, q1t) : (double)u * Z) - eps;
+    double t_hi = (nuc ? (double)u * __builtin_bit_cast(double, q1b) : (double)u * Z) + eps;
+    if (XF && targ) { t_lo = -1.0; t_hi = -2.0; }  // (no draw region)
     {
       int lo = 1 << 30, hi = -1;
       uint32_t nest = 0;  // elements in either region (an upper estimate: bin mass / the bin's least mass)
@@ -442,7 +499,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const int lo2 = S.mi[2];
     const int hi2 = S.mi[3];
     const uint32_t nest = S.u3[0];
-    if (hi2 < 0 || !rfin) flags |= RF_REGION;
+    if (!(XF && targ) && (hi2 < 0 || !rfin)) flags |= RF_REGION;
     const bool need2 = !row_skips_draw(P, r);
     // ---- crowded regions take the second level (a row-uniform decision: every
     // chunk merged the same bins; a chunk whose first barrier timed out is
@@ -450,7 +507,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     // (past 3/4 of the row's lists, so that no chunk's share passes its own
     // list, or half of what the chunks' wave segments take)
     const bool crowded = __builtin_expect(nest > (uint32_t)min(CAPR * 3 / 4, G * CLMAX / 2), 0);
-    const bool refine = crowded && !mp && !S.mi[6] && rfin && (!nuc || (hi1 >= 0 && hi1 - lo1 < RW)) &&
+    const bool refine = crowded && !tc && !S.mi[6] && rfin && (!nuc || (hi1 >= 0 && hi1 - lo1 < RW)) &&
                         (!need2 || (hi2 >= 0 && hi2 - lo2 < RW));
     if (crowded && !refine) flags |= RF_WIDE;
     if (S.mi[6] && tid == 0) add_agent(ctr + CTR_FINE, 1u);
@@ -701,6 +758,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     sm.ab1 = 0.0; sm.ab2 = 0.0; sm.nab1 = 0;
 #pragma unroll
     for (int i = 0; i < NW; i++) { sm.ab1 += S.d4[i]; sm.ab2 += S.d5[i]; sm.nab1 += S.u4[i]; }
+    if (XF && tcase == TYP_LOW) sm.ab1 = lowtw;  // (no region 1)
   }
 
   // ---- the chunk's summary, then the arrival count ----
@@ -1073,7 +1131,7 @@ __device__ __forceinline__ int topk_decide(const RowCfg& g, int V, const uint64_
 
 template <int DT, int VPE, bool XF>
 __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const int r, const RowCfg& g,
-                                           const uint32_t epoch) {
+                                           const uint32_t epoch, const int tcase) {
   const KParams& P = F.k;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = F.G;
@@ -1146,7 +1204,13 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     const double A2 = rreduce16(rfin ? a.ab2 * sc : 0.0, OpAdd{});
     // entropy rows: sum of e ln e over the row, against the row reference
     // (a chunk dl octaves under it: e 2^-dl, log2 e - dl), in log2 units
-    const double AH = (XF && P.entropy) ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
+    // (and typical rows without top-p / min-p, with their -inf count)
+    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    const double AH = (XF && (P.entropy || tpl)) ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
+    // (a typical cut under the histogram: the dropped logits and the least kept key)
+    const bool low = tcase == TYP_LOW;
+    const uint32_t ndr = low ? rreduce16(in ? tw_n(a.ab1) : 0u, OpAdd{}) : 0u;
+    const uint32_t mkp = low ? rreduce16(in ? tw_key(a.ab1) : 0xFFFFFFFFu, OpMin{}) : 0u;
     if (lane < G) {
       S.cn[0][lane] = (int)a.n1;
       S.cn[1][lane] = (int)a.n2;
@@ -1168,6 +1232,8 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       S.mi[21] = a.reg[0]; S.mi[22] = a.reg[1]; S.mi[23] = a.reg[2]; S.mi[24] = a.reg[3];
       S.mi[25] = nmax;
       S.md[0] = Z; S.md[1] = A1; S.md[2] = A2; S.md[3] = AH;
+      S.mi[29] = (int)ndr;
+      S.mi[31] = (int)mkp;
       S.mf[0] = R;
     }
   }
@@ -1287,10 +1353,21 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     chosen_z = xmax;
   } else if (status == 0 && hmode) {
     // ======================= nucleus / pure =======================
-    const bool nuc = mode == MODE_NUCLEUS;
+    const double Z = S.md[0];
+    // typical-p without top-p / min-p (sampling.py:207-238): the threshold
+    // z - zmax >= dmin from the row's entropy; a row holding -inf (NaN
+    // entropy) or whose threshold keeps nothing keeps only the argmax (targ),
+    // one whose threshold keeps its least logit keeps every logit (tall: a
+    // pure row); the chunks decided the same
+    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    // (the case every chunk decided from the same summaries: this workgroup's own)
+    const double dmin = tpl ? typical_dmin(Z, S.md[3], Rref, xmax, c, g.typp) : 0.0;
+    if (tpl && (tcase < TYP_ARGMAX || tcase > TYP_LOW)) return 6;
+    bool targ = tcase == TYP_ARGMAX;  // typical-p row keeping only its argmax
+    const bool tall = tcase == TYP_ALL || tcase == TYP_LOW;
+    const bool nuc = mode == MODE_NUCLEUS && !tall;
     const bool want2 = !row_skips_draw(P, r);
     const int lo1 = S.mi[21], hi1 = S.mi[22], lo2 = S.mi[23], hi2 = S.mi[24];
-    const double Z = S.md[0];
     const uint64_t Zfx = (uint64_t)(Z * kFix);
     if ((nuc && N1 > KM) || (want2 && N2 > KM)) return 7;
     uint32_t vkey = 0, n_tie = kNoTie;
@@ -1318,8 +1395,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     RG_STAMP(28);
     uint64_t ckey = 0;  // the last kept id's sort key
     int qc = -1, pd = -1;
-    bool targ = false;  // typical-p row keeping only its argmax
-    if (nuc) {
+    if (nuc && !targ) {
       // sorted position p of the row is kept iff its exclusive prefix <= limit
       const uint64_t A1 = (uint64_t)(S.md[1] * kFix);
       const double pl = g.topp > 0.0f ? (double)g.topp * (double)Zfx : 0.0;
@@ -1328,16 +1404,19 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       // the first dropped position
       const bool tp = !XF || g.topp < 1.0f;
       int lo = tp ? wave_first_true(0, N1, [&](int p) { return A1 + (p > 0 ? S.sc[0][p - 1] : 0ull) > limit; }) : N1;
-      bool mcut = false;  // region 1 holds the whole min-p boundary range
-      if (XF && __builtin_expect(g.minp > 0.0f, 0)) {
+      bool mcut = false;  // region 1 holds the whole boundary range of a threshold cut
+      if (XF && __builtin_expect(g.minp > 0.0f || tpl, 0)) {
         // min-p after top-p (sampling.py:187-205): keep z with mass_f(z, zmax)
-        // >= min_p, a prefix of the sorted order (exp2 is non-decreasing)
+        // >= min_p; typical-p: keep z - zmax >= dmin.  Each a prefix of the
+        // sorted order (exp2 is non-decreasing)
         const float zmax = __fdiv_rn(xmax, T);
         const int lm = wave_first_true(0, N1, [&](int p) {
-          return !(mass_f(key2f(key_z(S.sk[0][p])), zmax) >= g.minp);
+          const float z = key2f(key_z(S.sk[0][p]));
+          return tpl ? !((double)__fsub_rn(z, zmax) >= dmin) : !(mass_f(z, zmax) >= g.minp);
         });
         int bl, bh;
-        mcut = minp_bins(g.minp, xmax, c, Rref, bl, bh) && lo1 <= bl * FSUB && hi1 >= bh * FSUB + FSUB - 1;
+        mcut = cut_bins(tpl ? (float)exp(dmin) : g.minp, xmax, c, Rref, bl, bh) && lo1 <= bl * FSUB &&
+               hi1 >= bh * FSUB + FSUB - 1;
         lo = min(lo, lm);
       }
       // the cut must fall inside the list: something kept, and the id after
@@ -1359,12 +1438,20 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       kept_n = (int32_t)((uint32_t)S.mi[19] + (uint32_t)lo);
       ties = n_tie == kNoTie ? -1 : (int32_t)n_tie;
       cut = key2f(vkey);
-      if (XF && __builtin_expect(g.typp < 1.0f, 0)) {
+      if (XF && __builtin_expect(g.typp < 1.0f && !tpl, 0)) {
         // typical-p after top-p / min-p (sampling.py:207-238): a row that lost
         // ids holds -inf, its entropy is NaN and only the argmax is kept; a
         // row that kept every id takes the typical filter proper
         if (kept_n >= V) return 14;
         targ = true;
+      }
+    } else if (XF && tall) {
+      // every logit kept but those a cut under the histogram drops (the row holds no -inf)
+      kept_n = V - (tcase == TYP_LOW ? S.mi[29] : 0);
+      if (tcase == TYP_LOW) {
+        const float zc = __fdiv_rn(key2f((uint32_t)S.mi[31]), T);
+        vkey = f2key(zc);
+        cut = zc;
       }
     } else {
       kept_n = -1;  // filled below when asked
@@ -1378,7 +1465,8 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       if (lo == N2 || target < A2) return 9;
       pd = lo;
     }
-    if (wv == 0 && nuc) {  // the cut's collision group lies inside region 1 in every chunk
+    const bool cutd = nuc && (!XF || qc >= 0);  // (a typical row without a cut keeps its argmax)
+    if (wv == 0 && cutd) {  // the cut's collision group lies inside region 1 in every chunk
       const bool ok = group_inside(__uint_as_float(S.sx[0][qc]), lo1, hi1);
       if (lane == 0) S.mi[12] = ok ? 1 : 0;
     }
@@ -1387,7 +1475,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       if (lane == 0) S.mi[14] = ok ? 1 : 0;
     }
     __syncthreads();
-    if (nuc && !S.mi[12]) return 8;
+    if (cutd && !S.mi[12]) return 8;
     if (XF && __builtin_expect(targ, 0)) {
       // the argmax: the first id at the row's maximum z
       if (gam == 0x7FFFFFFF) return 14;
@@ -1414,7 +1502,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       if (nuc && dkey < ckey) return 12;
     }
     RG_STAMP(29);
-    if (!nuc && P.kept_count) {
+    if (!nuc && !(XF && tall) && P.kept_count) {
       // every finite logit is kept: count the -inf ones (a pass over the row)
       uint32_t ninf = 0;
       const int nvec = F.nvec;
@@ -1433,7 +1521,8 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       const float xq = penal_logit<DT>(P, g, row, r, (int)qtok, S);
       const float zq = __fdiv_rn(xq, T);
       const uint32_t kq = f2key(zq);
-      const bool kept = zq != -INFINITY && (!nuc || kq > vkey || (kq == vkey && (n_tie == kNoTie || qtok <= tie_lim)));
+      const bool kept = zq != -INFINITY && ((!nuc && tcase != TYP_LOW) || kq > vkey ||
+                                            (kq == vkey && (n_tie == kNoTie || qtok <= tie_lim)));
       if (kept) qprob = (float)((double)zmass_fix(zq, Rref) / (double)Zkept);
     }
   }
@@ -1513,7 +1602,8 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   // launches (stream-ordered before this one), read by every chunk of the row
   // before any of them arrives
   const uint32_t epoch = ld_agent(F.counters + (int64_t)r * 32 + CTR_EPOCH);
-  const int mode = chunk_phase<DT, VPE, NE, XF>(F, SU.c, r, j, g, epoch);
+  int tcase = -1;  // typical-p rows without other filters: TYP_*
+  const int mode = chunk_phase<DT, VPE, NE, XF>(F, SU.c, r, j, g, epoch, tcase);
   if (mode == MODE_DEFER) {
     if (j == 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (1 << 8);
     return;
@@ -1531,7 +1621,7 @@ __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   if (!SU.c.mi[7] || threadIdx.x >= FT) return;
   acquire_agent();
   RG_STAMP(24);
-  const int reason = final_phase<DT, VPE, XF>(F, SU.f, r, g, epoch);
+  const int reason = final_phase<DT, VPE, XF>(F, SU.f, r, g, epoch, tcase);
   RG_STAMP(31);
   if (reason > 0 && threadIdx.x == 0) F.status[r] = LPS_ROW_DEFERRED | (reason << 8);
 }

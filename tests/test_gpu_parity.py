@@ -321,6 +321,26 @@ def test_min_p_on_the_row_group_kernel(dev, dtype):
     print(f"min-p rows {dtype}: {rep}", flush=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_typical_p_full_rows_on_the_row_group_kernel(dev, dtype):
+    """Typical-p without top-k / top-p / min-p (sampling.py:207-238) at c2's
+    shape (four chunks per row, c2's penalties): the cut z - zmax >= lnZ -
+    exp(H) typical_p from the row's entropy over the chunks, rows whose cut
+    keeps every logit (run as pure rows), rows whose cut keeps nothing and rows
+    holding -inf (the argmax).  At most 2 of the 64 rows are deferred; kept sets
+    and draws equal the oracle's."""
+    from tests.test_gpu_stream import _deferral_reasons
+    w = W.c2_typical(dtype)
+    B = w.B
+    out = PY.run_workload(w, dev)
+    off = (out.row_path.cpu() != 0).nonzero().flatten().tolist()
+    print(f"typical rows {dtype}: off the row-group kernel {off}, reasons {_deferral_reasons(out, dev, B)}",
+          flush=True)
+    assert len(off) <= 2
+    rep = PY.check_rows(w, out)
+    print(f"typical rows {dtype}: {rep}", flush=True)
+
+
 def test_mirostat_long_low_entropy_loop(dev):
     """A peaked row (entropy below tau) makes prev grow every step, so
     k = int(exp(prev)) passes the vocabulary size; the reference's top-k

@@ -275,3 +275,71 @@ def test_min_p_rows(run_case, tmp_path, dtype, V):
     print("rows off the row-group kernel:", off, out.reasons)
     assert len(off) <= 4, (off, out.reasons)
     PY.check_rows(w, out)
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960)])
+def test_typical_p_full_rows(run_case, tmp_path, dtype, V):
+    """Typical-p without top-k / top-p / min-p (sampling.py:207-238) on
+    one-chunk rows of the row-group kernel: the cut z - zmax >= lnZ - exp(H)
+    typical_p from the row's entropy, located like a min-p boundary when it
+    lies in the histogram, counted by the chunks when it lies under it; rows
+    whose cut keeps every logit run as pure rows; rows holding -inf (NaN
+    entropy) and rows whose cut keeps nothing keep only the argmax.  In
+    bounds, kept sets and draws equal to the oracle's."""
+    B = 16
+    g = torch.Generator().manual_seed(41 + V)
+    i = torch.arange(B)
+    sig = torch.tensor([1.0, 2.5, 4.0, 0.5])[i % 4]
+    x = torch.randn((B, V), generator=g) * sig.view(-1, 1)
+    x[3, 100] = float("-inf")
+    x[7, :5] = float("-inf")
+    # rows 12-15: N(0, 3^2) with three spikes at +9, T 0.6: the cut lies under
+    # the histogram (mass ratio < 2^-31) but above the least logits
+    x[12:] = torch.randn((4, V), generator=g) * 3.0
+    x[12:, :3] = 9.0
+    x = x.to(dtype)
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    T = torch.tensor([1.0, 0.7, 1.3, 1.0])[(i // 4) % 4]
+    T[12:] = torch.tensor([0.6, 0.7, 0.7, 0.65])
+    typ = torch.tensor([0.2, 0.5, 0.9, 0.99, 0.7, 0.01, 0.95, 0.3])[i % 8]
+    typ[12:] = torch.tensor([0.9, 0.8, 0.9, 0.85])
+    w = W.Workload("typical", x, T, f(0, torch.int32), f(1.0), f(0.0), typ, f(1.0), f(0.0), f(0.0), None, None,
+                   torch.rand((B,), generator=g))
+    # (the cut under the histogram with dropped logits, inside it, and keeping
+    # everything are present; rows 3 and 7 hold -inf and keep the argmax)
+    kinds = set()
+    for r in range(B):
+        z = x[r].double() / float(T[r])
+        if torch.isinf(z).any():
+            continue
+        d = z - z.max()
+        e = torch.exp(d)
+        lnZ = torch.log(e.sum())
+        H = lnZ - (e * d).sum() / e.sum()
+        dmin = float(lnZ - torch.exp(H) * float(typ[r]))
+        kinds.add("argmax" if dmin > 0 else "all" if float(d.min()) >= dmin else
+                  "low" if dmin < np.log(2.0 ** -31) else "cut")
+    assert {"all", "low", "cut"} <= kinds, kinds
+    out = _run(run_case, w, tmp_path)
+    off = [r for r in range(B) if int(out.row_path[r]) != 0]
+    print("rows off the row-group kernel:", off, out.reasons)
+    assert len(off) <= 2, (off, out.reasons)
+    PY.check_rows(w, out)
+
+
+def test_typical_p_rows_shorter_than_a_chunk(run_case, tmp_path):
+    """Typical-p on full rows of V = 512 with penalties (the inputs of
+    test_min_p_typical's typical_noinf case): the chunk's slots past its
+    vectors hold -inf, which must not count as the row's -inf logits (that
+    would keep only the argmax); kept sets equal the oracle's.  (Rows of
+    several chunks have such slots in every chunk: the GPU test at c2's shape
+    covers them.)"""
+    B, V = 16, 512
+    w = _small(V, B, torch.float32, seed=11)
+    w.temperature = torch.full((B,), 0.8)
+    w.typical_p = torch.linspace(0.2, 0.99, B)
+    w.top_k = torch.zeros(B, dtype=torch.int32)
+    w.top_p = torch.ones(B)
+    out = _run(run_case, w, tmp_path)
+    assert (out.row_path == 0).all(), out.reasons
+    PY.check_rows(w, out)

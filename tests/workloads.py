@@ -106,6 +106,26 @@ def c2_minp(dtype=torch.bfloat16) -> Workload:
     return w
 
 
+def c2_typical(dtype=torch.bfloat16) -> Workload:
+    """c2's rows and penalties with typical-p alone: top_k 0, top_p 1, T cycling
+    0.3 / 0.6 / 1 / 1.5, typical_p cycling 0.2 / 0.5 / 0.9 / 0.99 / 0.7 / 0.01 /
+    0.95 / 0.3 / 0.05; row 5 holds a -inf logit.  The rows' cuts fall inside
+    the histogram, under it, under every logit (all kept) and above the
+    maximum (the argmax)."""
+    w = c2()
+    w.name = "c2_typical"
+    B = w.B
+    i = torch.arange(B)
+    w.top_k = torch.zeros(B, dtype=torch.int32)
+    w.top_p = torch.ones(B)
+    w.temperature = torch.tensor([0.3, 0.6, 1.0, 1.5])[i % 4]
+    w.typical_p = torch.tensor([0.2, 0.5, 0.9, 0.99, 0.7, 0.01, 0.95, 0.3, 0.05])[i % 9]
+    x = w.logits.to(dtype).clone()
+    x[5, 1000] = float("-inf")
+    w.logits = x
+    return w
+
+
 def c3(B=256, V=V_QWEN3, seed=3, flat=False) -> Workload:
     """B=256 fp32 Student-t(3)*2 (or flat N(0, 0.1^2)); top_p 0.95, T 1, no penalties."""
     g = torch.Generator().manual_seed(seed)
