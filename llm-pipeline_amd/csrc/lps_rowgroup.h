@@ -241,6 +241,9 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   RowCfg g;
   g.T = param_or(P.temperature, r, P.temperature_def);
   g.topk = param_or(P.top_k, r, P.top_k_def);
+  // top_k >= V keeps every id (sampling.py:152 clamps k to V; nothing is under
+  // the V-th value): the row samples as one without top-k
+  if (g.topk >= P.V) g.topk = 0;
   g.topp = param_or(P.top_p, r, P.top_p_def);
   g.minp = param_or(P.min_p, r, P.min_p_def);
   g.typp = param_or(P.typical_p, r, P.typical_p_def);
@@ -269,7 +272,6 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   // it is a threshold cut like min-p's)
   else mode = (g.topp < 1.0f || g.minp > 0.0f || g.typp < 1.0f) ? MODE_NUCLEUS : MODE_PURE;
   if (P.entropy && mode != MODE_NUCLEUS && mode != MODE_PURE) mode = MODE_DEFER;
-  if (mode == MODE_TOPK && g.typp < 1.0f && g.topk >= P.V) mode = MODE_DEFER;
   g.kprime = mode == MODE_TOPK ? (g.topk > g.ntop ? g.topk : g.ntop) : (mode == MODE_GREEDY ? g.ntop : 0);
   if (g.kprime > FAST_KMAX) mode = MODE_DEFER;
   g.mode = mode;

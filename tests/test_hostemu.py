@@ -136,13 +136,12 @@ def test_v64_mixed_params(run_case, tmp_path, dtype, hint):
 @pytest.mark.parametrize("hint", [0, 16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_v64_deferred_rows(run_case, tmp_path, dtype, hint):
-    """16-bit V = 64 rows the row-group kernel defers in its chunk phase (top_k
-    past 256, typical-p on a row no other filter cut) or finishes itself
-    (min-p without top-k, typical-p after top-p): the deferred rows are sampled
-    by the general kernel launched after it (16-byte vector loads), the others
-    by the row-group kernel.  With hint 16 (LPS_FLAG_ROWS_NO_MINP_TYPICAL, wrong
-    for these rows) the row-group kernel runs without the min-p / typical-p
-    code and defers those rows too: still sampled exactly."""
+    """16-bit V = 64 rows with top_k 300 (past V: every id kept, a row without
+    top-k), min-p without top-k and typical-p after top-p, which the row-group
+    kernel finishes itself.  With hint 16 (LPS_FLAG_ROWS_NO_MINP_TYPICAL,
+    wrong for the min-p / typical-p rows) the row-group kernel runs without
+    the min-p / typical-p code and defers those rows to the general kernel
+    launched after it (16-byte vector loads): still sampled exactly."""
     w = _small(64, 24, dtype, seed=71)
     i = torch.arange(24)
     w.top_k = torch.where(i % 4 == 1, torch.tensor(300, dtype=torch.int32), w.top_k)
@@ -152,10 +151,10 @@ def test_v64_deferred_rows(run_case, tmp_path, dtype, hint):
     w.temperature = torch.where(i % 4 != 0, torch.tensor(0.9), w.temperature)
     out = _run(run_case, w, tmp_path, flags=hint)
     print("paths", out.row_path.tolist(), out.reasons)
-    assert (out.row_path[i % 4 == 1] == 1).all() and (out.row_path[i % 4 == 0] == 0).all()
+    assert (out.row_path[i % 4 <= 1] == 0).all()
     assert (out.row_path[(i % 4 == 3) & (w.top_p >= 1)] == 1).all()
     if hint:
-        assert (out.row_path[i % 4 != 0] == 1).all()
+        assert (out.row_path[i % 4 >= 2] == 1).all()
     PY.check_rows(w, out)
 
 
