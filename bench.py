@@ -736,7 +736,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c2m", "c2t", "c3", "c3f", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c2m", "c2t", "c2k", "c3", "c3f", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
@@ -786,7 +786,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(), "c2m": lambda: W.c2_minp(), "c2t": lambda: W.c2_typical(),
+    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(), "c2m": lambda: W.c2_minp(), "c2t": lambda: W.c2_typical(), "c2k": lambda: W.c2_bigk(),
             "c3": lambda: W.c3(), "c3f": lambda: W.c3(flat=True), "c5": lambda: W.c5()}[args.config]
     w = make()
     lib = _lib.load()
@@ -866,6 +866,8 @@ def main():
                                "{1e-3,0.02,0.05,0.1,0.2,0.3,1}, top_p in {1,0.9,0.5,0.95}, typical_p 0.6 on 1 row in 9",
                         "c2t": "c2 with typical-p: c2's rows and penalties, top_k 0, top_p 1, T in {0.3,0.6,1,1.5}, "
                                "typical_p in {0.01,...,0.99}, one row holding -inf",
+                        "c2k": "c2 with large top-k: c2's rows and penalties, top_k in {257,...,5000}, top_p 1, "
+                               "T>=0.3, typical_p 0.7 on 1 row in 11",
                         "c3": "c3: B=256, V=151936 fp32 Student-t(3)*2, top_p 0.95, T 1",
                         "c3f": "c3 flat: B=256, V=151936 fp32 N(0,0.1^2), top_p 0.95, T 1",
                         "c5": "c5: B=512, V=151936 fp16, half greedy, half T 0.9/k 40/p 0.92, rep 1.05 over "

@@ -88,12 +88,12 @@ enum {
    * lets the launch skip the kernel no row needs. */
   LPS_FLAG_ROWS_TOPK = 4,      /* every row is greedy (temperature <= 0) or has top_k > 0 */
   LPS_FLAG_ROWS_NUCLEUS = 8,   /* no row is greedy or has top_k > 0 */
-  /* No row has min_p > 0 or typical_p < 1: the row-group kernel then runs
-   * without the code for those filters (rows without top-k that have them
-   * take the general kernel when the hint is wrong).  Without the hint that
-   * code is left out only when min_p and typical_p are NULL and their
-   * defaults are off. */
-  LPS_FLAG_ROWS_NO_MINP_TYPICAL = 16
+  /* No row has min_p > 0, typical_p < 1 or top_k > 256: the row-group kernel
+   * then runs without the code for those filters (rows that have them take
+   * the general kernel when the hint is wrong).  Without the hint that code is
+   * left out only when min_p, typical_p and top_k are NULL and their defaults
+   * need none of it. */
+  LPS_FLAG_ROWS_BASIC_FILTERS = 16
 };
 
 /* Residual used by lps_spec_verify on the first rejected position. */

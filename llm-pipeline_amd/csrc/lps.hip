@@ -162,11 +162,12 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   }
   if (run_rg) {
     // the variant with the entropy output, the mass-only path for pure rows
-    // without a draw (top_p >= 1 by default or per row), and min-p /
-    // typical-p rows without top-k (unless no row can have them: per-row
-    // arrays absent and the defaults off, or the caller's hint)
-    const bool mt = !(flags & LPS_FLAG_ROWS_NO_MINP_TYPICAL) &&
-                    (F.k.min_p != nullptr || F.k.min_p_def > 0.0f || F.k.typical_p != nullptr || F.k.typical_p_def < 1.0f);
+    // without a draw (top_p >= 1 by default or per row), min-p / typical-p rows
+    // without top-k and rows with top_k past FAST_KMAX (unless no row can have
+    // them: per-row arrays absent and the defaults off, or the caller's hint)
+    const bool mt = !(flags & LPS_FLAG_ROWS_BASIC_FILTERS) &&
+                    (F.k.min_p != nullptr || F.k.min_p_def > 0.0f || F.k.typical_p != nullptr ||
+                     F.k.typical_p_def < 1.0f || F.k.top_k != nullptr || F.k.top_k_def > rg::FAST_KMAX);
     const bool xf = F.k.entropy || mt ||
                     ((F.k.skip_draw || (F.k.logits2 && F.k.skip_draw2)) && (F.k.top_p != nullptr || !(F.k.top_p_def < 1.0f)));
     if (xf) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);

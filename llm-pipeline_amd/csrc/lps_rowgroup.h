@@ -56,7 +56,9 @@
 // applies the exact test to the sorted candidates), typical-p rows that top-p or
 // min-p cut (only the argmax is kept), and typical-p rows without other filters
 // (the cut from the row's entropy: the argmax, every logit, a threshold cut
-// like min-p's, or a cut under the histogram that the chunks count).
+// like min-p's, or a cut under the histogram that the chunks count), and rows
+// with top_k past the lists and no top-p / min-p (the chunks also publish a
+// count byte per bin; the merged counts locate the k-th largest's bin).
 // A row the kernel cannot finish exactly (e.g. a region wider than RW bins
 // holding more candidates than the lists take, typical-p after a top-p / min-p
 // that removed nothing, entropy with top-k or greedy) is marked LPS_ROW_DEFERRED in the workspace status and
@@ -204,7 +206,8 @@ struct RgParams {
   int32_t* status;     // [R]
   RgSum* sums;         // row r at sums + r * 2 * MAXG
   float* hist;         // row r at hist + r * G * HPUB
-  float* fine;         // second-level bins: row r at fine + r * G * FHN
+  float* fine;         // second-level bins: row r at fine + r * G * FHN (large top-k rows: one
+                       // count byte per published bin instead)
   uint4* cands;        // row r at cands + r * CAPR: chunk j owns [j * capw, (j + 1) * capw): its
                        // sorted list 1, then its sorted list 2, entries {z key, index, x bits, 0}
   int capw;            // list entries per chunk
@@ -218,6 +221,7 @@ struct RowCfg {
   int topk, ntop, mode, kprime, hlen;
   int64_t qtok;
   bool greedy, pen;
+  bool bigk;  // FAST_KMAX < top_k < V, no top-p / min-p: a nucleus row with a count cut
   const int32_t* hrow;
 };
 // Parameters and mode of row r (sampling.py:66-82 filter order; the row-group
@@ -239,6 +243,7 @@ __device__ __forceinline__ T param_or(const T* p, int64_t i, T def) {
 template <bool MT = true>
 __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   RowCfg g;
+  g.bigk = false;
   g.T = param_or(P.temperature, r, P.temperature_def);
   g.topk = param_or(P.top_k, r, P.top_k_def);
   // top_k >= V keeps every id (sampling.py:152 clamps k to V; nothing is under
@@ -263,7 +268,15 @@ __device__ __forceinline__ RowCfg row_cfg(const KParams& P, int r) {
   int mode;
   if (g.greedy) mode = MODE_GREEDY;
   else if (!(g.T >= 1e-4f)) mode = MODE_DEFER;
-  else if (g.topk > 0) mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
+  else if (g.topk > 0) {
+    mode = g.topk <= FAST_KMAX ? MODE_TOPK : MODE_DEFER;
+    // (past the lists: the k-th largest located by counts in the histogram,
+    // when neither top-p nor min-p follows; typical-p then keeps the argmax)
+    if (MT && mode == MODE_DEFER && !(g.topp < 1.0f) && !(g.minp > 0.0f) && g.ntop == 0) {
+      mode = MODE_NUCLEUS;
+      g.bigk = true;
+    }
+  }
   else if (!MT) {
     if (g.minp > 0.0f || g.typp < 1.0f || g.ntop > 0) mode = MODE_DEFER;
     else mode = g.topp < 1.0f ? MODE_NUCLEUS : MODE_PURE;

@@ -216,6 +216,17 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
         zs += m;
         hout[b] = (float)m;
       }
+      if (XF && g.bigk) {
+        // large top-k rows: the bins' counts too, one byte each (255: 255 or
+        // more), in the second level's area, which these rows do not use
+        static_assert(FHN * 4 == HPUB, "one byte per published bin");
+        uint8_t* cout = reinterpret_cast<uint8_t*>(F.fine + ((int64_t)r * G + j) * FHN);
+#pragma unroll
+        for (int i = 0; i < HLT; i++) {
+          const int b = tid + NT * i;
+          cout[b] = (uint8_t)min((uint32_t)(S.a.hist[b] >> 48), 255u);
+        }
+      }
       zs = wreduce(zs + (double)zlow, OpAdd{});
       nanc = wreduce(nanc, OpAdd{});
       if (lane == 0) { S.d[wv] = zs; S.u[wv] = nanc; }
@@ -229,7 +240,7 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     }
     // typical-p without top-p / min-p: the typical filter proper (a threshold
     // cut from the row's entropy), unless the row holds -inf
-    const bool tpl = XF && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    const bool tpl = XF && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f) && !g.bigk;
     if (XF && (P.entropy || tpl)) {
       // the chunk's sum of e * log2(e), fp32 per vector, fp64 across
       double zh = 0.0;
@@ -370,13 +381,60 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const double sx = bscan<NW, double>(msum, &stot, S.d2);
     // ---- regions: bins whose cumulative interval meets the targets ----
     const double eps = 1e-6 * Z;
+    // large top-k rows: the row bin of the k-th largest logit (kb), from the
+    // chunks' byte counts merged like the masses; a count of 255 at or above
+    // it (inexact), or a k past the binned logits, defers the row
+    int kb = -1;
+    if (XF && __builtin_expect(g.bigk, 0)) {
+      if (tid == 0) S.mi[7] = -1;
+      uint32_t cnt[HPT];
+      uint32_t satm = 0u;  // bit i: bin i's count saturated in some chunk
+#pragma unroll
+      for (int i = 0; i < HPT; i++) cnt[i] = 0u;
+      if (rfin) {
+        for (int w = 0; w < G; w++) {
+          const float rw = S.rf[w];
+          if (rw == -INFINITY) continue;
+          const int dw = (int)fminf(R - rw, 4096.0f);
+          const int src = HPUB - HPT - HPT * tid + HOCT * dw;
+          if (src > HPUB - HPT) continue;
+          const uint64_t v = ld_pub(reinterpret_cast<const uint64_t*>(
+              reinterpret_cast<const uint8_t*>(F.fine + ((int64_t)r * G + w) * FHN) + src));
+#pragma unroll
+          for (int i = 0; i < HPT; i++) {
+            // (byte HPT - 1 - i is row bin HB - 1 - HPT tid - i; the chunk's NaN bin is left out)
+            const uint32_t cc = (i == 0 && src == HPUB - HPT) ? 0u : (uint32_t)(v >> (8 * (HPT - 1 - i))) & 0xFFu;
+            cnt[i] += cc;
+            satm |= cc == 255u ? 1u << i : 0u;
+          }
+        }
+      }
+      if (tid == 0) cnt[0] = 0u;  // row bin HB - 1: NaN only
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < HPT; i++) cs += cnt[i];
+      uint32_t ctot;
+      uint32_t ca = bscan<NW, uint32_t>(cs, &ctot, S.u2);
+      const uint32_t kk = (uint32_t)g.topk;
+      int hs = -1;  // this thread's highest saturated bin
+#pragma unroll
+      for (int i = 0; i < HPT; i++) {
+        const int b = HB - 1 - HPT * tid - i;
+        if (ca < kk && ca + cnt[i] >= kk) S.mi[7] = b;
+        if ((satm >> i) & 1u) hs = max(hs, b);
+        ca += cnt[i];
+      }
+      hs = bred(hs, S.i2, OpMax{});
+      kb = S.mi[7];
+      if (kb < 0 || hs >= kb) flags |= RF_REGION;
+    }
     // threshold cuts (min-p; typical-p on a full row): the bins that can hold
     // the boundary [lom, him], and up to the lowest non-empty bin above them
     // (which holds the least kept id when every id of [lom, him] is dropped):
     // hm.  A typical row holding -inf, or whose cut keeps nothing, keeps only
     // the argmax (targ: no regions, no candidates); one whose cut keeps its
     // least logit keeps every logit, a pure row (tall)
-    bool tc = XF && mode == MODE_NUCLEUS && g.minp > 0.0f && rfin;
+    bool tc = XF && mode == MODE_NUCLEUS && (g.minp > 0.0f || g.bigk) && rfin;
     bool targ = false, tall = false;
     int lom = 0, him = -1, hm = -1;
     double lowtw = 0.0;  // (a typical cut under the histogram: the chunk's dropped logits, least kept key)
@@ -408,7 +466,9 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
     const bool nuc = mode == MODE_NUCLEUS && !tall;
     const bool topp_on = nuc && (!XF || g.topp < 1.0f);  // (without XF every nucleus row has top-p)
     const double Pm = topp_on ? (g.topp > 0.0f ? (double)g.topp * Z : 0.0) : Z;
-    if (__builtin_expect(tc, 0)) {
+    if (XF && g.bigk) {
+      lom = him = hm = kb;  // (the k-th largest lies in bin kb)
+    } else if (__builtin_expect(tc, 0)) {
       if (!tpl && !cut_bins(g.minp, key2f((uint32_t)S.mi[8]), c, R, lom, him)) flags |= RF_REGION;
       int bp = 1 << 30;
 #pragma unroll
@@ -1205,7 +1265,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     // entropy rows: sum of e ln e over the row, against the row reference
     // (a chunk dl octaves under it: e 2^-dl, log2 e - dl), in log2 units
     // (and typical rows without top-p / min-p, with their -inf count)
-    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f) && !g.bigk;
     const double AH = (XF && (P.entropy || tpl)) ? rreduce16(rfin ? sc * (a.zent - (double)(R - a.ref) * a.zsum) : 0.0, OpAdd{}) : 0.0;
     // (a typical cut under the histogram: the dropped logits and the least kept key)
     const bool low = tcase == TYP_LOW;
@@ -1359,7 +1419,7 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
     // entropy) or whose threshold keeps nothing keeps only the argmax (targ),
     // one whose threshold keeps its least logit keeps every logit (tall: a
     // pure row); the chunks decided the same
-    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f);
+    const bool tpl = XF && mode == MODE_NUCLEUS && g.typp < 1.0f && !(g.topp < 1.0f) && !(g.minp > 0.0f) && !g.bigk;
     // (the case every chunk decided from the same summaries: this workgroup's own)
     const double dmin = tpl ? typical_dmin(Z, S.md[3], Rref, xmax, c, g.typp) : 0.0;
     if (tpl && (tcase < TYP_ARGMAX || tcase > TYP_LOW)) return 6;
@@ -1405,7 +1465,15 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
       const bool tp = !XF || g.topp < 1.0f;
       int lo = tp ? wave_first_true(0, N1, [&](int p) { return A1 + (p > 0 ? S.sc[0][p - 1] : 0ull) > limit; }) : N1;
       bool mcut = false;  // region 1 holds the whole boundary range of a threshold cut
-      if (XF && __builtin_expect(g.minp > 0.0f || tpl, 0)) {
+      if (XF && __builtin_expect(g.bigk, 0)) {
+        // top-k past the lists (sampling.py:139-156): every z at or above the
+        // k-th largest, which is list 0's entry k - (ids above region 1)
+        const int kk = g.topk - S.mi[19];
+        if (kk < 1 || kk > N1) return 6;
+        const uint32_t zk = key_z(S.sk[0][kk - 1]);
+        lo = wave_first_true(kk, N1, [&](int p) { return key_z(S.sk[0][p]) < zk; });
+        mcut = true;  // (every id under region 1 is under the k-th largest)
+      } else if (XF && __builtin_expect(g.minp > 0.0f || tpl, 0)) {
         // min-p after top-p (sampling.py:187-205): keep z with mass_f(z, zmax)
         // >= min_p; typical-p: keep z - zmax >= dmin.  Each a prefix of the
         // sorted order (exp2 is non-decreasing)
@@ -1586,8 +1654,9 @@ __device__ __forceinline__ int final_phase(const RgParams& F, RgFinalS& S, const
 // The kernel: grid of ceil(R / 8) * 8 * G workgroups of NT threads.
 // ===========================================================================
 // XF: the launch asks for the entropy output, may hold pure rows without a
-// draw (the mass-only path), or may hold min-p / typical-p rows without top-k;
-// the code of all three is absent otherwise (such rows are then deferred).
+// draw (the mass-only path), or may hold min-p / typical-p rows without top-k
+// or rows with top_k past FAST_KMAX; that code is absent otherwise (such rows
+// are then deferred).
 template <int DT, int VPE, int NE, bool XF>
 __global__ __launch_bounds__(NT) void rowgroup_kernel(RgParams F) {
   __shared__ RgShared<NE> SU;

@@ -38,7 +38,7 @@ LPS_FLAG_GENERIC = 1
 LPS_FLAG_APPEND_HISTORY = 2
 LPS_FLAG_ROWS_TOPK = 4
 LPS_FLAG_ROWS_NUCLEUS = 8
-LPS_FLAG_ROWS_NO_MINP_TYPICAL = 16
+LPS_FLAG_ROWS_BASIC_FILTERS = 16
 
 LPS_RESIDUAL_TARGET = 0
 LPS_RESIDUAL_LEVIATHAN = 1

@@ -65,6 +65,9 @@ class SamplingParams:
         )
 
 
+# the row-group kernel's largest top_k / top-N taken from its candidate lists
+FAST_KMAX = 256
+
 _WS_LOCK = threading.Lock()
 _WS = {}
 
@@ -102,22 +105,22 @@ def row_kind_flags(temperature, top_k, min_p=None, typical_p=None) -> int:
     """Row-kind hint flags for ``lps_sample`` from host-side per-row
     parameters (scalars, sequences or CPU tensors): ``LPS_FLAG_ROWS_TOPK`` when
     every row is greedy (temperature <= 0) or has top_k > 0,
-    ``LPS_FLAG_ROWS_NUCLEUS`` when none is; ``LPS_FLAG_ROWS_NO_MINP_TYPICAL``
-    when ``min_p`` and ``typical_p`` are given and no row has min_p > 0 or
-    typical_p < 1.  Nothing is hinted from device tensors, whose values the
-    host does not hold.  The hints only choose which kernels (and which build
-    of the row-group kernel) a launch runs; a row that breaks one is still
-    sampled exactly, by the general kernel."""
+    ``LPS_FLAG_ROWS_NUCLEUS`` when none is; ``LPS_FLAG_ROWS_BASIC_FILTERS``
+    when ``min_p`` and ``typical_p`` are given and no row has min_p > 0,
+    typical_p < 1 or top_k > 256.  Nothing is hinted from device tensors,
+    whose values the host does not hold.  The hints only choose which kernels
+    (and which build of the row-group kernel) a launch runs; a row that breaks
+    one is still sampled exactly, by the general kernel."""
     def host(v):
         if isinstance(v, torch.Tensor):
             return v.reshape(-1) if v.device.type == "cpu" else None
         return torch.as_tensor(v).reshape(-1)
     flags = 0
     if min_p is not None and typical_p is not None:
-        mp, tp = host(min_p), host(typical_p)
-        if mp is not None and tp is not None and not bool((mp.float() > 0).any()) \
-                and not bool((tp.float() < 1).any()):
-            flags |= _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
+        mp, tp, kk = host(min_p), host(typical_p), host(top_k)
+        if mp is not None and tp is not None and kk is not None and not bool((mp.float() > 0).any()) \
+                and not bool((tp.float() < 1).any()) and not bool((kk.long() > FAST_KMAX).any()):
+            flags |= _lib.LPS_FLAG_ROWS_BASIC_FILTERS
     T, k = host(temperature), host(top_k)
     if T is None or k is None:
         return flags
@@ -310,10 +313,10 @@ def sample_rows(logits: torch.Tensor, params: SamplingParams, uniforms: Optional
     a.kept_ties = D.ptr(out.kept_ties)
     a.kept_count = D.ptr(out.kept_count)
     a.row_path = D.ptr(out.row_path)
-    hints = _lib.LPS_FLAG_ROWS_TOPK | _lib.LPS_FLAG_ROWS_NUCLEUS | _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
+    hints = _lib.LPS_FLAG_ROWS_TOPK | _lib.LPS_FLAG_ROWS_NUCLEUS | _lib.LPS_FLAG_ROWS_BASIC_FILTERS
     if row_kind_hint & ~hints:
         raise ValueError("row_kind_hint takes LPS_FLAG_ROWS_TOPK / LPS_FLAG_ROWS_NUCLEUS / "
-                         "LPS_FLAG_ROWS_NO_MINP_TYPICAL only")
+                         "LPS_FLAG_ROWS_BASIC_FILTERS only")
     a.flags = ((0 if path == "auto" else _lib.LPS_FLAG_GENERIC) | (_lib.LPS_FLAG_APPEND_HISTORY if append_history else 0)
                | row_kind_hint)
     if noalloc:

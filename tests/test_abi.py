@@ -186,7 +186,7 @@ def test_row_kind_flags():
     """Row-kind hints from host-side parameters; nothing is hinted from values
     the host does not hold, and no min-p / typical-p hint without both."""
     from lps import _lib, row_kind_flags
-    TOPK, NUC, NMT = _lib.LPS_FLAG_ROWS_TOPK, _lib.LPS_FLAG_ROWS_NUCLEUS, _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL
+    TOPK, NUC, NMT = _lib.LPS_FLAG_ROWS_TOPK, _lib.LPS_FLAG_ROWS_NUCLEUS, _lib.LPS_FLAG_ROWS_BASIC_FILTERS
     assert row_kind_flags([0.0, 1.0], [0, 5]) == TOPK
     assert row_kind_flags(1.0, 0) == NUC
     assert row_kind_flags([0.0, 1.0], [0, 0]) == 0
@@ -195,7 +195,8 @@ def test_row_kind_flags():
     assert row_kind_flags(1.0, 0, [0.0, 0.05], 1.0) == NUC
     assert row_kind_flags(1.0, 0, 0.0, [1.0, 0.9]) == NUC
     assert row_kind_flags(1.0, 0, 0.0) == NUC
-    assert _lib.LPS_FLAG_ROWS_NO_MINP_TYPICAL == 16
+    assert row_kind_flags(1.0, [5, 300], 0.0, 1.0) == TOPK
+    assert _lib.LPS_FLAG_ROWS_BASIC_FILTERS == 16
 
 
 def test_lm_head_argument_errors(lib):

@@ -341,6 +341,30 @@ def test_typical_p_full_rows_on_the_row_group_kernel(dev, dtype):
     print(f"typical rows {dtype}: {rep}", flush=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_top_k_past_the_lists_on_the_row_group_kernel(dev, dtype):
+    """top_k from 257 to V - 1 without top-p (sampling.py:139-156) at c2's
+    shape (four chunks per row, c2's penalties): the k-th largest located by
+    the chunks' merged byte counts, its bin's elements as candidates, every
+    tie of the k-th value kept; typical-p after it keeps the argmax.  Every
+    row with k <= 5000 stays on the row-group kernel; rows whose k-th largest
+    lies in dense bins (k = 20000: counts saturate, candidates overflow) or
+    under the histogram (k = V - 1) are deferred to the general kernel.  Kept
+    sets and draws equal the oracle's."""
+    from tests.test_gpu_stream import _deferral_reasons
+    w = W.c2_bigk(dtype)
+    B = w.B
+    w.top_k[3::7] = 20000
+    w.top_k[4::7] = 151935
+    out = PY.run_workload(w, dev)
+    off = (out.row_path.cpu() != 0).nonzero().flatten().tolist()
+    print(f"large top-k rows {dtype}: off the row-group kernel {off}, reasons {_deferral_reasons(out, dev, B)}",
+          flush=True)
+    assert not set(off) & set((w.top_k <= 5000).nonzero().flatten().tolist())
+    rep = PY.check_rows(w, out)
+    print(f"large top-k rows {dtype}: {rep}", flush=True)
+
+
 def test_mirostat_long_low_entropy_loop(dev):
     """A peaked row (entropy below tau) makes prev grow every step, so
     k = int(exp(prev)) passes the vocabulary size; the reference's top-k

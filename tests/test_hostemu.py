@@ -126,7 +126,7 @@ def test_v64_mixed_params(run_case, tmp_path, dtype, hint):
     """The inputs of test_small_vocab_mixed_params at V = 64 (16-byte vector
     rows, one chunk): the row-group kernel at G = 1, then the general kernel on
     the rows it defers (top_k beyond V, top_p <= 0, T < 1e-4 ...); both builds
-    of the row-group kernel (hint 16, LPS_FLAG_ROWS_NO_MINP_TYPICAL: the one
+    of the row-group kernel (hint 16, LPS_FLAG_ROWS_BASIC_FILTERS: the one
     without the min-p / typical-p code).  In bounds, and equal to the oracle."""
     w = _small(64, 24, dtype, seed=64 + int(dtype == torch.bfloat16) * 7)
     out = _run(run_case, w, tmp_path, flags=hint)
@@ -138,7 +138,7 @@ def test_v64_mixed_params(run_case, tmp_path, dtype, hint):
 def test_v64_deferred_rows(run_case, tmp_path, dtype, hint):
     """16-bit V = 64 rows with top_k 300 (past V: every id kept, a row without
     top-k), min-p without top-k and typical-p after top-p, which the row-group
-    kernel finishes itself.  With hint 16 (LPS_FLAG_ROWS_NO_MINP_TYPICAL,
+    kernel finishes itself.  With hint 16 (LPS_FLAG_ROWS_BASIC_FILTERS,
     wrong for the min-p / typical-p rows) the row-group kernel runs without
     the min-p / typical-p code and defers those rows to the general kernel
     launched after it (16-byte vector loads): still sampled exactly."""
@@ -341,4 +341,31 @@ def test_typical_p_rows_shorter_than_a_chunk(run_case, tmp_path):
     w.top_p = torch.ones(B)
     out = _run(run_case, w, tmp_path)
     assert (out.row_path == 0).all(), out.reasons
+    PY.check_rows(w, out)
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960)])
+def test_top_k_past_the_lists(run_case, tmp_path, dtype, V):
+    """top_k from 257 to V - 1 without top-p / min-p (sampling.py:139-156; the
+    Mirostat draw's shape) on one-chunk rows of the row-group kernel: the
+    chunks' byte counts locate the bin of the k-th largest logit, whose
+    elements are region 1's candidates; every tie of the k-th value is kept;
+    typical-p after it keeps the argmax.  In bounds; rows whose counts
+    saturate near the cut are deferred (at most a quarter here); kept sets
+    and draws equal the oracle's."""
+    B = 16
+    g = torch.Generator().manual_seed(51 + V)
+    i = torch.arange(B)
+    sig = torch.tensor([1.0, 2.5, 4.0, 0.5])[i % 4]
+    x = (torch.randn((B, V), generator=g) * sig.view(-1, 1)).to(dtype)
+    f = lambda v, dt=torch.float32: torch.full((B,), v, dtype=dt)
+    k = torch.tensor([257, 300, 1000, 4000, V - 1, 512, 2048, 777], dtype=torch.int32)[i % 8]
+    T = torch.tensor([1.0, 0.7, 1.3, 1.0])[(i // 4) % 4]
+    typ = torch.where(i == 13, torch.tensor(0.8), torch.tensor(1.0))
+    w = W.Workload("bigk", x, T, k, f(1.0), f(0.0), typ, f(1.0), f(0.0), f(0.0), None, None,
+                   torch.rand((B,), generator=g))
+    out = _run(run_case, w, tmp_path)
+    off = [r for r in range(B) if int(out.row_path[r]) != 0]
+    print("rows off the row-group kernel:", off, out.reasons)
+    assert len(off) <= B // 4, (off, out.reasons)
     PY.check_rows(w, out)

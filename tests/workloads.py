@@ -126,6 +126,23 @@ def c2_typical(dtype=torch.bfloat16) -> Workload:
     return w
 
 
+def c2_bigk(dtype=torch.bfloat16) -> Workload:
+    """c2's rows and penalties with top_k past the fast lists and no top-p
+    (the shape of a Mirostat draw at high k): top_k cycling 300 / 1000 / 5000
+    / 700 / 3000 / 257 / 2048, top_p 1, T clamped to >= 0.3, typical_p 0.7 on
+    every eleventh row (the argmax after top-k)."""
+    w = c2()
+    w.name = "c2_bigk"
+    w.logits = w.logits.to(dtype)
+    B = w.B
+    i = torch.arange(B)
+    w.top_k = torch.tensor([300, 1000, 5000, 700, 3000, 257, 2048], dtype=torch.int32)[i % 7]
+    w.top_p = torch.ones(B)
+    w.temperature = w.temperature.clamp(min=0.3)
+    w.typical_p = torch.where(i % 11 == 5, torch.tensor(0.7), torch.tensor(1.0))
+    return w
+
+
 def c3(B=256, V=V_QWEN3, seed=3, flat=False) -> Workload:
     """B=256 fp32 Student-t(3)*2 (or flat N(0, 0.1^2)); top_p 0.95, T 1, no penalties."""
     g = torch.Generator().manual_seed(seed)
