@@ -123,8 +123,31 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
 
 // Largest t with #{values >= t} >= m over the wave (M values per lane,
 // m >= 1, at least m values present): the m-th largest value of the wave.
+// For m <= 16, by taking the wave's largest remaining value and its copies
+// out until m are counted (at most m rounds); else a 32-step bit search.
 template <int M>
 __device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t (&v)[M], uint32_t m) {
+  if (m <= 16u) {
+    uint32_t w[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) w[i] = v[i];
+    uint32_t need = m, t = 0;
+#pragma unroll 1
+    for (int it = 0; it < 16; it++) {
+      uint32_t lm = w[0];
+#pragma unroll
+      for (int i = 1; i < M; i++) lm = w[i] > lm ? w[i] : lm;
+      t = wreduce(lm, OpMax{});
+      uint32_t n = 0;
+#pragma unroll
+      for (int i = 0; i < M; i++) n += (uint32_t)__builtin_popcountll(wballot(w[i] == t));
+      if (n >= need || t == 0u) break;
+      need -= n;
+#pragma unroll
+      for (int i = 0; i < M; i++) w[i] = w[i] == t ? 0u : w[i];
+    }
+    return t;
+  }
   uint32_t t = 0;
 #pragma unroll 1
   for (int b = 31; b >= 0; b--) {
