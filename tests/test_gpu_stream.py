@@ -92,6 +92,39 @@ def test_large_mixed_batch_any_hint(dev, dtype, hint):
     _print(f"{dtype} hint {hint}: general-kernel rows {int(path.sum())}/{B}")
 
 
+@pytest.mark.parametrize("hint", [0, _lib.LPS_FLAG_ROWS_BASIC_FILTERS])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_batch_every_filter(dev, dtype, hint):
+    """A batch larger than one resident round whose rows use every filter:
+    greedy and top-k rows (the streaming kernel), top-p, min-p without top-k
+    (alone and after top-p), typical-p alone and after top-p, and top_k past
+    the lists (the row-group kernel's extra-features build), in one launch.
+    Without a hint every row finishes on a fast kernel (tie-heavy rows aside);
+    with a wrong LPS_FLAG_ROWS_BASIC_FILTERS hint the min-p / typical-p /
+    large-top-k rows take the general kernel.  Every row matches the oracle."""
+    B, V = 320, 4096
+    w = _big(B, V, dtype, seed=29 + int(dtype == torch.float16))
+    i = torch.arange(B)
+    kind = i % 8
+    T = torch.where(kind == 0, torch.tensor(0.0), torch.tensor(0.8))
+    k = torch.tensor([0, 40, 0, 0, 0, 0, 0, 600], dtype=torch.int32)[kind]
+    p = torch.tensor([1.0, 0.9, 0.9, 1.0, 0.8, 1.0, 0.9, 1.0])[kind]
+    mp = torch.tensor([0.0, 0.0, 0.0, 0.05, 0.1, 0.0, 0.0, 0.0])[kind]
+    tp = torch.tensor([1.0, 1.0, 1.0, 1.0, 1.0, 0.5, 0.7, 1.0])[kind]
+    w.temperature, w.top_k, w.top_p, w.min_p, w.typical_p = T, k, p, mp, tp
+    out = PY.run_workload(w, dev, row_kind_hint=hint)
+    PY.check_rows(w, out)
+    path = out.row_path.cpu()
+    plain = i % 7 != 0      # tie-heavy rows may overflow a wave's segment and defer
+    extra = (kind >= 3)
+    reasons = _deferral_reasons(out, dev, B)
+    _print(f"{dtype} hint {hint}: {len(reasons)} deferred rows, reasons {sorted(set(reasons.values()))}")
+    if hint == 0:
+        assert (path[plain] == 0).all()
+    else:
+        assert (path[extra] == 1).all() and (path[plain & ~extra] == 0).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_large_topk_batch_logprobs(dev, dtype):
     """Greedy and top-k rows only (k up to the streaming kernel's 128, and past
