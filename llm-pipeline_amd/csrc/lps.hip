@@ -68,13 +68,41 @@ struct RgWs {
 // Rows per row-group launch; larger batches are split into launches.
 constexpr int RG_MAX_ROWS = 1024;
 
+// CUs of the current device (cached per device): one resident round of
+// row-group workgroups.
+// (threads that race on a device's first call each store the same value)
+std::atomic<int> g_cus[64];
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int c = g_cus[dev].load(std::memory_order_relaxed);
+  if (!c) {
+    int n = 0;
+    c = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+    g_cus[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
+// Whether a launch needs the row-group kernel's build with the extra features:
+// the entropy output, the mass-only path for pure rows without a draw (top_p
+// >= 1 by default or per row), min-p / typical-p rows without top-k and rows
+// with top_k past FAST_KMAX (unless no row can have them: per-row arrays
+// absent and the defaults off, or the caller's hint).
+bool rg_wants_xf(const KParams& k, int flags) {
+  const bool mt = !(flags & LPS_FLAG_ROWS_BASIC_FILTERS) &&
+                  (k.min_p != nullptr || k.min_p_def > 0.0f || k.typical_p != nullptr || k.typical_p_def < 1.0f ||
+                   k.top_k != nullptr || k.top_k_def > rg::FAST_KMAX);
+  return k.entropy || mt || ((k.skip_draw || (k.logits2 && k.skip_draw2)) && (k.top_p != nullptr || !(k.top_p_def < 1.0f)));
+}
+
 // Launch shape of the row-group kernel for a batch: logits per thread (NE) of
 // the instantiated variants, chunks per row (G <= MAXG), vectors per chunk.
 struct RgPlan {
   int vpe, ne, G, cv, nvec, capw;
   bool ok;
 };
-RgPlan rg_plan(int dtype, bool vec, int R, int V) {
+RgPlan rg_plan(int dtype, bool vec, int R, int V, bool lean = false) {
   RgPlan p{};
   p.vpe = !vec ? 1 : (dtype == LPS_DTYPE_F32 ? 4 : 8);
   p.nvec = V / p.vpe;
@@ -82,6 +110,14 @@ RgPlan rg_plan(int dtype, bool vec, int R, int V) {
   // fp32 rows of small batches: 24 logits per thread, so a row spreads over
   // more workgroups (latency); rows read element by element: 40; otherwise 80
   p.ne = p.vpe == 1 ? 40 : ((p.vpe == 4 && R <= 16 && chunks(24) <= rg::MAXG) ? 24 : 80);
+  // batches of more than one resident round of workgroups (one per CU), in the
+  // build without the extra features: 100 (fp32) or 104 (16-bit) logits per
+  // thread when that takes fewer chunks per row (fewer rounds, each a little
+  // longer; the other build would spill registers at that size)
+  if (lean && p.ne == 80) {
+    const int wide = p.vpe == 4 ? 100 : 104;
+    if (chunks(wide) < chunks(80) && (long)((R + 7) / 8 * 8) * chunks(80) > (long)device_cus()) p.ne = wide;
+  }
   p.G = chunks(p.ne);
   p.ok = p.G >= 1 && p.G <= rg::MAXG && V >= 1;
   p.cv = p.ok ? (p.nvec + p.G - 1) / p.G : 1;
@@ -123,22 +159,6 @@ RgWs rg_layout(void* base, int R, int V) {
   return w;
 }
 
-// CUs of the current device (cached per device): one resident round of
-// row-group workgroups.
-// (threads that race on a device's first call each store the same value)
-std::atomic<int> g_cus[64];
-int device_cus() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int c = g_cus[dev].load(std::memory_order_relaxed);
-  if (!c) {
-    int n = 0;
-    c = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
-    g_cus[dev].store(c, std::memory_order_relaxed);
-  }
-  return c;
-}
-
 template <int DT, int VPE, int NE>
 hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   const unsigned grid = (unsigned)((F.k.R + 7) / 8 * 8 * F.G);
@@ -161,17 +181,14 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
     }
   }
   if (run_rg) {
-    // the variant with the entropy output, the mass-only path for pure rows
-    // without a draw (top_p >= 1 by default or per row), min-p / typical-p rows
-    // without top-k and rows with top_k past FAST_KMAX (unless no row can have
-    // them: per-row arrays absent and the defaults off, or the caller's hint)
-    const bool mt = !(flags & LPS_FLAG_ROWS_BASIC_FILTERS) &&
-                    (F.k.min_p != nullptr || F.k.min_p_def > 0.0f || F.k.typical_p != nullptr ||
-                     F.k.typical_p_def < 1.0f || F.k.top_k != nullptr || F.k.top_k_def > rg::FAST_KMAX);
-    const bool xf = F.k.entropy || mt ||
-                    ((F.k.skip_draw || (F.k.logits2 && F.k.skip_draw2)) && (F.k.top_p != nullptr || !(F.k.top_p_def < 1.0f)));
-    if (xf) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);
-    else hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, false>), dim3(grid), dim3(rg::NT), 0, s, F);
+    // the build with the extra features when the launch may need them (the
+    // plans of more than 80 logits per thread are made only for the other)
+    if (rg_wants_xf(F.k, flags)) {
+      if constexpr (NE <= 80) hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, true>), dim3(grid), dim3(rg::NT), 0, s, F);
+      else return hipErrorInvalidValue;
+    } else {
+      hipLaunchKernelGGL((rg::rowgroup_kernel<DT, VPE, NE, false>), dim3(grid), dim3(rg::NT), 0, s, F);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -188,8 +205,10 @@ hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, int flags, hip
   if (p.vpe == 1) return launch_rg<DT, 1, 40>(F, flags, s);
   if constexpr (DT == LPS_DTYPE_F32) {
     if (p.ne == 24) return launch_rg<DT, 4, 24>(F, flags, s);
+    if (p.ne == 100) return launch_rg<DT, 4, 100>(F, flags, s);
     return launch_rg<DT, 4, 80>(F, flags, s);
   } else {
+    if (p.ne == 104) return launch_rg<DT, 8, 104>(F, flags, s);
     return launch_rg<DT, 8, 80>(F, flags, s);
   }
 }
@@ -245,7 +264,7 @@ hipError_t run_sample(const KParams& P, int dtype, bool vec, void* ws, size_t ws
     }
     return hipSuccess;
   }
-  const RgPlan p = rg_plan(dtype, vec, plan_rows, P.V);
+  const RgPlan p = rg_plan(dtype, vec, plan_rows, P.V, !rg_wants_xf(P, flags));
   if (!p.ok) return dispatch_gen(dtype, vec, P, s);
   const RgWs w = rg_layout(ws, plan_rows, P.V);
   rg::RgParams F{};

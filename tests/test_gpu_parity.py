@@ -34,6 +34,21 @@ def test_c2_mixed_params_bf16_full_size(dev):
     _print(f"c2: {rep}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_c2_rows_past_one_round(dev, dtype):
+    """c2's rows at B=96 (16-bit): more chunk workgroups than one resident
+    round at 80 logits per thread, so the row-group kernel runs 104 per
+    thread (three chunks per row) for the nucleus rows while the top-k rows
+    stream; every row against the oracle."""
+    w = W.c2(B=96)
+    w.logits = w.logits.to(dtype)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out)
+    paths = out.row_path.cpu()
+    _print(f"c2 B=96 {dtype}: {rep}; general-kernel rows {int((paths == 1).sum())}")
+    assert int((paths == 1).sum()) <= 2, paths.tolist()
+
+
 @pytest.mark.parametrize("B", [16, 256])
 @pytest.mark.parametrize("flat", [False, True])
 def test_c3_nucleus_fp32(dev, flat, B):
