@@ -276,10 +276,17 @@ __device__ __forceinline__ int chunk_phase(const RgParams& F, RgChunkS<NE>& S, c
       uint32_t ni = 0;
       float mn = INFINITY;
 #pragma unroll
-      for (int s = 0; s < NE; s++) {
-        const bool inr = tid + (s / VPE) * NT < nv;
-        ni += inr && C.x[s] == -INFINITY ? 1u : 0u;
-        mn = inr ? fminf(mn, C.x[s]) : mn;
+      for (int q = 0; q < NE / VPE; q++) {
+        uint32_t nq = 0;
+        float mq = INFINITY;
+#pragma unroll
+        for (int e = 0; e < VPE; e++) {
+          nq += C.x[q * VPE + e] == -INFINITY ? 1u : 0u;
+          mq = fminf(mq, C.x[q * VPE + e]);
+        }
+        const bool inr = tid + q * NT < nv;  // (vector q of this thread)
+        ni += inr ? nq : 0u;
+        mn = inr ? fminf(mn, mq) : mn;
       }
       const uint32_t nis = bred(ni, S.u2, OpAdd{});
       sm.ab1 = tw_pack(nis, f2key(bred(mn, S.f, OpMin{})));
