@@ -87,8 +87,10 @@ def test_mask_equals_masked_logits(dev, name, path):
 
 
 def test_mask_split_kernels(dev):
-    """128 c2 rows with legality masks: 512 row-group workgroups, more than one
-    resident round on 256 CUs."""
+    """128 c2 rows with legality masks: more than one resident round of
+    row-group workgroups on 256 CUs, so the top-k and greedy rows take the
+    streaming kernel and the nucleus rows the row-group kernel at 104 logits
+    per thread (three chunks per row)."""
     w = W.c2(B=128)
     m = _mask(w.B, w.V, seed=5)
     wm = _masked(w, m)
