@@ -190,7 +190,12 @@ template <int DT, int VPE, bool AM>
 __global__ __launch_bounds__(SNT, 4) void stream_kernel(RgParams F) {
   __shared__ StShared S;
   const KParams& P = F.k;
-  const int r = blockIdx.x;
+  // rows skewed over the XCDs (workgroup b runs on XCD b % 8): group k of 8
+  // workgroups puts row 8k + ((x + k) mod 8) on XCD x, so rows that alternate
+  // in kind (greedy / sampled, or any period dividing 8) spread over every
+  // XCD instead of one kind per XCD; a last partial group keeps b
+  const int wgi = blockIdx.x, wgk = wgi >> 3;
+  const int r = (wgk * 8 + 8 <= P.R) ? wgk * 8 + (((wgi & 7) + wgk) & 7) : wgi;
   if (r >= P.R) return;
   // (the wave index through readfirstlane: the compiler then knows it is
   // wave-uniform, and the chunk loop below is a scalar loop)
