@@ -92,6 +92,22 @@ def test_large_mixed_batch_any_hint(dev, dtype, hint):
     _print(f"{dtype} hint {hint}: general-kernel rows {int(path.sum())}/{B}")
 
 
+@pytest.mark.parametrize("B", [263, 301])
+def test_large_mixed_batch_ragged_group(dev, B):
+    """A mixed batch past one resident round whose size is not a multiple of 8:
+    the streaming kernel places groups of 8 rows skewed over the XCDs and the
+    last, partial group as is; every row against the oracle, every plain row
+    on a fast kernel."""
+    V = 4096
+    w = _big(B, V, torch.bfloat16, seed=B)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out)
+    path = out.row_path.cpu()
+    plain = torch.arange(B) % 7 != 0      # tie-heavy rows may overflow a wave's segment and defer
+    _print(f"B={B}: {rep}; general-kernel rows {int(path.sum())}/{B}")
+    assert (path[plain] == 0).all()
+
+
 @pytest.mark.parametrize("hint", [0, _lib.LPS_FLAG_ROWS_BASIC_FILTERS])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_large_batch_every_filter(dev, dtype, hint):
