@@ -108,6 +108,22 @@ def test_large_mixed_batch_ragged_group(dev, B):
     assert (path[plain] == 0).all()
 
 
+@pytest.mark.parametrize("kinds", ["mixed", "nucleus"])
+def test_batch_past_the_launch_row_limit(dev, kinds):
+    """1100 rows: more than one row-group launch takes (1024 rows), so the
+    batch runs as blocks of rows, each its own launch over the same workspace
+    (row counters and epochs carried from block to block); every row against
+    the oracle, every plain row on a fast kernel."""
+    B, V = 1100, 4096
+    w = _big(B, V, torch.bfloat16, seed=1100 + len(kinds), kinds=kinds)
+    out = PY.run_workload(w, dev)
+    rep = PY.check_rows(w, out)
+    path = out.row_path.cpu()
+    plain = torch.arange(B) % 7 != 0      # tie-heavy rows may overflow a wave's segment and defer
+    _print(f"B={B} {kinds}: {rep}; general-kernel rows {int(path.sum())}/{B}")
+    assert (path[plain] == 0).all()
+
+
 @pytest.mark.parametrize("hint", [0, _lib.LPS_FLAG_ROWS_BASIC_FILTERS])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_large_batch_every_filter(dev, dtype, hint):
