@@ -736,7 +736,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c2", "c2m", "c2t", "c2k", "c3", "c3f", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c1g", "c1h", "c2", "c2m", "c2t", "c2k", "c3", "c3f", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--generic", action="store_true", help="time the general one-workgroup-per-row kernel")
@@ -786,7 +786,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c2": lambda: W.c2(), "c2m": lambda: W.c2_minp(), "c2t": lambda: W.c2_typical(), "c2k": lambda: W.c2_bigk(),
+    make = {"c1": lambda: W.c1(), "c1g": lambda: W.c1(greedy=True), "c1h": lambda: W.c1(dtype=torch.bfloat16), "c2": lambda: W.c2(), "c2m": lambda: W.c2_minp(), "c2t": lambda: W.c2_typical(), "c2k": lambda: W.c2_bigk(),
             "c3": lambda: W.c3(), "c3f": lambda: W.c3(flat=True), "c5": lambda: W.c5()}[args.config]
     w = make()
     lib = _lib.load()
@@ -860,6 +860,8 @@ def main():
 
     cfg = {"workload": {"c1": "c1: B=1, V=151936 fp32, rep 1.1 over 64 ids, T 0.7, top_k 50, top_p 0.9",
                         "c1g": "c1 greedy: B=1, V=151936 fp32, rep 1.1, T=0",
+                        "c1h": "c1 in bf16: B=1, V=151936 bf16 (c1's logits rounded), rep 1.1 over 64 ids, T 0.7, "
+                               "top_k 50, top_p 0.9",
                         "c2": "c2: B=64, V=151936 bf16 N(0,3^2)+3 spikes, T~U[0.3,1.2], top_k in {0,20,50,100}, "
                               "top_p~U[0.8,1], presence 0.5, frequency 0.3 over 512 Zipf(1.1) ids/row",
                         "c2m": "c2 with min-p: c2's rows and penalties, top_k 0, T>=0.3, min_p in "

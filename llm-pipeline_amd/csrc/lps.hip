@@ -107,9 +107,10 @@ RgPlan rg_plan(int dtype, bool vec, int R, int V, bool lean = false) {
   p.vpe = !vec ? 1 : (dtype == LPS_DTYPE_F32 ? 4 : 8);
   p.nvec = V / p.vpe;
   auto chunks = [&](int ne) { return (p.nvec + rg::NT * (ne / p.vpe) - 1) / (rg::NT * (ne / p.vpe)); };
-  // fp32 rows of small batches: 24 logits per thread, so a row spreads over
-  // more workgroups (latency); rows read element by element: 40; otherwise 80
-  p.ne = p.vpe == 1 ? 40 : ((p.vpe == 4 && R <= 16 && chunks(24) <= rg::MAXG) ? 24 : 80);
+  // rows of small batches: 24 logits per thread, so a row spreads over more
+  // workgroups (latency; a 16-bit Qwen3 row: 13 chunks instead of 4); rows
+  // read element by element: 40; otherwise 80
+  p.ne = p.vpe == 1 ? 40 : ((R <= 16 && chunks(24) <= rg::MAXG) ? 24 : 80);
   // batches of more than one resident round of workgroups (one per CU), in the
   // build without the extra features: 100 (fp32) or 104 (16-bit) logits per
   // thread when that takes fewer chunks per row (fewer rounds, each a little
@@ -208,6 +209,7 @@ hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, int flags, hip
     if (p.ne == 100) return launch_rg<DT, 4, 100>(F, flags, s);
     return launch_rg<DT, 4, 80>(F, flags, s);
   } else {
+    if (p.ne == 24) return launch_rg<DT, 8, 24>(F, flags, s);
     if (p.ne == 104) return launch_rg<DT, 8, 104>(F, flags, s);
     return launch_rg<DT, 8, 80>(F, flags, s);
   }

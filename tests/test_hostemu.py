@@ -210,10 +210,11 @@ def test_flat_rows_second_level(run_case, tmp_path):
 
 
 def test_flat_rows_second_level_16bit(run_case, tmp_path):
-    """Flat bf16 rows of one chunk (40960 logits, NE = 80): with 8 mantissa
-    bits the logits tie in large groups; rows the second level resolves finish
-    on the row-group kernel, the others are deferred; all match the oracle."""
-    w = _flat(40960, 4, torch.bfloat16, 0.02, seed=12)
+    """Flat bf16 rows of one chunk (12288 logits: 24 per thread, the plan of
+    batches of at most 16 rows): with 8 mantissa bits the logits tie in large
+    groups; rows the second level resolves finish on the row-group kernel, the
+    others are deferred; all match the oracle."""
+    w = _flat(12288, 4, torch.bfloat16, 0.02, seed=12)
     out = _run(run_case, w, tmp_path)
     PY.check_rows(w, out)
 
@@ -276,7 +277,7 @@ def test_min_p_rows(run_case, tmp_path, dtype, V):
     PY.check_rows(w, out)
 
 
-@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960)])
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 12288)])
 def test_typical_p_full_rows(run_case, tmp_path, dtype, V):
     """Typical-p without top-k / top-p / min-p (sampling.py:207-238) on
     one-chunk rows of the row-group kernel: the cut z - zmax >= lnZ - exp(H)
@@ -344,7 +345,7 @@ def test_typical_p_rows_shorter_than_a_chunk(run_case, tmp_path):
     PY.check_rows(w, out)
 
 
-@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960)])
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 12288)])
 def test_top_k_past_the_lists(run_case, tmp_path, dtype, V):
     """top_k from 257 to V - 1 without top-p / min-p (sampling.py:139-156; the
     Mirostat draw's shape) on one-chunk rows of the row-group kernel: the

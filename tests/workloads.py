@@ -50,11 +50,12 @@ def _full(B, v, dtype=torch.float32):
     return torch.full((B,), v, dtype=dtype)
 
 
-def c1(V=V_QWEN3, seed=1, greedy=False) -> Workload:
-    """B=1 fp32 N(0, 2^2); rep 1.1 over 64 uniform ids; T 0.7, k 50, p 0.9."""
+def c1(V=V_QWEN3, seed=1, greedy=False, dtype=torch.float32) -> Workload:
+    """B=1 fp32 N(0, 2^2) (or rounded to dtype); rep 1.1 over 64 uniform ids;
+    T 0.7, k 50, p 0.9."""
     g = torch.Generator().manual_seed(seed)
     B = 1
-    x = torch.randn((B, V), generator=g) * 2.0
+    x = (torch.randn((B, V), generator=g) * 2.0).to(dtype)
     hist = torch.randint(0, V, (B, 64), generator=g, dtype=torch.int32)
     return Workload("c1", x, _full(B, 0.0 if greedy else 0.7), _full(B, 50, torch.int32), _full(B, 0.9),
                     _full(B, 0.0), _full(B, 1.0), _full(B, 1.1), _full(B, 0.0), _full(B, 0.0), hist,
