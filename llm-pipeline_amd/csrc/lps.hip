@@ -107,10 +107,11 @@ RgPlan rg_plan(int dtype, bool vec, int R, int V, bool lean = false) {
   p.vpe = !vec ? 1 : (dtype == LPS_DTYPE_F32 ? 4 : 8);
   p.nvec = V / p.vpe;
   auto chunks = [&](int ne) { return (p.nvec + rg::NT * (ne / p.vpe) - 1) / (rg::NT * (ne / p.vpe)); };
-  // rows of small batches: 24 logits per thread, so a row spreads over more
-  // workgroups (latency; a 16-bit Qwen3 row: 13 chunks instead of 4); rows
-  // read element by element: 40; otherwise 80
-  p.ne = p.vpe == 1 ? 40 : ((R <= 16 && chunks(24) <= rg::MAXG) ? 24 : 80);
+  // rows of small batches (fp32: up to 16 rows, 16-bit: up to 12): 24
+  // logits per thread, so a row spreads over more workgroups (latency; a
+  // 16-bit Qwen3 row: 13 chunks instead of 4); rows read element by element:
+  // 40; otherwise 80
+  p.ne = p.vpe == 1 ? 40 : ((R <= (p.vpe == 4 ? 16 : 12) && chunks(24) <= rg::MAXG) ? 24 : 80);
   // batches of more than one resident round of workgroups (one per CU), in the
   // build without the extra features: 100 (fp32) or 104 (16-bit) logits per
   // thread when that takes fewer chunks per row (fewer rounds, each a little

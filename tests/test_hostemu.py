@@ -211,7 +211,7 @@ def test_flat_rows_second_level(run_case, tmp_path):
 
 def test_flat_rows_second_level_16bit(run_case, tmp_path):
     """Flat bf16 rows of one chunk (12288 logits: 24 per thread, the plan of
-    batches of at most 16 rows): with 8 mantissa bits the logits tie in large
+    16-bit batches of at most 12 rows): with 8 mantissa bits the logits tie in large
     groups; rows the second level resolves finish on the row-group kernel, the
     others are deferred; all match the oracle."""
     w = _flat(12288, 4, torch.bfloat16, 0.02, seed=12)
