@@ -112,6 +112,9 @@ RgPlan rg_plan(int dtype, bool vec, int R, int V, bool lean = false) {
   // 16-bit Qwen3 row: 13 chunks instead of 4); rows read element by element:
   // 40; otherwise 80
   p.ne = p.vpe == 1 ? 40 : ((R <= (p.vpe == 4 ? 16 : 12) && chunks(24) <= rg::MAXG) ? 24 : 80);
+  // up to 32 rows: 40 per thread while every chunk still fits one resident
+  // round (a Qwen3 row: 8 chunks instead of 4)
+  if (p.ne == 80 && R <= 32 && (long)((R + 7) / 8 * 8) * chunks(40) <= (long)device_cus()) p.ne = 40;
   // batches of more than one resident round of workgroups (one per CU), in the
   // build without the extra features: 100 (fp32) or 104 (16-bit) logits per
   // thread when that takes fewer chunks per row (fewer rounds, each a little
@@ -207,10 +210,12 @@ hipError_t dispatch_rg_dt(const rg::RgParams& F, const RgPlan& p, int flags, hip
   if (p.vpe == 1) return launch_rg<DT, 1, 40>(F, flags, s);
   if constexpr (DT == LPS_DTYPE_F32) {
     if (p.ne == 24) return launch_rg<DT, 4, 24>(F, flags, s);
+    if (p.ne == 40) return launch_rg<DT, 4, 40>(F, flags, s);
     if (p.ne == 100) return launch_rg<DT, 4, 100>(F, flags, s);
     return launch_rg<DT, 4, 80>(F, flags, s);
   } else {
     if (p.ne == 24) return launch_rg<DT, 8, 24>(F, flags, s);
+    if (p.ne == 40) return launch_rg<DT, 8, 40>(F, flags, s);
     if (p.ne == 104) return launch_rg<DT, 8, 104>(F, flags, s);
     return launch_rg<DT, 8, 80>(F, flags, s);
   }

@@ -219,6 +219,16 @@ def test_flat_rows_second_level_16bit(run_case, tmp_path):
     PY.check_rows(w, out)
 
 
+def test_sixteen_bit_rows_past_32(run_case, tmp_path):
+    """33 bf16 rows of 40960 logits: past 32 rows the plan holds 80 logits per
+    thread, one chunk per row here; c2's mixed parameters and penalties, in
+    bounds and equal to the oracle."""
+    w = W.c2(B=33, V=40960, H=64)
+    out = _run(run_case, w, tmp_path)
+    assert (out.row_path == 0).all(), out.reasons
+    PY.check_rows(w, out)
+
+
 def test_entropy_pure_rows(run_case, tmp_path):
     """The entropy output (the first call of sample_mirostat_v2: pure rows,
     draw skipped) on one-chunk rows of the row-group kernel, and on rows with a
@@ -262,7 +272,7 @@ def _minp_rows(V, dtype, seed):
                       torch.rand((B,), generator=g))
 
 
-@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 40960), (torch.float16, 40960)])
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 12288), (torch.bfloat16, 20480), (torch.float16, 20480)])
 def test_min_p_rows(run_case, tmp_path, dtype, V):
     """min-p without top-k on one-chunk rows of the row-group kernel (region 1
     covers the bins that can hold the min-p boundary; the finaliser applies the
