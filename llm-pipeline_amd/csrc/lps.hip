@@ -171,8 +171,14 @@ hipError_t launch_rg(rg::RgParams F, int flags, hipStream_t s) {
   // top-k rows stream through one workgroup each (stream_kernel), the
   // row-group kernel takes the others; the row-kind hints skip a kernel no row
   // needs (a row the hint misjudges is deferred to the general kernel)
+  // (with nucleus rows possible the batch may run both kernels, one after
+  // the other: the streaming kernel then pays only past 8 rounds; c2's mixed
+  // rows at 96 to 640 rows take 54-199 us on the row-group kernel alone,
+  // 113-692 us on both)
   bool big = false;
-  if constexpr (VPE > 1) big = grid > (unsigned)device_cus() && F.k.V <= rg::STREAM_VMAX;
+  const unsigned cus = (unsigned)device_cus();
+  const unsigned lim = (flags & LPS_FLAG_ROWS_TOPK) ? cus : cus * 8u;
+  if constexpr (VPE > 1) big = grid > lim && F.k.V <= rg::STREAM_VMAX;
   const bool run_stream = big && !(flags & LPS_FLAG_ROWS_NUCLEUS);
   const bool run_rg = !(run_stream && (flags & LPS_FLAG_ROWS_TOPK));
   if constexpr (VPE > 1) {

@@ -108,6 +108,20 @@ def test_large_mixed_batch_ragged_group(dev, B):
     assert (path[plain] == 0).all()
 
 
+def test_mixed_batch_on_both_kernels(dev):
+    """c2's mixed rows at B=700 (V=151936 bf16): past 8 resident rounds of
+    row-group workgroups, so the greedy and top-k rows stream and the nucleus
+    rows take the row-group kernel (which skips the streamed rows); every row
+    on a fast kernel, every seventh row against the oracle."""
+    w = W.c2(B=700)
+    out = PY.run_workload(w, dev)
+    rows = list(range(0, w.B, 7))
+    rep = PY.check_rows(w, out, rows=rows)
+    path = out.row_path.cpu()
+    _print(f"c2 B=700: {rep}; general-kernel rows {int(path.sum())}/{w.B}")
+    assert int((path == 1).sum()) <= 3, path.nonzero().flatten().tolist()
+
+
 @pytest.mark.parametrize("kinds", ["mixed", "nucleus"])
 def test_batch_past_the_launch_row_limit(dev, kinds):
     """1100 rows: more than one row-group launch takes (1024 rows), so the
